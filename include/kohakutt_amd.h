@@ -1,0 +1,154 @@
+/*
+ * kohakutt_amd -- C ABI of the MI355X (gfx950) attention + norm hot path.
+ *
+ * Plain C: device pointers, int64 sizes and element strides, dtype codes and an opaque
+ * stream (a hipStream_t passed as void*).  No torch or HIP types cross this boundary.
+ *
+ * Conventions (the reference's C ABI, src/kohakutt_native/csrc/py_bridge/ktt_capi.h:1-3,
+ * 96-124, and capi.cpp:19,58-79, returns NULL / -1 and keeps the message in a
+ * thread_local string read by ktt_last_error(); this ABI keeps that error model):
+ *   - every entry point returns KMI_OK (0) or a negative kmi_status; the message of the
+ *     last failure on the calling thread is kmi_last_error();
+ *   - arguments are validated on the host before anything is enqueued: a rejected call
+ *     launches nothing;
+ *   - work is enqueued on `stream` and never synchronised; nothing is allocated, except
+ *     that kmi_attn_fwd uses the caller's workspace (kmi_attn_workspace_bytes) for
+ *     split-KV partials;
+ *   - calls are thread-safe (no mutable global state besides the thread_local error).
+ */
+#ifndef KOHAKUTT_AMD_H
+#define KOHAKUTT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KMI_ABI_VERSION 1
+
+/* Element types of operands. */
+enum kmi_dtype {
+    KMI_BF16 = 1,
+    KMI_F16 = 2,
+    KMI_F32 = 3,
+    KMI_BOOL = 4 /* one byte, nonzero = keep */
+};
+
+enum kmi_status {
+    KMI_OK = 0,
+    KMI_EINVAL = -1,       /* malformed arguments (shapes, strides, pointers) */
+    KMI_EUNSUPPORTED = -2, /* well-formed but outside what the kernels take */
+    KMI_EHIP = -3,         /* a HIP runtime error at launch */
+    KMI_EWORKSPACE = -4    /* workspace missing or too small */
+};
+
+/* How kmi_attn_args.mask is laid out. */
+enum kmi_mask_mode {
+    KMI_MASK_NONE = 0,
+    /* element (b, h, i, j) at mask + b*s[0] + h*s[1] + i*s[2] + j*s[3] (stride 0 =
+     * broadcast).  Varlen calls index it with packed token indices: (h, t_q, t_k) at
+     * mask + h*s[1] + t_q*s[2] + t_k*s[3] (a [Tk] key mask is s = {0, 0, 0, 1}). */
+    KMI_MASK_STRIDED = 1,
+    /* varlen only: sequence i's row-major [Lq_i, Lk_i] block follows sequence i-1's;
+     * element (h, r, c) of sequence i at mask + sum_{j<i} Lq_j*Lk_j + h*s[1] + r*Lk_i + c. */
+    KMI_MASK_PACKED = 2
+};
+
+/*
+ * Attention forward: out = softmax(scale * q k^T + mask) v per (batch, query head),
+ * query head h reading K/V head h / (heads_q / heads_kv).
+ *
+ * Replaces the reference's bridge::sdpa / ktt_sdpa (ktt_capi.h:96-124,
+ * device_attention.cpp:265-497) for the dense route and bridge::sdpa_varlen
+ * (device_attention.cpp:681-761) for packed sequences.
+ *
+ * Dense: q [B, Hq, Sq, D], k/v [B, Hkv, Sk, D], out [B, Hq, Sq, D]; *_stride give the
+ *   element strides of the batch, head and sequence dims (the head-dim stride is 1).
+ * Varlen (cu_seqlens_q != NULL): `batch` sequences; q [Tq, Hq, D], k/v [Tk, Hkv, D]
+ *   indexed by packed token; stride[0] is ignored; cu_seqlens_* are device int32
+ *   [batch + 1] offsets, seq_q / seq_k are the longest sequence lengths (grid bounds).
+ * causal: 0 none; 1 causal.  Dense causal is top-left (query i sees keys <= i, the
+ *   reference's aten_attention.cpp:106-107); varlen causal is bottom-right (query r sees
+ *   the first min(Lk, r + 1 + Lk - Lq) keys, varlen_plan.hpp:70).
+ * Masks: bool keeps nonzero keys; float masks are added to the logits; both are clamped
+ *   at -5e5 (the reference's kMaskedLogit), so a masked key gets exactly zero weight when
+ *   its row keeps any key and a fully-masked row is the softmax over its raw scores.
+ * lse (optional, fp32, natural log): dense [B, Hq, Sq] / varlen [Hq, Tq] with strides
+ *   lse_stride (batch, head, seq); varlen ignores lse_stride[0].
+ * Supported: dtype BF16 or F16, head_dim 64 or 128, heads_kv dividing heads_q.
+ */
+typedef struct kmi_attn_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    float* lse;
+    int32_t dtype;
+    int32_t causal;
+    int64_t batch, heads_q, heads_kv, seq_q, seq_k, head_dim;
+    int64_t q_stride[3];
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[3];
+    int64_t lse_stride[3];
+    double scale;
+    const void* mask;
+    int32_t mask_dtype;
+    int32_t mask_mode;
+    int64_t mask_stride[4];
+    const int32_t* cu_seqlens_q;
+    const int32_t* cu_seqlens_k;
+    /* varlen: packed token counts Tq / Tk.  The kernels clamp every offset into
+     * [0, total] (so malformed device offsets cannot read or write out of bounds; they are
+     * validated where the caller holds them on the host). */
+    int64_t total_q, total_k;
+    /* 0: chosen by the library (split-KV for short query tiles over long key ranges);
+     * 1: no split; n > 1: at most n key splits. */
+    int32_t num_splits;
+    int32_t reserved;
+} kmi_attn_args;
+
+/* Bytes of workspace kmi_attn_fwd needs for `args` (0 when it does not split). */
+int kmi_attn_workspace_bytes(const kmi_attn_args* args, size_t* bytes);
+
+/* Enqueues the attention forward of `args` on `stream` (hipStream_t). */
+int kmi_attn_fwd(const kmi_attn_args* args, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
+ * LayerNorm forward over rows of `width` contiguous elements:
+ *   y = (x - mean) * rstd * weight + bias, rstd = 1 / sqrt(max(var, 0) + eps),
+ * mean / rstd written as fp32 [rows] (either may be NULL).  weight / bias may be NULL;
+ * x / y dtype BF16, F16 or F32; weight / bias BF16, F16 or F32.
+ * Replaces the reference's ktt_layer_norm (ktt_capi.h:96-124; bridge::layer_norm,
+ * device_norm.cpp:235-300; ktt_norm::forward, ktt_norm/program.cpp:436).
+ */
+int kmi_layer_norm_fwd(const void* x, const void* weight, const void* bias, void* y,
+                       float* mean, float* rstd, int64_t rows, int64_t width,
+                       int32_t x_dtype, int32_t w_dtype, int32_t b_dtype, double eps,
+                       void* stream);
+
+/*
+ * RMSNorm forward: y = x * rstd * weight (+ bias), rstd = 1 / sqrt(mean(x^2) + eps),
+ * rstd written as fp32 [rows] (may be NULL).
+ * Replaces the reference's ktt_rms_norm / ktt_rms_norm_train (ktt_capi.h:96-124;
+ * bridge::rms_norm, device_norm.cpp:203-233; ktt::rms_norm with bias,
+ * aten_fused.cpp:60-85).
+ */
+int kmi_rms_norm_fwd(const void* x, const void* weight, const void* bias, void* y,
+                     float* rstd, int64_t rows, int64_t width, int32_t x_dtype,
+                     int32_t w_dtype, int32_t b_dtype, double eps, void* stream);
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* kmi_last_error(void);
+
+/* KMI_ABI_VERSION of the loaded library. */
+int kmi_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KOHAKUTT_AMD_H */

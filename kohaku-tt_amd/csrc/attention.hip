@@ -1,0 +1,605 @@
+// Flash-attention forward for gfx950: dense / GQA / MQA, causal, bool and additive masks,
+// packed variable-length sequences, and split-KV with an fp32 merge pass for short query
+// tiles over long key ranges (decode).
+//
+// Reference semantics (src/kohakutt_native/csrc/aten/attention):
+//   - logits = scale * q.k + max(mask, -5e5) (ktt_flash/program.cpp:912-919 mask_operand;
+//     varlen_plan.hpp:17 kMaskedLogit); bool masks keep nonzero keys and drop the rest to
+//     -5e5 (aten_attention.cpp:223-238).  A masked key therefore has exactly zero weight
+//     when its row keeps a key, and a fully-masked row is the softmax over its raw scores.
+//   - online softmax in base 2 with scale * log2(e) folded into the logits, P rounded to
+//     the operand type for the PV product, O and l in fp32, O / l rounded once
+//     (ktt_flash/compute.cpp:193-500 computes the same recurrence on Tensix tiles).
+//   - dense causal is top-left (aten_attention.cpp:106-107); varlen causal is bottom-right:
+//     query r sees min(Lk, r + 1 + Lk - Lq) keys (varlen_plan.hpp:43-82).
+//
+// MI355X design (not the reference's Tensix reader/compute/writer split):
+//   - a 256-thread workgroup (4 wavefronts) owns BM = 64 * NQB "virtual rows" of one
+//     (sequence, K/V head): row r is query position r / G of query head kvh * G + r % G,
+//     so the G query heads of a GQA group share every K/V tile it stages in LDS;
+//   - S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_{bf16,f16}: with that
+//     orientation the S accumulator of a lane is already the B operand of the PV product
+//     (no cross-lane shuffles), and each lane owns one query row for the softmax state;
+//   - K tiles are stored row-major, V tiles transposed (with the key order the MFMA
+//     operand expects), both padded against LDS bank conflicts, double-buffered through
+//     registers so the next tile's HBM reads overlap this tile's MFMAs;
+//   - causal work skips key tiles past the tile's last query and issues the heaviest
+//     query tiles first; masking is per element only on tiles that need it.
+#include "common.hpp"
+
+#include <algorithm>
+#include <mutex>
+
+namespace kmi {
+namespace {
+
+constexpr int BN = 64;  // keys per LDS tile
+constexpr int NWAVES = 4;
+constexpr int NTHREADS = NWAVES * kWave;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kMaskedLogit = -5e5f;
+
+struct AttnParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    float* lse;
+    float* part_o;    // [splits][rows_total][hq][D] fp32 (normalised partial outputs)
+    float* part_lse;  // [splits][rows_total][hq] fp32, base-2 log-sum-exp
+    int64_t qs[3], ks[3], vs[3], os[3], ls[3];
+    const void* mask;
+    int64_t ms[4];
+    const int32_t* cu_q;
+    const int32_t* cu_k;
+    int mask_dtype, mask_mode;
+    int batch, hq, hkv, group, seq_q, seq_k;
+    int causal;
+    float scale_log2;
+    int splits, tiles_per_split;
+    int nx;  // query tiles per (sequence, K/V head)
+    int total_q, total_k;  // varlen packed token counts
+    int64_t rows_total;
+};
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<bf16> {
+    typedef bf16x8 v8;
+    static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Mfma<f16> {
+    typedef f16x8 v8;
+    static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+// Mask value (logit units, clamped at the masked logit) of element `i`.
+__device__ __forceinline__ float mask_logit(const void* m, int dtype, int64_t i) {
+    float x;
+    switch (dtype) {
+        case KMI_BOOL: return static_cast<const uint8_t*>(m)[i] ? 0.f : kMaskedLogit;
+        case KMI_BF16: x = to_f32(static_cast<const bf16*>(m)[i]); break;
+        case KMI_F16: x = to_f32(static_cast<const f16*>(m)[i]); break;
+        default: x = static_cast<const float*>(m)[i];
+    }
+    return fmaxf(x, kMaskedLogit);  // -inf -> -5e5
+}
+
+// Position of key `kk` (0..BN-1) in a transposed V row: within each 32-key chunk the
+// MFMA B operand of lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3 as slots 8g..8g+7.
+__device__ __forceinline__ int vpos(int kk) {
+    const int c = kk & 31;
+    return (kk & ~31) + 8 * ((c & 15) >> 2) + ((c >> 4) << 2) + (c & 3);
+}
+
+template <typename T, int D, int NQB>
+__global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
+    typedef typename Mfma<T>::v8 v8;
+    constexpr int BM = NWAVES * 16 * NQB;
+    constexpr int KP = D + 8;   // K tile row pitch (elements)
+    constexpr int VP = BN + 8;  // V^T tile row pitch (elements)
+    constexpr int DC = D / 32;  // 32-wide chunks of the head dim
+    constexpr int DB = D / 16;  // 16-wide blocks of the head dim
+    constexpr int KB = BN / 16;
+    constexpr int VPT = BN * D / 8 / NTHREADS;  // 16-byte K vectors per thread per tile
+    constexpr int UPT = VPT / 2;                // (2 keys x 8 dims) V units per thread
+    static_assert(VPT >= 2 && VPT % 2 == 0, "tile shape");
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    T* k_lds = reinterpret_cast<T*>(smem);
+    T* v_lds = k_lds + 2 * BN * KP;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g4 = lane >> 4;
+    const int l16 = lane & 15;
+
+    // Work item: heaviest query tiles first (causal), then (sequence, K/V head), split.
+    int64_t lin = blockIdx.x;
+    const int split = static_cast<int>(lin % p.splits);
+    lin /= p.splits;
+    const int bh = static_cast<int>(lin % (p.batch * p.hkv));
+    int xt = static_cast<int>(lin / (p.batch * p.hkv));
+    if (p.causal) xt = p.nx - 1 - xt;
+    const int seq = bh / p.hkv;
+    const int kvh = bh % p.hkv;
+    const int G = p.group;
+
+    int q0 = 0, lq = p.seq_q, k0 = 0, lk = p.seq_k;
+    int64_t qb_off = seq * p.qs[0], kb_off = seq * p.ks[0], vb_off = seq * p.vs[0];
+    int64_t ob_off = seq * p.os[0], lb_off = seq * p.ls[0];
+    int64_t row_base = static_cast<int64_t>(seq) * p.seq_q;  // partial-row index of query 0
+    if (p.cu_q) {
+        q0 = min(max(p.cu_q[seq], 0), p.total_q);
+        lq = min(max(p.cu_q[seq + 1], q0), p.total_q) - q0;
+        k0 = min(max(p.cu_k[seq], 0), p.total_k);
+        lk = min(max(p.cu_k[seq + 1], k0), p.total_k) - k0;
+        lq = min(lq, p.seq_q);  // the grid covers max_q queries per sequence
+        qb_off = kb_off = vb_off = ob_off = lb_off = 0;
+        row_base = q0;
+    }
+    const int vrows = lq * G;
+    const int r_begin = xt * BM;
+    if (r_begin >= vrows || lk <= 0) return;
+    const int r_end = min(vrows, r_begin + BM);
+    const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys < i + 1 + coff
+    int kend = lk;
+    if (p.causal) kend = max(0, min(lk, (r_end - 1) / G + 1 + coff));
+    const int ntiles = (kend + BN - 1) / BN;
+    int t_begin = 0, t_end = ntiles;
+    if (p.splits > 1) {
+        t_begin = split * p.tiles_per_split;
+        t_end = min(ntiles, t_begin + p.tiles_per_split);
+    }
+    const int first_pos = r_begin / G;  // smallest query position in the tile
+
+    // Mask addressing: per-sequence base.
+    const void* mptr = p.mask;
+    int64_t m_seq = 0;
+    if (p.mask_mode == KMI_MASK_STRIDED) {
+        m_seq = p.cu_q ? (static_cast<int64_t>(q0) * p.ms[2] + static_cast<int64_t>(k0) * p.ms[3])
+                       : seq * p.ms[0];
+    } else if (p.mask_mode == KMI_MASK_PACKED) {
+        for (int s = 0; s < seq; ++s) {
+            const int a0 = min(max(p.cu_q[s], 0), p.total_q), a1 = min(max(p.cu_q[s + 1], a0), p.total_q);
+            const int b0 = min(max(p.cu_k[s], 0), p.total_k), b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
+            m_seq += static_cast<int64_t>(a1 - a0) * (b1 - b0);
+        }
+    }
+    const int64_t m_key = p.mask_mode == KMI_MASK_PACKED ? 1 : p.ms[3];
+
+    // This lane's rows: Q fragments (B operand of S^T = K Q^T) and row metadata.
+    const T* qp = static_cast<const T*>(p.q);
+    const T* kp = static_cast<const T*>(p.k);
+    const T* vp = static_cast<const T*>(p.v);
+    v8 qf[NQB][DC];
+    int pos[NQB], head[NQB];
+    bool valid[NQB];
+    int64_t mrow[NQB];
+    const int wave_row0 = r_begin + wave * 16 * NQB;
+    const bool wave_active = wave_row0 < r_end;
+#pragma unroll
+    for (int b = 0; b < NQB; ++b) {
+        const int r = wave_row0 + 16 * b + l16;
+        valid[b] = r < r_end;
+        const int rr = valid[b] ? r : r_begin;
+        pos[b] = rr / G;
+        head[b] = kvh * G + rr % G;
+        const T* src = qp + qb_off + head[b] * p.qs[1] + static_cast<int64_t>(q0 + pos[b]) * p.qs[2];
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+            if (valid[b]) {
+                qf[b][c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qf[b][c][j] = static_cast<T>(0.f);
+            }
+        }
+        if (p.mask_mode == KMI_MASK_PACKED) {
+            mrow[b] = m_seq + head[b] * p.ms[1] + static_cast<int64_t>(pos[b]) * lk;
+        } else {
+            mrow[b] = m_seq + head[b] * p.ms[1] + static_cast<int64_t>(pos[b]) * p.ms[2];
+        }
+    }
+
+    // K / V tile prefetch registers.
+    u32x4 kreg[VPT];
+    u32x4 vreg[UPT][2];
+    auto load_tile = [&](int t) {
+        const int key0 = t * BN;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int u = tid + NTHREADS * i;
+            const int key = u / (D / 8), dg = u % (D / 8);
+            const int kk = key0 + key;
+            if (kk < lk) {
+                kreg[i] = *reinterpret_cast<const u32x4*>(
+                    kp + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + kk) * p.ks[2] + 8 * dg);
+            } else {
+                kreg[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+            const int u = tid + NTHREADS * i;
+            const int kpair = u / (D / 8), dg = u % (D / 8);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int kk = key0 + 2 * kpair + e;
+                if (kk < lk) {
+                    vreg[i][e] = *reinterpret_cast<const u32x4*>(
+                        vp + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + kk) * p.vs[2] + 8 * dg);
+                } else {
+                    vreg[i][e] = u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+    };
+    auto store_tile = [&](int buf) {
+        T* kl = k_lds + buf * BN * KP;
+        T* vl = v_lds + buf * D * VP;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int u = tid + NTHREADS * i;
+            const int key = u / (D / 8), dg = u % (D / 8);
+            *reinterpret_cast<u32x4*>(kl + key * KP + 8 * dg) = kreg[i];
+        }
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+            const int u = tid + NTHREADS * i;
+            const int kpair = u / (D / 8), dg = u % (D / 8);
+            const int col = vpos(2 * kpair);
+            const uint16_t* a = reinterpret_cast<const uint16_t*>(&vreg[i][0]);
+            const uint16_t* b = reinterpret_cast<const uint16_t*>(&vreg[i][1]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t pair = static_cast<uint32_t>(a[e]) | (static_cast<uint32_t>(b[e]) << 16);
+                *reinterpret_cast<uint32_t*>(vl + (8 * dg + e) * VP + col) = pair;
+            }
+        }
+    };
+
+    f32x4 o[DB][NQB];
+    float m_run[NQB], l_run[NQB];
+#pragma unroll
+    for (int b = 0; b < NQB; ++b) {
+        m_run[b] = -INFINITY;
+        l_run[b] = 0.f;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) o[d][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    if (t_begin < t_end) {
+        load_tile(t_begin);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (int t = t_begin; t < t_end; ++t) {
+        const int buf = (t - t_begin) & 1;
+        const bool has_next = t + 1 < t_end;
+        if (has_next) load_tile(t + 1);
+        if (wave_active) {
+            const T* kl = k_lds + buf * BN * KP;
+            const T* vl = v_lds + buf * D * VP;
+            f32x4 s[KB][NQB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int b = 0; b < NQB; ++b) s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < DC; ++c) {
+                    const v8 a = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
+#pragma unroll
+                    for (int b = 0; b < NQB; ++b) s[kb][b] = Mfma<T>::run(a, qf[b][c], s[kb][b]);
+                }
+            }
+            const int key0 = t * BN;
+            const bool need_causal = p.causal && (key0 + BN - 1 > first_pos + coff);
+            const bool need_tail = key0 + BN > lk;
+            v8 pf[NQB][BN / 32];
+#pragma unroll
+            for (int b = 0; b < NQB; ++b) {
+                float x[KB][4];
+                float mt = -INFINITY;
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kk = key0 + 16 * kb + 4 * g4 + i;
+                        float val = s[kb][b][i] * p.scale_log2;
+                        if (p.mask_mode != KMI_MASK_NONE && kk < lk)
+                            val += kLog2e * mask_logit(mptr, p.mask_dtype, mrow[b] + kk * m_key);
+                        if ((need_tail && kk >= lk) || (need_causal && kk > pos[b] + coff)) val = -INFINITY;
+                        x[kb][i] = val;
+                        mt = fmaxf(mt, val);
+                    }
+                }
+                mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+                mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+                const float m_new = fmaxf(m_run[b], mt);
+                const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                const float alpha = __builtin_amdgcn_exp2f(m_run[b] - m_use);
+                m_run[b] = m_new;
+                float ls = 0.f;
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float e = __builtin_amdgcn_exp2f(x[kb][i] - m_use);
+                        x[kb][i] = e;
+                        ls += e;
+                    }
+                }
+                l_run[b] = l_run[b] * alpha + ls;
+#pragma unroll
+                for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
+#pragma unroll
+                for (int c2 = 0; c2 < BN / 32; ++c2) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        pf[b][c2][i] = static_cast<T>(x[2 * c2][i]);
+                        pf[b][c2][4 + i] = static_cast<T>(x[2 * c2 + 1][i]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+#pragma unroll
+                for (int c2 = 0; c2 < BN / 32; ++c2) {
+                    const v8 a = *reinterpret_cast<const v8*>(vl + (16 * d + l16) * VP + 32 * c2 + 8 * g4);
+#pragma unroll
+                    for (int b = 0; b < NQB; ++b) o[d][b] = Mfma<T>::run(a, pf[b][c2], o[d][b]);
+                }
+            }
+        }
+        if (has_next) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (!wave_active) return;
+    // Epilogue: l across the four lanes of a row, then O / l (or the split partial).
+#pragma unroll
+    for (int b = 0; b < NQB; ++b) {
+        float l = l_run[b];
+        l += __shfl_xor(l, 16, kWave);
+        l += __shfl_xor(l, 32, kWave);
+        if (!valid[b]) continue;
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const float lse2 = l > 0.f ? m_run[b] + log2f(l) : -INFINITY;
+        if (p.splits > 1) {
+            const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos[b]) * p.hq + head[b];
+            float* dst = p.part_o + prow * D;
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                *reinterpret_cast<f32x4*>(dst + 16 * d + 4 * g4) = o[d][b] * inv;
+            }
+            if (g4 == 0) p.part_lse[prow] = lse2;
+        } else {
+            T* dst = static_cast<T*>(p.out) + ob_off + head[b] * p.os[1] + static_cast<int64_t>(q0 + pos[b]) * p.os[2];
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                typedef T v4 __attribute__((ext_vector_type(4)));
+                v4 w;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(o[d][b][i] * inv);
+                *reinterpret_cast<v4*>(dst + 16 * d + 4 * g4) = w;
+            }
+            if (p.lse && g4 == 0)
+                p.lse[lb_off + head[b] * p.ls[1] + static_cast<int64_t>(q0 + pos[b]) * p.ls[2]] = lse2 * kLn2;
+        }
+    }
+}
+
+// Merge of split-KV partials: one wavefront per (query row, head), lanes over D.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (item >= p.rows_total * p.hq) return;
+    const int64_t row = item / p.hq;
+    const int h = static_cast<int>(item % p.hq);
+    float m = -INFINITY;
+    for (int s = 0; s < p.splits; ++s) m = fmaxf(m, p.part_lse[s * p.rows_total * p.hq + item]);
+    constexpr int PER = D / 64;
+    float acc[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+    float wsum = 0.f;
+    if (m != -INFINITY) {
+        for (int s = 0; s < p.splits; ++s) {
+            const int64_t idx = s * p.rows_total * p.hq + item;
+            const float w = __builtin_amdgcn_exp2f(p.part_lse[idx] - m);
+            wsum += w;
+            const float* src = p.part_o + idx * D;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) acc[j] += w * src[lane + 64 * j];
+        }
+    }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    int seq = 0, posn = static_cast<int>(row);
+    int64_t ob_off = 0, lb_off = 0;
+    if (!p.cu_q) {
+        seq = static_cast<int>(row / p.seq_q);
+        posn = static_cast<int>(row % p.seq_q);
+        ob_off = seq * p.os[0];
+        lb_off = seq * p.ls[0];
+    }
+    T* dst = static_cast<T*>(p.out) + ob_off + h * p.os[1] + static_cast<int64_t>(posn) * p.os[2];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) dst[lane + 64 * j] = static_cast<T>(acc[j] * inv);
+    if (p.lse && lane == 0)
+        p.lse[lb_off + h * p.ls[1] + static_cast<int64_t>(posn) * p.ls[2]] =
+            wsum > 0.f ? (m + log2f(wsum)) * kLn2 : -INFINITY;
+}
+
+constexpr size_t lds_bytes(int d, size_t elem) {
+    return (2 * BN * (d + 8) + 2 * d * (BN + 8)) * elem;
+}
+
+struct Plan {
+    int nqb, nx, splits, tiles_per_split;
+    int64_t rows_total;
+    size_t ws_bytes;
+};
+
+const char* check_args(const kmi_attn_args* a) {
+    if (!a) return "null args";
+    if (a->dtype != KMI_BF16 && a->dtype != KMI_F16) return "dtype must be BF16 or F16";
+    if (a->head_dim != 64 && a->head_dim != 128) return "head_dim must be 64 or 128";
+    if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seq_q < 0 || a->seq_k <= 0)
+        return "sizes must be positive (seq_q may be 0)";
+    if (a->heads_q % a->heads_kv != 0) return "heads_kv must divide heads_q";
+    if (!a->q || !a->k || !a->v || !a->out) return "null q, k, v or out";
+    for (const void* ptr : {a->q, a->k, a->v})
+        if (reinterpret_cast<uintptr_t>(ptr) % 16) return "q, k and v must be 16-byte aligned";
+    if (reinterpret_cast<uintptr_t>(a->out) % 8) return "out must be 8-byte aligned";
+    for (int i = 0; i < 3; ++i) {
+        if (a->q_stride[i] % 8 || a->k_stride[i] % 8 || a->v_stride[i] % 8)
+            return "q, k and v strides must be multiples of 8 elements";
+        if (a->o_stride[i] % 4) return "out strides must be multiples of 4 elements";
+    }
+    if (a->seq_q > (1 << 30) / 64 || a->seq_k > (1 << 30) || a->heads_q > 65536)
+        return "sizes too large";
+    const bool varlen = a->cu_seqlens_q != nullptr;
+    if (varlen != (a->cu_seqlens_k != nullptr)) return "cu_seqlens_q and cu_seqlens_k go together";
+    if (varlen && (a->total_q < 0 || a->total_k <= 0 || a->total_q > (1 << 30) / 64 || a->total_k > (1 << 30)))
+        return "varlen totals out of range";
+    if (a->mask_mode != KMI_MASK_NONE) {
+        if (!a->mask) return "mask_mode set without a mask";
+        if (a->mask_dtype < KMI_BF16 || a->mask_dtype > KMI_BOOL) return "bad mask dtype";
+        if (a->mask_mode == KMI_MASK_PACKED && !varlen) return "packed masks are varlen only";
+        if (a->mask_mode != KMI_MASK_STRIDED && a->mask_mode != KMI_MASK_PACKED) return "bad mask mode";
+    }
+    return nullptr;
+}
+
+Plan make_plan(const kmi_attn_args* a) {
+    Plan pl{};
+    const int64_t G = a->heads_q / a->heads_kv;
+    const int64_t vrows = a->seq_q * G;
+    const int64_t units = a->batch * a->heads_kv;
+    // Two 16-row blocks per wavefront when that still gives every CU two workgroups.
+    pl.nqb = (ceil_div(vrows, 128) * units >= 512) ? 2 : 1;
+    const int64_t bm = 64 * pl.nqb;
+    pl.nx = static_cast<int>(ceil_div(vrows, bm));
+    const int64_t nk = ceil_div(a->seq_k, BN);
+    const int64_t base = static_cast<int64_t>(pl.nx) * units;
+    int64_t splits = 1;
+    if (a->num_splits == 0) {
+        if (base < 128 && nk >= 8) splits = std::min<int64_t>(ceil_div(512, base), nk / 2);
+    } else {
+        splits = std::max<int64_t>(1, std::min<int64_t>(a->num_splits, nk));
+    }
+    pl.tiles_per_split = static_cast<int>(ceil_div(nk, splits));
+    pl.splits = static_cast<int>(ceil_div(nk, pl.tiles_per_split));
+    pl.rows_total = a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q;
+    pl.ws_bytes = 0;
+    return pl;
+}
+
+// Split partials are indexed by query row: b * Sq + i (dense) or the packed token (varlen).
+size_t ws_bytes_for(const kmi_attn_args* a, const Plan& pl) {
+    if (pl.splits <= 1) return 0;
+    return static_cast<size_t>(pl.splits) * pl.rows_total * a->heads_q * (a->head_dim + 1) * sizeof(float);
+}
+
+template <typename T, int D, int NQB>
+hipError_t launch_fwd(const AttnParams& p, int64_t grid, hipStream_t stream) {
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    const size_t lds = lds_bytes(D, sizeof(T));
+    std::call_once(once, [&] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    });
+    if (attr_err != hipSuccess) return attr_err;
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS),
+                       lds, stream, p);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream) {
+    const int64_t grid = static_cast<int64_t>(pl.nx) * p.batch * p.hkv * pl.splits;
+    hipError_t err = pl.nqb == 2 ? launch_fwd<T, D, 2>(p, grid, stream) : launch_fwd<T, D, 1>(p, grid, stream);
+    if (err != hipSuccess || pl.splits <= 1) return err;
+    const int64_t items = p.rows_total * p.hq;
+    hipLaunchKernelGGL((attn_merge_kernel<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 4))), dim3(256), 0,
+                       stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace kmi
+
+extern "C" int kmi_attn_workspace_bytes(const kmi_attn_args* args, size_t* bytes) {
+    using namespace kmi;
+    if (!bytes) return fail(KMI_EINVAL, "kmi_attn_workspace_bytes: null bytes");
+    if (const char* why = check_args(args)) return fail(KMI_EINVAL, std::string("kmi_attn_workspace_bytes: ") + why);
+    *bytes = ws_bytes_for(args, make_plan(args));
+    return KMI_OK;
+}
+
+extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+    using namespace kmi;
+    if (const char* why = check_args(a)) return fail(KMI_EINVAL, std::string("kmi_attn_fwd: ") + why);
+    if (a->seq_q == 0) return KMI_OK;
+    const Plan pl = make_plan(a);
+    const size_t need = ws_bytes_for(a, pl);
+    if (need > 0 && (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16))
+        return fail(KMI_EWORKSPACE, "kmi_attn_fwd: workspace missing, misaligned or smaller than "
+                                    "kmi_attn_workspace_bytes");
+    AttnParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.out = a->out;
+    p.lse = a->lse;
+    for (int i = 0; i < 3; ++i) {
+        p.qs[i] = a->q_stride[i];
+        p.ks[i] = a->k_stride[i];
+        p.vs[i] = a->v_stride[i];
+        p.os[i] = a->o_stride[i];
+        p.ls[i] = a->lse_stride[i];
+    }
+    p.mask = a->mask_mode == KMI_MASK_NONE ? nullptr : a->mask;
+    p.mask_mode = a->mask_mode;
+    p.mask_dtype = a->mask_dtype;
+    for (int i = 0; i < 4; ++i) p.ms[i] = a->mask_stride[i];
+    p.cu_q = a->cu_seqlens_q;
+    p.cu_k = a->cu_seqlens_k;
+    p.batch = static_cast<int>(a->batch);
+    p.hq = static_cast<int>(a->heads_q);
+    p.hkv = static_cast<int>(a->heads_kv);
+    p.group = p.hq / p.hkv;
+    p.seq_q = static_cast<int>(a->seq_q);
+    p.seq_k = static_cast<int>(a->seq_k);
+    p.causal = a->causal ? 1 : 0;
+    p.scale_log2 = static_cast<float>(a->scale * 1.4426950408889634);
+    p.splits = pl.splits;
+    p.tiles_per_split = pl.tiles_per_split;
+    p.nx = pl.nx;
+    p.rows_total = pl.rows_total;
+    p.total_q = static_cast<int>(a->total_q);
+    p.total_k = static_cast<int>(a->total_k);
+    if (pl.splits > 1) {
+        p.part_o = static_cast<float*>(workspace);
+        p.part_lse = p.part_o + static_cast<size_t>(pl.splits) * p.rows_total * p.hq * a->head_dim;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t err;
+    if (a->dtype == KMI_BF16) {
+        err = a->head_dim == 64 ? launch_all<bf16, 64>(p, pl, s) : launch_all<bf16, 128>(p, pl, s);
+    } else {
+        err = a->head_dim == 64 ? launch_all<f16, 64>(p, pl, s) : launch_all<f16, 128>(p, pl, s);
+    }
+    return hip_status(err, "kmi_attn_fwd");
+}

@@ -1,0 +1,296 @@
+// LayerNorm / RMSNorm forward for gfx950 with fp32 statistics.
+//
+// Reference semantics: src/kohakutt_native/csrc/aten/nn/aten_norm.cpp:65-127 (layer_norm:
+// y = (x - mean) * rstd * weight + bias, fp32 mean / rstd), :604-652 (rms_norm), and
+// aten_fused.cpp:13-28 (rms_norm with bias); statistics as ktt_norm/fwd_compute.cpp:
+// 275-358: two passes (mean, then the centred sum of squares), var = relu(M2 / W),
+// rstd = 1 / sqrt(var + eps).  The reference splits a tile row of 32 rows over a group of
+// Tensix cores and merges partial statistics (Chan); here a 64-lane wavefront owns one
+// row, keeps it in registers (one HBM read, one HBM write) and reduces across lanes.
+//
+// Fast path: rows whose width is a multiple of one 16-byte vector and whose pointers are
+// 16-byte aligned; each lane holds up to VPL vectors of the row.  Generic path: one
+// 256-thread block per row with element loads (any width and alignment).
+#include "common.hpp"
+
+namespace kmi {
+namespace {
+
+template <typename T, int E>
+struct alignas(E * sizeof(T)) Pack {
+    T e[E];
+};
+
+template <typename T, int E>
+__device__ __forceinline__ void load_pack(const T* p, float* out) {
+    const Pack<T, E> v = *reinterpret_cast<const Pack<T, E>*>(p);
+#pragma unroll
+    for (int j = 0; j < E; ++j) out[j] = to_f32(v.e[j]);
+}
+
+template <typename T, int E>
+__device__ __forceinline__ void store_pack(T* p, const float* in) {
+    Pack<T, E> v;
+#pragma unroll
+    for (int j = 0; j < E; ++j) v.e[j] = from_f32<T>(in[j]);
+    *reinterpret_cast<Pack<T, E>*>(p) = v;
+}
+
+// One wavefront per row, 4 rows per 256-thread block.  T: x / y; W: weight and bias.
+template <typename T, typename W, int VPL, bool LAYER>
+__global__ __launch_bounds__(256) void norm_rows_wave(
+    const T* __restrict__ x, const W* __restrict__ weight, const W* __restrict__ bias,
+    T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
+    int64_t rows, int width, float eps) {
+    constexpr int E = 16 / sizeof(T);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int nvec = width / E;
+    const T* xr = x + row * width;
+    float v[VPL][E];
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = lane + kWave * i;
+        if (vi < nvec) {
+            load_pack<T, E>(xr + vi * E, v[i]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < E; ++j) v[i][j] = 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < E; ++j) sum += LAYER ? v[i][j] : v[i][j] * v[i][j];
+    }
+    sum = wave_sum(sum);
+    const float inv_w = 1.f / static_cast<float>(width);
+    float mean = 0.f, rstd;
+    if (LAYER) {
+        mean = sum * inv_w;
+        float m2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int vi = lane + kWave * i;
+            if (vi < nvec) {
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const float c = v[i][j] - mean;
+                    m2 += c * c;
+                }
+            }
+        }
+        m2 = wave_sum(m2);
+        rstd = 1.f / sqrtf(fmaxf(m2 * inv_w, 0.f) + eps);
+    } else {
+        rstd = 1.f / sqrtf(sum * inv_w + eps);
+    }
+    T* yr = y + row * width;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = lane + kWave * i;
+        if (vi < nvec) {
+            float o[E], g[E], b[E];
+            if (weight) {
+                load_pack<W, E>(weight + vi * E, g);
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; ++j) g[j] = 1.f;
+            }
+            if (bias) {
+                load_pack<W, E>(bias + vi * E, b);
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; ++j) b[j] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < E; ++j) o[j] = (v[i][j] - mean) * rstd * g[j] + b[j];
+            store_pack<T, E>(yr + vi * E, o);
+        }
+    }
+    if (lane == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
+    switch (dtype) {
+        case KMI_BF16: return to_f32(static_cast<const bf16*>(p)[i]);
+        case KMI_F16: return to_f32(static_cast<const f16*>(p)[i]);
+        default: return static_cast<const float*>(p)[i];
+    }
+}
+
+__device__ __forceinline__ void store_any(void* p, int dtype, int64_t i, float v) {
+    switch (dtype) {
+        case KMI_BF16: static_cast<bf16*>(p)[i] = from_f32<bf16>(v); break;
+        case KMI_F16: static_cast<f16*>(p)[i] = from_f32<f16>(v); break;
+        default: static_cast<float*>(p)[i] = v;
+    }
+}
+
+__device__ float block_sum(float v, float* scratch) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < static_cast<int>(blockDim.x >> 6); ++i) t += scratch[i];
+    return t;
+}
+
+// One 256-thread block per row; any width, any alignment; x read three times.
+template <bool LAYER>
+__global__ __launch_bounds__(256) void norm_rows_generic(
+    const void* x, const void* weight, const void* bias, void* y, float* mean_out,
+    float* rstd_out, int64_t width, int x_dtype, int w_dtype, int b_dtype, float eps) {
+    __shared__ float scratch[4];
+    const int64_t row = blockIdx.x;
+    const int64_t base = row * width;
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
+        const float a = load_any(x, x_dtype, base + i);
+        s += LAYER ? a : a * a;
+    }
+    s = block_sum(s, scratch);
+    const float inv_w = 1.f / static_cast<float>(width);
+    float mean = 0.f, rstd;
+    if (LAYER) {
+        mean = s * inv_w;
+        float m2 = 0.f;
+        for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
+            const float c = load_any(x, x_dtype, base + i) - mean;
+            m2 += c * c;
+        }
+        m2 = block_sum(m2, scratch);
+        rstd = 1.f / sqrtf(fmaxf(m2 * inv_w, 0.f) + eps);
+    } else {
+        rstd = 1.f / sqrtf(s * inv_w + eps);
+    }
+    for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
+        float o = (load_any(x, x_dtype, base + i) - mean) * rstd;
+        if (weight) o *= load_any(weight, w_dtype, i);
+        if (bias) o += load_any(bias, b_dtype, i);
+        store_any(y, x_dtype, base + i, o);
+    }
+    if (threadIdx.x == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+template <typename T, typename W, bool LAYER>
+hipError_t launch_wave(const void* x, const void* w, const void* b, void* y, float* mean,
+                       float* rstd, int64_t rows, int width, float eps, int vpl,
+                       hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(rows, 4))), block(256);
+    auto* xp = static_cast<const T*>(x);
+    auto* wp = static_cast<const W*>(w);
+    auto* bp = static_cast<const W*>(b);
+    auto* yp = static_cast<T*>(y);
+#define KMI_NORM_CASE(N)                                                                  \
+    case N:                                                                               \
+        hipLaunchKernelGGL((norm_rows_wave<T, W, N, LAYER>), grid, block, 0, stream, xp,  \
+                           wp, bp, yp, mean, rstd, rows, width, eps);                     \
+        break;
+    switch (vpl) {
+        KMI_NORM_CASE(1)
+        KMI_NORM_CASE(2)
+        KMI_NORM_CASE(4)
+        KMI_NORM_CASE(8)
+        KMI_NORM_CASE(16)
+        default: return hipErrorInvalidValue;
+    }
+#undef KMI_NORM_CASE
+    return hipGetLastError();
+}
+
+int dtype_size(int dt) {
+    switch (dt) {
+        case KMI_BF16:
+        case KMI_F16: return 2;
+        case KMI_F32: return 4;
+        default: return 0;
+    }
+}
+
+bool aligned(const void* p, int64_t bytes) {
+    return p == nullptr || (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+template <bool LAYER>
+int norm_fwd(const char* name, const void* x, const void* w, const void* b, void* y,
+             float* mean, float* rstd, int64_t rows, int64_t width, int x_dtype,
+             int w_dtype, int b_dtype, double eps, hipStream_t stream) {
+    const int xs = dtype_size(x_dtype);
+    if (xs == 0) return fail(KMI_EINVAL, std::string(name) + ": x dtype must be BF16, F16 or F32");
+    if ((w && dtype_size(w_dtype) == 0) || (b && dtype_size(b_dtype) == 0))
+        return fail(KMI_EINVAL, std::string(name) + ": weight / bias dtype must be BF16, F16 or F32");
+    if (rows < 0 || width < 0) return fail(KMI_EINVAL, std::string(name) + ": negative size");
+    if (rows == 0) return KMI_OK;
+    if (width == 0) return fail(KMI_EINVAL, std::string(name) + ": empty rows");
+    if (!x || !y) return fail(KMI_EINVAL, std::string(name) + ": null x or y");
+    if (rows > (int64_t{1} << 31) * 4 || width > (int64_t{1} << 30))
+        return fail(KMI_EUNSUPPORTED, std::string(name) + ": too many rows or too wide");
+    const float e = static_cast<float>(eps);
+    const int epv = 16 / xs;
+    const int64_t nvec = width / epv;
+    const int64_t vpl_need = ceil_div(nvec, kWave);
+    // Weight and bias share one type on the fast path: x's own type or fp32.
+    const bool params_ok =
+        (!w || w_dtype == x_dtype || w_dtype == KMI_F32) &&
+        (!b || b_dtype == x_dtype || b_dtype == KMI_F32) &&
+        (!w || !b || w_dtype == b_dtype);
+    const int pdt = w ? w_dtype : (b ? b_dtype : x_dtype);
+    const int64_t pbytes = static_cast<int64_t>(epv) * dtype_size(pdt);
+    const bool fast = width % epv == 0 && vpl_need <= 16 && params_ok &&
+                      aligned(x, 16) && aligned(y, 16) && aligned(w, pbytes) &&
+                      aligned(b, pbytes);
+    hipError_t err;
+    if (fast) {
+        int vpl = 1;
+        while (vpl < vpl_need) vpl <<= 1;
+        const int wd = static_cast<int>(width);
+        const bool pf32 = pdt == KMI_F32;
+        switch (x_dtype) {
+            case KMI_BF16:
+                err = pf32 ? launch_wave<bf16, float, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream)
+                           : launch_wave<bf16, bf16, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream);
+                break;
+            case KMI_F16:
+                err = pf32 ? launch_wave<f16, float, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream)
+                           : launch_wave<f16, f16, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream);
+                break;
+            default:
+                err = launch_wave<float, float, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream);
+        }
+    } else {
+        hipLaunchKernelGGL((norm_rows_generic<LAYER>), dim3(static_cast<unsigned>(rows)),
+                           dim3(256), 0, stream, x, w, b, y, mean, rstd, width, x_dtype,
+                           w_dtype, b_dtype, e);
+        err = hipGetLastError();
+    }
+    return hip_status(err, name);
+}
+
+}  // namespace
+}  // namespace kmi
+
+extern "C" int kmi_layer_norm_fwd(const void* x, const void* weight, const void* bias,
+                                  void* y, float* mean, float* rstd, int64_t rows,
+                                  int64_t width, int32_t x_dtype, int32_t w_dtype,
+                                  int32_t b_dtype, double eps, void* stream) {
+    return kmi::norm_fwd<true>("kmi_layer_norm_fwd", x, weight, bias, y, mean, rstd, rows,
+                               width, x_dtype, w_dtype, b_dtype, eps,
+                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kmi_rms_norm_fwd(const void* x, const void* weight, const void* bias,
+                                void* y, float* rstd, int64_t rows, int64_t width,
+                                int32_t x_dtype, int32_t w_dtype, int32_t b_dtype,
+                                double eps, void* stream) {
+    return kmi::norm_fwd<false>("kmi_rms_norm_fwd", x, weight, bias, y, nullptr, rstd,
+                                rows, width, x_dtype, w_dtype, b_dtype, eps,
+                                static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,623 @@
+// torch op layer: the reference's op surface on the CUDA/HIP dispatch keys, calling the
+// C ABI (include/kohakutt_amd.h) into the gfx950 kernels.
+//
+// Reference boundary (src/kohakutt_native/csrc/aten):
+//   attention/aten_attention.cpp:959-974  aten::_fused_sdp_choice (+ its dispatch stub),
+//       aten::_scaled_dot_product_fused_attention_overrideable (+ _backward) on PrivateUse1;
+//   nn/aten_norm.cpp:797-811  aten::native_layer_norm, aten::rms_norm (AutogradPrivateUse1);
+//   nn/aten_fused.cpp:114-127  ktt::rms_norm(x, weight, bias, eps);
+//   attention/aten_varlen.cpp:323-349  ktt::_sdpa_varlen;
+//   attention/aten_attention.cpp:935-952  ktt::sdpa_refusal.
+// Here the same names are registered on CUDA / AutogradCUDA (ROCm tensors use the CUDA
+// key).  torch's scaled_dot_product_attention calls the _fused_sdp_choice dispatch stub
+// directly, so the stub's CUDA entry is replaced too; calls the kernels do not take keep
+// torch's own choice (at::cuda::_fused_sdp_choice), and norms they do not take go to
+// torch's own CUDA kernels.
+#include <ATen/ATen.h>
+#include <ATen/native/transformers/attention.h>
+#include <ATen/ops/_fused_sdp_choice_cuda_dispatch.h>
+#include <ATen/ops/native_layer_norm_cuda_dispatch.h>
+#include <ATen/ops/rms_norm_compositeimplicitautograd_dispatch.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/autograd.h>
+#include <torch/library.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdlib>
+#include <string>
+
+#include "../../include/kohakutt_amd.h"
+
+namespace kta {
+namespace {
+
+using at::Tensor;
+using std::optional;
+
+constexpr double kMaskedLogit = -5e5;
+
+bool env_on(const char* name) {
+    const char* v = std::getenv(name);
+    return !(v && v[0] == '0');
+}
+
+// KMI_ATTENTION=0 / KMI_NORMS=0 (read at load) leave the ops to torch; ktt::_set_enabled
+// switches them at run time.
+std::atomic<bool> g_attention{env_on("KMI_ATTENTION")};
+std::atomic<bool> g_norms{env_on("KMI_NORMS")};
+// Calls the kernels took, per family (ktt::counters).
+std::atomic<int64_t> g_attn_calls{0}, g_norm_calls{0}, g_attn_declined{0};
+
+void check(int status, const char* what) {
+    TORCH_CHECK(status == KMI_OK, "kohakutt_amd: ", what, " failed (", status, "): ", kmi_last_error());
+}
+
+int code_of(at::ScalarType t) {
+    switch (t) {
+        case at::kBFloat16: return KMI_BF16;
+        case at::kHalf: return KMI_F16;
+        case at::kFloat: return KMI_F32;
+        case at::kBool: return KMI_BOOL;
+        default: return 0;
+    }
+}
+
+void* stream_of(const Tensor& t) {
+    return static_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+// ---------------------------------------------------------------- attention
+
+bool mask_given(const optional<Tensor>& m) { return m.has_value() && m->defined(); }
+
+// Why the kernels do not take SDPA(q, k, v, mask, ...), or "" when they do.  The
+// conditions of the reference's fused_refusal (aten_attention.cpp:62-127): 4-D non-empty
+// q/k/v of one float type, fp32 only without gradients (cast to bf16 at entry), no
+// dropout, one head dim, K/V heads dividing Q heads, causal without a mask, a mask that
+// broadcasts to [B, H, Sq, Sk]; plus what these kernels cover: CUDA tensors, head dim 64
+// or 128, bool / bf16 / f16 / f32 / f64 masks.
+std::string sdpa_refusal_impl(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask,
+                              double dropout_p, bool is_causal) {
+    if (!g_attention.load()) return "kohakutt_amd attention is switched off";
+    const bool grads = q.requires_grad() || k.requires_grad() || v.requires_grad();
+    for (const Tensor* t : {&q, &k, &v}) {
+        const auto st = t->scalar_type();
+        if (!t->is_cuda() || t->dim() != 4 || t->numel() == 0 ||
+            !(st == at::kBFloat16 || st == at::kHalf || (st == at::kFloat && !grads)) ||
+            st != q.scalar_type())
+            return "q, k and v must be non-empty 4-D bf16 / fp16 GPU tensors (fp32 without gradients)";
+    }
+    if (dropout_p != 0.0) return "dropout";
+    const int64_t d = q.size(3);
+    if (k.size(3) != d || v.size(3) != d) return "q, k and v need one head dim";
+    if (d != 64 && d != 128) return "head dim must be 64 or 128";
+    if (k.size(0) != q.size(0) || v.size(0) != q.size(0) || v.size(1) != k.size(1) || q.size(1) % k.size(1) != 0 ||
+        v.size(2) != k.size(2))
+        return "q, k and v shapes do not match (K / V heads must divide Q heads)";
+    if (is_causal && mask.has_value()) return "causal takes no mask";
+    if (mask_given(mask)) {
+        const Tensor& m = *mask;
+        if (!m.is_cuda() || m.device() != q.device()) return "the mask must be on q's device";
+        if (m.dim() > 4) return "the mask must broadcast to [B, H, Sq, Sk]";
+        const int64_t full[4] = {q.size(0), q.size(1), q.size(2), k.size(2)};
+        for (int64_t i = 0; i < m.dim(); ++i) {
+            const int64_t s = m.size(m.dim() - 1 - i);
+            if (s != 1 && s != full[3 - i]) return "the mask must broadcast to [B, H, Sq, Sk]";
+        }
+        const auto mt = m.scalar_type();
+        if (!(mt == at::kBool || mt == at::kBFloat16 || mt == at::kHalf || mt == at::kFloat || mt == at::kDouble))
+            return "mask dtype must be bool or floating";
+    }
+    return "";
+}
+
+// q/k/v as the kernels read them: last-dim stride 1, 16-byte aligned, strides multiples
+// of 8 elements; anything else is copied once.
+Tensor kernel_operand(const Tensor& t) {
+    bool ok = t.stride(-1) == 1 && reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0;
+    for (int64_t i = 0; ok && i + 1 < t.dim(); ++i) ok = t.stride(i) % 8 == 0;
+    return ok ? t : t.contiguous();
+}
+
+// The mask as a 4-D strided view broadcast to [B, H, Sq, Sk] (broadcast dims stride 0).
+Tensor mask_operand(const Tensor& m, const Tensor& q, int64_t sk) {
+    Tensor x = m;
+    if (x.scalar_type() == at::kDouble) x = x.to(at::kFloat);
+    while (x.dim() < 4) x = x.unsqueeze(0);
+    return x.expand({q.size(0), q.size(1), q.size(2), sk});
+}
+
+struct AttnOut {
+    Tensor out, lse;
+};
+
+AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, const optional<Tensor>& mask,
+                      bool is_causal, optional<double> scale) {
+    c10::DeviceGuard guard(q_in.device());
+    Tensor q = q_in, k = k_in, v = v_in;
+    const bool fp32 = q.scalar_type() == at::kFloat;
+    if (fp32) {
+        // The reference casts fp32 (without gradients) to bf16 at entry and the output
+        // back (aten_attention.cpp:400-415).
+        q = q.to(at::kBFloat16);
+        k = k.to(at::kBFloat16);
+        v = v.to(at::kBFloat16);
+    }
+    q = kernel_operand(q);
+    k = kernel_operand(k);
+    v = kernel_operand(v);
+    const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3);
+    const int64_t Hk = k.size(1), Sk = k.size(2);
+    Tensor out = at::empty({B, H, Sq, D}, q.options());
+    Tensor lse = at::empty({B, H, Sq}, q.options().dtype(at::kFloat));
+    kmi_attn_args a{};
+    a.q = q.data_ptr();
+    a.k = k.data_ptr();
+    a.v = v.data_ptr();
+    a.out = out.data_ptr();
+    a.lse = lse.data_ptr<float>();
+    a.dtype = code_of(q.scalar_type());
+    a.causal = is_causal ? 1 : 0;
+    a.batch = B;
+    a.heads_q = H;
+    a.heads_kv = Hk;
+    a.seq_q = Sq;
+    a.seq_k = Sk;
+    a.head_dim = D;
+    for (int i = 0; i < 3; ++i) {
+        a.q_stride[i] = q.stride(i);
+        a.k_stride[i] = k.stride(i);
+        a.v_stride[i] = v.stride(i);
+        a.o_stride[i] = out.stride(i);
+        a.lse_stride[i] = lse.stride(i);
+    }
+    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
+    Tensor m;
+    if (mask_given(mask)) {
+        m = mask_operand(*mask, q, Sk);
+        a.mask = m.data_ptr();
+        a.mask_dtype = code_of(m.scalar_type());
+        a.mask_mode = KMI_MASK_STRIDED;
+        for (int i = 0; i < 4; ++i) a.mask_stride[i] = m.stride(i);
+    }
+    size_t ws = 0;
+    check(kmi_attn_workspace_bytes(&a, &ws), "kmi_attn_workspace_bytes");
+    Tensor work;
+    if (ws) work = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
+    check(kmi_attn_fwd(&a, ws ? work.data_ptr() : nullptr, ws, stream_of(q)), "kmi_attn_fwd");
+    g_attn_calls.fetch_add(1);
+    if (fp32) out = out.to(at::kFloat);
+    return {out, lse};
+}
+
+using SdpaResult = std::tuple<Tensor, Tensor, Tensor, Tensor, c10::SymInt, c10::SymInt, Tensor, Tensor, Tensor>;
+
+// aten::_scaled_dot_product_fused_attention_overrideable on CUDA (the reference's
+// tt_sdpa_overrideable, aten_attention.cpp:389-713): the kernels, or the math route for
+// calls they refuse.  The log-sum-exp is always written (fp32, natural log).
+SdpaResult sdpa_overrideable(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& attn_bias,
+                             double dropout_p, bool is_causal, bool return_debug_mask, optional<double> scale) {
+    (void)return_debug_mask;
+    const int64_t sq = q.size(2), sk = k.size(2);
+    const std::string why = sdpa_refusal_impl(q, k, v, attn_bias, dropout_p, is_causal);
+    Tensor out, lse;
+    if (why.empty()) {
+        auto r = run_attention(q, k, v, attn_bias, is_causal, scale);
+        out = r.out;
+        lse = r.lse;
+    } else {
+        g_attn_declined.fetch_add(1);
+        out = std::get<0>(at::_scaled_dot_product_attention_math(q, k, v, attn_bias, dropout_p, is_causal,
+                                                                  std::nullopt, scale, q.size(1) != k.size(1)));
+        lse = at::empty({q.size(0), q.size(1), sq}, q.options().dtype(at::kFloat));
+    }
+    auto seed = at::empty({}, at::dtype(at::kLong));
+    auto offset = at::empty({}, at::dtype(at::kLong));
+    return {out, lse, Tensor(), Tensor(), c10::SymInt(sq), c10::SymInt(sk), seed, offset, Tensor()};
+}
+
+// The math backward of the overrideable op, in fp32 (the reference's
+// tt_sdpa_overrideable_backward recomputes through math off its training route,
+// aten_attention.cpp:716-812).  Probabilities follow the forward's mask semantics.
+std::tuple<Tensor, Tensor, Tensor, Tensor> sdpa_overrideable_backward(
+    const Tensor& grad_out, const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& attn_bias,
+    std::array<bool, 4> grad_input_mask, const Tensor& out, const Tensor& logsumexp, const Tensor& cum_seq_q,
+    const Tensor& cum_seq_k, c10::SymInt max_q, c10::SymInt max_k, double dropout_p, bool is_causal,
+    const Tensor& philox_seed, const Tensor& philox_offset, optional<double> scale) {
+    (void)out, (void)logsumexp, (void)cum_seq_q, (void)cum_seq_k, (void)max_q, (void)max_k;
+    (void)philox_seed, (void)philox_offset;
+    TORCH_CHECK(dropout_p == 0.0, "kohakutt_amd: attention backward takes no dropout");
+    c10::DeviceGuard guard(q.device());
+    const int64_t H = q.size(1), Hk = k.size(1), Sq = q.size(2), Sk = k.size(2), D = q.size(3);
+    const int64_t G = H / Hk;
+    const double s = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
+    Tensor qf = q.to(at::kFloat), kf = k.to(at::kFloat), vf = v.to(at::kFloat), go = grad_out.to(at::kFloat);
+    if (G > 1) {
+        kf = kf.repeat_interleave(G, 1);
+        vf = vf.repeat_interleave(G, 1);
+    }
+    Tensor logits = at::matmul(qf, kf.transpose(-2, -1).contiguous()) * s;
+    if (attn_bias.defined()) {
+        Tensor add = attn_bias.scalar_type() == at::kBool
+                         ? at::zeros(attn_bias.sizes(), logits.options()).masked_fill(attn_bias.logical_not(), kMaskedLogit)
+                         : attn_bias.to(at::kFloat).clamp_min(kMaskedLogit);
+        logits = logits + add;
+    }
+    if (is_causal) {
+        auto keep = at::ones({Sq, Sk}, q.options().dtype(at::kBool)).tril();
+        logits = logits.masked_fill(keep.logical_not(), -INFINITY);
+    }
+    Tensor p = at::softmax(logits, -1);
+    Tensor dv = at::matmul(p.transpose(-2, -1).contiguous(), go);
+    Tensor dp = at::matmul(go, vf.transpose(-2, -1).contiguous());
+    Tensor ds = p * (dp - (dp * p).sum(-1, true));
+    Tensor dq = at::matmul(ds, kf) * s;
+    Tensor dk = at::matmul(ds.transpose(-2, -1).contiguous(), qf) * s;
+    if (G > 1) {
+        dk = dk.view({q.size(0), Hk, G, Sk, D}).sum(2);
+        dv = dv.view({q.size(0), Hk, G, Sk, D}).sum(2);
+    }
+    Tensor dbias;
+    if (grad_input_mask[3] && attn_bias.defined() && attn_bias.is_floating_point()) {
+        dbias = ds.sum_to_size(attn_bias.sizes()).to(attn_bias.scalar_type());
+    }
+    return {grad_input_mask[0] ? dq.to(q.scalar_type()) : Tensor(),
+            grad_input_mask[1] ? dk.to(k.scalar_type()) : Tensor(),
+            grad_input_mask[2] ? dv.to(v.scalar_type()) : Tensor(), dbias};
+}
+
+// The _fused_sdp_choice dispatch stub's CUDA entry and the aten op: overrideable when
+// the kernels take the call (and torch.nn.attention.sdpa_kernel allows that backend),
+// torch's own choice otherwise (the reference's tt_fused_sdp_choice,
+// aten_attention.cpp:194-219).
+int64_t fused_sdp_choice(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask,
+                         double dropout_p, bool is_causal, optional<double> scale, bool enable_gqa) {
+    if (at::globalContext().userEnabledOverrideableSDP() &&
+        sdpa_refusal_impl(q, k, v, mask, dropout_p, is_causal).empty())
+        return static_cast<int64_t>(at::SDPBackend::overrideable);
+    return at::cuda::_fused_sdp_choice(q, k, v, mask, dropout_p, is_causal, scale, enable_gqa);
+}
+
+std::string sdpa_refusal_op(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask,
+                            bool is_causal) {
+    return sdpa_refusal_impl(q, k, v, mask, 0.0, is_causal);
+}
+
+// ---------------------------------------------------------------- varlen
+
+// ktt::_sdpa_varlen: packed attention over cu_seqlens (the reference's
+// aten_varlen.cpp:165-231 / bridge::sdpa_varlen).  key_mask: [Tk] bool keep-mask or
+// additive; attn_mask: every sequence's [Lq_i, Lk_i] block, concatenated (additive or
+// bool), shared by the heads.  Returns (out [Tq, H, D], lse [H, Tq] fp32).
+std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in,
+                                       const Tensor& cu_q_in, const Tensor& cu_k_in, int64_t max_q, int64_t max_k,
+                                       bool is_causal, optional<double> scale, const optional<Tensor>& key_mask,
+                                       const optional<Tensor>& attn_mask) {
+    TORCH_CHECK(q_in.is_cuda() && k_in.is_cuda() && v_in.is_cuda(), "kohakutt_amd: sdpa_varlen needs GPU tensors");
+    TORCH_CHECK(q_in.dim() == 3 && k_in.dim() == 3 && v_in.dim() == 3,
+                "kohakutt_amd: sdpa_varlen takes q [Tq, H, D], k / v [Tk, Hk, D]");
+    TORCH_CHECK(k_in.size(0) == v_in.size(0) && k_in.size(1) == v_in.size(1) && q_in.size(1) % k_in.size(1) == 0,
+                "kohakutt_amd: sdpa_varlen shapes do not match (K / V heads must divide Q heads)");
+    TORCH_CHECK(q_in.size(2) == k_in.size(2) && v_in.size(2) == q_in.size(2),
+                "kohakutt_amd: sdpa_varlen needs one head dim");
+    TORCH_CHECK(!(mask_given(key_mask) && mask_given(attn_mask)),
+                "kohakutt_amd: sdpa_varlen takes key_mask or attn_mask, not both");
+    c10::DeviceGuard guard(q_in.device());
+    Tensor q = q_in, k = k_in, v = v_in;
+    const bool fp32 = q.scalar_type() == at::kFloat;
+    if (fp32) {
+        q = q.to(at::kBFloat16);
+        k = k.to(at::kBFloat16);
+        v = v.to(at::kBFloat16);
+    }
+    TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type() &&
+                    (q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf),
+                "kohakutt_amd: sdpa_varlen takes bf16 / fp16 (or fp32, cast to bf16)");
+    q = kernel_operand(q);
+    k = kernel_operand(k);
+    v = kernel_operand(v);
+    const int64_t nseq = cu_q_in.numel() - 1;
+    TORCH_CHECK(nseq >= 1 && cu_k_in.numel() == cu_q_in.numel(),
+                "kohakutt_amd: sdpa_varlen needs cumulative offsets [0, ..., total] of equal count for queries and keys");
+    Tensor cu_q = cu_q_in.to(q.device(), at::kInt).contiguous();
+    Tensor cu_k = cu_k_in.to(q.device(), at::kInt).contiguous();
+    const int64_t Tq = q.size(0), H = q.size(1), D = q.size(2), Tk = k.size(0);
+    Tensor out = at::empty({Tq, H, D}, q.options());
+    Tensor lse = at::empty({H, Tq}, q.options().dtype(at::kFloat));
+    if (Tq == 0) return {fp32 ? out.to(at::kFloat) : out, lse};
+    TORCH_CHECK(Tk > 0, "kohakutt_amd: sdpa_varlen: a sequence with queries needs keys");
+    kmi_attn_args a{};
+    a.q = q.data_ptr();
+    a.k = k.data_ptr();
+    a.v = v.data_ptr();
+    a.out = out.data_ptr();
+    a.lse = lse.data_ptr<float>();
+    a.dtype = code_of(q.scalar_type());
+    a.causal = is_causal ? 1 : 0;
+    a.batch = nseq;
+    a.heads_q = H;
+    a.heads_kv = k.size(1);
+    a.seq_q = std::max<int64_t>(1, max_q);
+    a.seq_k = std::max<int64_t>(1, max_k);
+    a.head_dim = D;
+    // [T, H, D] tensors: stride[1] is the head stride, stride[2] the token stride.
+    a.q_stride[1] = q.stride(1);
+    a.q_stride[2] = q.stride(0);
+    a.k_stride[1] = k.stride(1);
+    a.k_stride[2] = k.stride(0);
+    a.v_stride[1] = v.stride(1);
+    a.v_stride[2] = v.stride(0);
+    a.o_stride[1] = out.stride(1);
+    a.o_stride[2] = out.stride(0);
+    a.lse_stride[1] = lse.stride(0);
+    a.lse_stride[2] = lse.stride(1);
+    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
+    a.cu_seqlens_q = cu_q.data_ptr<int32_t>();
+    a.cu_seqlens_k = cu_k.data_ptr<int32_t>();
+    a.total_q = Tq;
+    a.total_k = Tk;
+    Tensor m;
+    if (mask_given(key_mask)) {
+        m = *key_mask;
+        TORCH_CHECK(m.dim() == 1 && m.size(0) == Tk, "kohakutt_amd: sdpa_varlen key_mask must be [", Tk,
+                    "] (one value per packed key)");
+        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
+        m = m.to(q.device()).contiguous();
+        a.mask_mode = KMI_MASK_STRIDED;
+        a.mask_stride[3] = 1;
+    } else if (mask_given(attn_mask)) {
+        // The block-packed mask must hold sum(Lq_i * Lk_i) values: the offsets are read
+        // on the host to check it (the kernels index the mask by them).
+        Tensor hq = cu_q_in.to(at::kCPU, at::kLong).contiguous(), hk = cu_k_in.to(at::kCPU, at::kLong).contiguous();
+        const int64_t* pq = hq.data_ptr<int64_t>();
+        const int64_t* pk = hk.data_ptr<int64_t>();
+        int64_t need = 0;
+        for (int64_t i = 0; i < nseq; ++i) {
+            const int64_t a0 = std::min(std::max<int64_t>(pq[i], 0), Tq), a1 = std::min(std::max(pq[i + 1], a0), Tq);
+            const int64_t b0 = std::min(std::max<int64_t>(pk[i], 0), Tk), b1 = std::min(std::max(pk[i + 1], b0), Tk);
+            need += (a1 - a0) * (b1 - b0);
+        }
+        m = *attn_mask;
+        TORCH_CHECK(m.numel() == need, "kohakutt_amd: sdpa_varlen packed mask must hold sum(Lq_i * Lk_i) = ", need,
+                    " values, got ", m.numel());
+        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
+        m = m.to(q.device()).contiguous().view({-1});
+        a.mask_mode = KMI_MASK_PACKED;
+    }
+    if (m.defined()) {
+        a.mask = m.data_ptr();
+        a.mask_dtype = code_of(m.scalar_type());
+        TORCH_CHECK(a.mask_dtype != 0, "kohakutt_amd: sdpa_varlen mask dtype must be bool or floating");
+    }
+    size_t ws = 0;
+    check(kmi_attn_workspace_bytes(&a, &ws), "kmi_attn_workspace_bytes");
+    Tensor work;
+    if (ws) work = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
+    check(kmi_attn_fwd(&a, ws ? work.data_ptr() : nullptr, ws, stream_of(q)), "kmi_attn_fwd (varlen)");
+    g_attn_calls.fetch_add(1);
+    return {fp32 ? out.to(at::kFloat) : out, lse};
+}
+
+// ---------------------------------------------------------------- norms
+
+bool norm_dtype(at::ScalarType t) { return t == at::kBFloat16 || t == at::kHalf || t == at::kFloat; }
+
+// True when the kernels take a norm of x over its trailing `normalized` dims with
+// parameters `params` (undefined, or GPU tensors with `width` elements).  Mirrors the
+// reference's own_norm (aten_norm.cpp:22-40), widened to any trailing dims.
+bool norms_take(const Tensor& x, int64_t width, std::initializer_list<const optional<Tensor>*> params) {
+    if (!g_norms.load() || !x.is_cuda() || x.numel() == 0 || !norm_dtype(x.scalar_type()) || width <= 0) return false;
+    for (const auto* p : params) {
+        if (*p && (*p)->defined() &&
+            (!(*p)->is_cuda() || (*p)->device() != x.device() || (*p)->numel() != width ||
+             !norm_dtype((*p)->scalar_type())))
+            return false;
+    }
+    return true;
+}
+
+// Weight / bias as the kernels read them: contiguous, one type that is x's or fp32.
+void norm_params(const Tensor& x, optional<Tensor>& w, optional<Tensor>& b) {
+    const bool hw = w && w->defined(), hb = b && b->defined();
+    auto st = hw ? w->scalar_type() : (hb ? b->scalar_type() : x.scalar_type());
+    const bool same = (!hw || w->scalar_type() == st) && (!hb || b->scalar_type() == st);
+    if (!same || (st != x.scalar_type() && st != at::kFloat)) st = at::kFloat;
+    if (hw) w = w->to(st).contiguous();
+    if (hb) b = b->to(st).contiguous();
+}
+
+std::tuple<Tensor, Tensor, Tensor> native_layer_norm(const Tensor& input, at::IntArrayRef normalized_shape,
+                                                     const optional<Tensor>& weight, const optional<Tensor>& bias,
+                                                     double eps) {
+    const int64_t nd = static_cast<int64_t>(normalized_shape.size());
+    bool shape_ok = nd >= 1 && nd <= input.dim();
+    for (int64_t i = 0; shape_ok && i < nd; ++i) shape_ok = input.size(input.dim() - nd + i) == normalized_shape[i];
+    int64_t width = 1;
+    for (auto s : normalized_shape) width *= s;
+    if (!shape_ok || !norms_take(input, width, {&weight, &bias}))
+        return at::cuda::native_layer_norm(input, normalized_shape, weight, bias, eps);
+    c10::DeviceGuard guard(input.device());
+    Tensor x = input.contiguous();
+    optional<Tensor> w = weight, b = bias;
+    norm_params(x, w, b);
+    const int64_t rows = x.numel() / width;
+    std::vector<int64_t> stat_sizes(input.sizes().begin(), input.sizes().end());
+    for (int64_t i = input.dim() - nd; i < input.dim(); ++i) stat_sizes[i] = 1;
+    Tensor y = at::empty_like(x);
+    Tensor mean = at::empty(stat_sizes, x.options().dtype(at::kFloat));
+    Tensor rstd = at::empty(stat_sizes, x.options().dtype(at::kFloat));
+    const bool hw = w && w->defined(), hb = b && b->defined();
+    check(kmi_layer_norm_fwd(x.data_ptr(), hw ? w->data_ptr() : nullptr, hb ? b->data_ptr() : nullptr, y.data_ptr(),
+                             mean.data_ptr<float>(), rstd.data_ptr<float>(), rows, width, code_of(x.scalar_type()),
+                             hw ? code_of(w->scalar_type()) : 0, hb ? code_of(b->scalar_type()) : 0, eps,
+                             stream_of(x)),
+          "kmi_layer_norm_fwd");
+    g_norm_calls.fetch_add(1);
+    return {y, mean, rstd};
+}
+
+// y, rstd of RMSNorm over the trailing dims (width elements per row), optional bias.
+std::tuple<Tensor, Tensor> rms_forward(const Tensor& input, int64_t width, optional<Tensor> w, optional<Tensor> b,
+                                       double eps, int64_t nd) {
+    c10::DeviceGuard guard(input.device());
+    Tensor x = input.contiguous();
+    norm_params(x, w, b);
+    const int64_t rows = x.numel() / width;
+    std::vector<int64_t> stat_sizes(input.sizes().begin(), input.sizes().end());
+    for (int64_t i = input.dim() - nd; i < input.dim(); ++i) stat_sizes[i] = 1;
+    Tensor y = at::empty_like(x);
+    Tensor rstd = at::empty(stat_sizes, x.options().dtype(at::kFloat));
+    const bool hw = w && w->defined(), hb = b && b->defined();
+    check(kmi_rms_norm_fwd(x.data_ptr(), hw ? w->data_ptr() : nullptr, hb ? b->data_ptr() : nullptr, y.data_ptr(),
+                           rstd.data_ptr<float>(), rows, width, code_of(x.scalar_type()),
+                           hw ? code_of(w->scalar_type()) : 0, hb ? code_of(b->scalar_type()) : 0, eps, stream_of(x)),
+          "kmi_rms_norm_fwd");
+    g_norm_calls.fetch_add(1);
+    return {y, rstd};
+}
+
+// RMSNorm with gradients: the kernel forward, an fp32 backward from the saved rstd (the
+// reference's RmsNormFunction, aten_norm.cpp:548-599).
+struct RmsNormFn : public torch::autograd::Function<RmsNormFn> {
+    static Tensor forward(torch::autograd::AutogradContext* ctx, const Tensor& x, const Tensor& w, int64_t nd,
+                          double eps) {
+        int64_t width = 1;
+        for (int64_t i = x.dim() - nd; i < x.dim(); ++i) width *= x.size(i);
+        optional<Tensor> wo;
+        if (w.defined()) wo = w;
+        auto [y, rstd] = rms_forward(x, width, wo, std::nullopt, eps, nd);
+        ctx->save_for_backward({x, w, rstd});
+        ctx->saved_data["nd"] = nd;
+        return y;
+    }
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                   torch::autograd::variable_list grads) {
+        auto saved = ctx->get_saved_variables();
+        const Tensor& x = saved[0];
+        const Tensor& w = saved[1];
+        const Tensor& rstd = saved[2];
+        const int64_t nd = ctx->saved_data["nd"].toInt();
+        std::vector<int64_t> dims;
+        for (int64_t i = x.dim() - nd; i < x.dim(); ++i) dims.push_back(i);
+        int64_t width = 1;
+        for (auto d : dims) width *= x.size(d);
+        Tensor g = grads[0].to(at::kFloat), xf = x.to(at::kFloat);
+        Tensor xhat = xf * rstd;
+        Tensor gw = w.defined() ? g * w.to(at::kFloat) : g;
+        Tensor dx = rstd * (gw - xhat * (gw * xhat).sum(dims, true) / static_cast<double>(width));
+        Tensor dw;
+        if (w.defined()) {
+            std::vector<int64_t> lead;
+            for (int64_t i = 0; i < x.dim() - nd; ++i) lead.push_back(i);
+            dw = lead.empty() ? (g * xhat) : (g * xhat).sum(lead);
+            dw = dw.reshape(w.sizes()).to(w.scalar_type());
+        }
+        return {dx.to(x.scalar_type()), dw, Tensor(), Tensor()};
+    }
+};
+
+// aten::rms_norm at AutogradCUDA (the reference registers it at AutogradPrivateUse1,
+// aten_norm.cpp:604-652,797-799); eps defaults to float32 epsilon.
+Tensor rms_norm(const Tensor& input, c10::SymIntArrayRef normalized_shape, const optional<Tensor>& weight,
+                optional<double> eps) {
+    const double e = eps.value_or(static_cast<double>(std::numeric_limits<float>::epsilon()));
+    const int64_t nd = static_cast<int64_t>(normalized_shape.size());
+    bool shape_ok = nd >= 1 && nd <= input.dim();
+    int64_t width = 1;
+    for (int64_t i = 0; shape_ok && i < nd; ++i) {
+        const auto s = normalized_shape[i].maybe_as_int();
+        shape_ok = s.has_value() && input.size(input.dim() - nd + i) == *s;
+        if (shape_ok) width *= *s;
+    }
+    if (!shape_ok || !norms_take(input, width, {&weight})) return at::compositeimplicitautograd::rms_norm_symint(input, normalized_shape, weight, eps);
+    const bool hw = weight && weight->defined();
+    const bool grads = at::GradMode::is_enabled() && (input.requires_grad() || (hw && weight->requires_grad()));
+    if (grads) return RmsNormFn::apply(input, hw ? *weight : Tensor(), nd, e);
+    at::AutoDispatchBelowADInplaceOrView below;
+    return std::get<0>(rms_forward(input, width, weight, std::nullopt, e, nd));
+}
+
+// ktt::rms_norm(x, weight, bias, eps): RMSNorm over the last dim with an optional bias,
+// one kernel on GPU tensors (aten_fused.cpp:60-85), the fp32 composite elsewhere
+// (aten_fused.cpp:13-28).
+Tensor ktt_rms_norm_cuda(const Tensor& x, const optional<Tensor>& weight, const optional<Tensor>& bias, double eps) {
+    TORCH_CHECK(x.dim() >= 1, "ktt::rms_norm needs at least one dim");
+    const int64_t width = x.size(-1);
+    if (!norms_take(x, width, {&weight, &bias})) {
+        optional<Tensor> w;
+        if (weight && weight->defined()) w = weight->to(at::kFloat);
+        Tensor y = at::rms_norm(x.to(at::kFloat), {width}, w, eps);
+        if (bias && bias->defined()) y = y + bias->to(at::kFloat);
+        return y.to(x.scalar_type());
+    }
+    return std::get<0>(rms_forward(x, width, weight, bias, eps, 1));
+}
+
+Tensor ktt_rms_norm_composite(const Tensor& x, const optional<Tensor>& weight, const optional<Tensor>& bias,
+                              double eps) {
+    optional<Tensor> w;
+    if (weight && weight->defined()) w = weight->to(at::kFloat);
+    Tensor y = at::rms_norm(x.to(at::kFloat), {x.size(-1)}, w, eps);
+    if (bias && bias->defined()) y = y + bias->to(at::kFloat);
+    return y.to(x.scalar_type());
+}
+
+// ---------------------------------------------------------------- control
+
+void set_enabled(bool attention, bool norms) {
+    g_attention.store(attention);
+    g_norms.store(norms);
+}
+
+std::vector<int64_t> counters() {
+    return {g_attn_calls.load(), g_attn_declined.load(), g_norm_calls.load(),
+            g_attention.load() ? 1 : 0, g_norms.load() ? 1 : 0};
+}
+
+void reset_counters() {
+    g_attn_calls.store(0);
+    g_attn_declined.store(0);
+    g_norm_calls.store(0);
+}
+
+// Installs the CUDA entry of the _fused_sdp_choice stub at load time.
+struct StubInstall {
+    StubInstall() { at::native::_fused_sdp_choice_stub.set_cuda_dispatch_ptr(&fused_sdp_choice); }
+} g_stub_install;
+
+}  // namespace
+}  // namespace kta
+
+TORCH_LIBRARY(ktt, m) {
+    m.def("rms_norm(Tensor x, Tensor? weight=None, Tensor? bias=None, float eps=1e-6) -> Tensor");
+    m.def(
+        "_sdpa_varlen(Tensor q, Tensor k, Tensor v, Tensor cu_seq_q, Tensor cu_seq_k, int max_q, int max_k, "
+        "bool is_causal=False, float? scale=None, Tensor? key_mask=None, Tensor? attn_mask=None) -> (Tensor, Tensor)");
+    m.def("sdpa_refusal(Tensor q, Tensor k, Tensor v, Tensor? mask=None, bool is_causal=False) -> str",
+          TORCH_FN(kta::sdpa_refusal_op));
+    m.def("_set_enabled(bool attention, bool norms) -> ()", TORCH_FN(kta::set_enabled));
+    m.def("counters() -> int[]", TORCH_FN(kta::counters));
+    m.def("reset_counters() -> ()", TORCH_FN(kta::reset_counters));
+}
+
+TORCH_LIBRARY_IMPL(ktt, CUDA, m) {
+    m.impl("rms_norm", TORCH_FN(kta::ktt_rms_norm_cuda));
+    m.impl("_sdpa_varlen", TORCH_FN(kta::sdpa_varlen));
+}
+
+TORCH_LIBRARY_IMPL(ktt, CompositeExplicitAutograd, m) {
+    m.impl("rms_norm", TORCH_FN(kta::ktt_rms_norm_composite));
+}
+
+TORCH_LIBRARY_IMPL(aten, CUDA, m) {
+    m.impl("_fused_sdp_choice", TORCH_FN(kta::fused_sdp_choice));
+    m.impl("_scaled_dot_product_fused_attention_overrideable", TORCH_FN(kta::sdpa_overrideable));
+    m.impl("_scaled_dot_product_fused_attention_overrideable_backward", TORCH_FN(kta::sdpa_overrideable_backward));
+    m.impl("native_layer_norm", TORCH_FN(kta::native_layer_norm));
+}
+
+TORCH_LIBRARY_IMPL(aten, AutogradCUDA, m) {
+    m.impl("rms_norm", TORCH_FN(kta::rms_norm));
+}

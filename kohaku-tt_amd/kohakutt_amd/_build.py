@@ -1,0 +1,148 @@
+"""In-tree build of the native parts, gfx950 only.
+
+* ``libkohakutt_amd.so`` -- the HIP kernels and the C ABI (``include/kohakutt_amd.h``),
+  built with ``hipcc --offload-arch=gfx950``; no torch.
+* ``_torch_ops.so`` -- the torch op registrations (``csrc/torch_ops.cpp``), a host-only
+  C++ library linked against torch and ``libkohakutt_amd.so`` and loaded with
+  ``torch.ops.load_library``.
+
+Both land next to this file so they travel with the source tree.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent  # kohaku-tt_amd/
+REPO = ROOT.parent
+CSRC = ROOT / "csrc"
+BUILD = ROOT / "_build"
+INCLUDE = REPO / "include"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = ROCM / "bin" / "hipcc"
+ARCH = "gfx950"
+
+CAPI_LIB = PKG / "libkohakutt_amd.so"
+OPS_LIB = PKG / "_torch_ops.so"
+
+HIP_SOURCES = ["capi.hip", "norm.hip", "attention.hip"]
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-Wall",
+    # Packed fp32 VALU forms are kept out of every kernel.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in proc.stdout.splitlines() if "packed-fp32-ops" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(map(str, cmd))}\n{out}")
+    return out
+
+
+def build_capi(jobs: int = 4) -> Path:
+    """Compiles the HIP kernels and links ``libkohakutt_amd.so``."""
+    BUILD.mkdir(exist_ok=True)
+    objs = []
+    cmds = []
+    for src in HIP_SOURCES:
+        obj = BUILD / (src + ".o")
+        objs.append(obj)
+        cmds.append([str(HIPCC), *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(_run, cmds))
+    tmp = CAPI_LIB.with_suffix(".so.tmp")
+    _run([str(HIPCC), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, CAPI_LIB)
+    return CAPI_LIB
+
+
+def _torch_paths():
+    import torch
+    import torch.utils.cpp_extension as ext
+
+    incs = ext.include_paths()
+    libdir = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return incs, libdir, abi
+
+
+def build_torch_ops() -> Path:
+    """Compiles ``csrc/torch_ops.cpp`` into ``_torch_ops.so``."""
+    incs, libdir, abi = _torch_paths()
+    BUILD.mkdir(exist_ok=True)
+    obj = BUILD / "torch_ops.o"
+    cxx = os.environ.get("CXX", "g++")
+    _run(
+        [
+            cxx,
+            "-O2",
+            "-fPIC",
+            "-std=c++17",
+            "-Wall",
+            "-Wno-unused-parameter",
+            f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            "-D__HIP_PLATFORM_AMD__=1",
+            "-DUSE_ROCM=1",
+            *[f"-I{p}" for p in incs],
+            f"-I{ROCM / 'include'}",
+            f"-I{INCLUDE}",
+            "-c",
+            str(CSRC / "torch_ops.cpp"),
+            "-o",
+            str(obj),
+        ]
+    )
+    tmp = OPS_LIB.with_suffix(".so.tmp")
+    _run(
+        [
+            cxx,
+            "-shared",
+            "-fPIC",
+            str(obj),
+            "-o",
+            str(tmp),
+            f"-L{PKG}",
+            "-lkohakutt_amd",
+            f"-L{libdir}",
+            "-ltorch",
+            "-ltorch_cpu",
+            "-ltorch_hip",
+            "-lc10",
+            "-lc10_hip",
+            f"-L{ROCM / 'lib'}",
+            "-lamdhip64",
+            "-Wl,-z,defs",
+            "-Wl,-rpath,$ORIGIN",
+            f"-Wl,-rpath,{libdir}",
+            f"-Wl,-rpath,{ROCM / 'lib'}",
+        ]
+    )
+    os.replace(tmp, OPS_LIB)
+    return OPS_LIB
+
+
+def build_all() -> None:
+    build_capi()
+    build_torch_ops()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(f"built {CAPI_LIB} and {OPS_LIB}", file=sys.stderr)

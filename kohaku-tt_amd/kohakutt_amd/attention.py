@@ -1,0 +1,179 @@
+"""Attention entry points beyond torch's own (the reference's ``kohakutt.sdpa`` and
+``kohakutt.sdpa_varlen``, ``src/kohakutt/attention.py:10-76``), and the GPU kernel of
+``torch_attn::_varlen_attn`` (``torch.nn.attention.varlen.varlen_attn``), which the
+reference registers for its device in ``src/kohakutt/torch_backend/varlen.py:62-104,
+247-252``."""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+_MASKED_LOGIT = -5e5
+
+
+def sdpa(q, k, v, key_lengths=None, is_causal=False, scale=None):
+    """``F.scaled_dot_product_attention`` of q [B, H, Sq, D], k / v [B, Hk, Sk, D] with
+    the key mask ``key < key_lengths[b]`` (B ints in [1, Sk]: a list, CPU or GPU tensor),
+    as the reference's ``kohakutt.sdpa`` (``attention.py:10-23``).  The lengths become a
+    [B, 1, 1, Sk] bool padding mask (with causal, a [B, 1, Sq, Sk] mask that also holds
+    the top-left causal rule)."""
+    gqa = q.size(1) != k.size(1)
+    if key_lengths is None:
+        return F.scaled_dot_product_attention(
+            q, k, v, is_causal=is_causal, scale=scale, enable_gqa=gqa
+        )
+    b, sq, sk = q.size(0), q.size(2), k.size(2)
+    lengths = torch.as_tensor(key_lengths, device=q.device).reshape(b, 1, 1, 1)
+    mask = torch.arange(sk, device=q.device).reshape(1, 1, 1, sk) < lengths
+    if is_causal:
+        rows = torch.arange(sq, device=q.device).reshape(1, 1, sq, 1)
+        mask = mask & (torch.arange(sk, device=q.device).reshape(1, 1, 1, sk) <= rows)
+    return F.scaled_dot_product_attention(
+        q, k, v, attn_mask=mask, scale=scale, enable_gqa=gqa
+    )
+
+
+def offsets(cu_seq):
+    """Cumulative offsets as a tuple of host ints (a list, or a CPU or GPU int tensor; a
+    GPU tensor is downloaded)."""
+    if isinstance(cu_seq, torch.Tensor):
+        return tuple(int(x) for x in cu_seq.detach().cpu().tolist())
+    return tuple(int(x) for x in cu_seq)
+
+
+def check_offsets(cu_q, cu_k, causal, total_q=None, total_k=None):
+    """Validates host offsets with the reference's rules and messages
+    (``ktt_flash/varlen_plan.hpp:43-82``); returns the per-sequence (Lq, Lk)."""
+    if len(cu_q) < 2 or len(cu_q) != len(cu_k) or cu_q[0] != 0 or cu_k[0] != 0:
+        raise ValueError(
+            "kohakutt_amd: sdpa_varlen needs cumulative offsets [0, ..., total] of equal "
+            "count for queries and keys"
+        )
+    lengths = []
+    for b in range(len(cu_q) - 1):
+        lq, lk = cu_q[b + 1] - cu_q[b], cu_k[b + 1] - cu_k[b]
+        if lq < 0 or lk < 0 or (lq > 0 and lk == 0):
+            raise ValueError(
+                "kohakutt_amd: sdpa_varlen offsets must not decrease, and a sequence with "
+                "queries needs keys"
+            )
+        if causal and lq > lk:
+            raise ValueError(
+                "kohakutt_amd: causal sdpa_varlen with more queries than keys in a "
+                "sequence leaves queries without keys"
+            )
+        lengths.append((lq, lk))
+    if total_q is not None and cu_q[-1] != total_q:
+        raise ValueError(f"kohakutt_amd: cu_seq_q must end at the {total_q} packed queries")
+    if total_k is not None and cu_k[-1] != total_k:
+        raise ValueError(f"kohakutt_amd: cu_seq_k must end at the {total_k} packed keys")
+    return lengths
+
+
+def _host(cu):
+    return not isinstance(cu, torch.Tensor) or not cu.is_cuda
+
+
+def sdpa_varlen(
+    q,
+    k,
+    v,
+    cu_seq_q,
+    cu_seq_k=None,
+    max_q=None,
+    max_k=None,
+    is_causal=False,
+    scale=None,
+    attn_mask=None,
+    packed_mask=None,
+):
+    """Scaled dot-product attention over packed variable-length sequences (the
+    reference's ``kohakutt.sdpa_varlen``, ``attention.py:26-76``).
+
+    q [Tq, H, D], k [Tk, Hkv, D], v [Tk, Hkv, D] (bf16 / fp16; fp32 is cast to bf16)
+    hold every sequence's tokens back to back.  ``cu_seq_q`` / ``cu_seq_k`` are the
+    cumulative offsets [0, ..., total] (a list or an int tensor; ``cu_seq_k`` defaults to
+    ``cu_seq_q``).  Each query attends to the keys of its own sequence; with
+    ``is_causal``, query r of a sequence sees its first min(Lk, r + 1 + Lk - Lq) keys.
+    Returns [Tq, H, D].
+
+    ``attn_mask``: a key mask [Tk] (bool: True keeps the key; float: added to its
+    logits, clamped at -5e5), as the reference takes it.
+    ``packed_mask``: this build's per-row mask -- every sequence's row-major
+    [Lq_i, Lk_i] block concatenated (bool or additive, shared by the heads), usable
+    together with ``is_causal``.
+
+    Host offsets (lists, CPU tensors) are validated with the reference's errors; GPU
+    offsets are trusted (the kernels clamp them into the packed token ranges)."""
+    cu_k_in = cu_seq_q if cu_seq_k is None else cu_seq_k
+    if _host(cu_seq_q) and _host(cu_k_in):
+        cu_q, cu_k = offsets(cu_seq_q), offsets(cu_k_in)
+        lengths = check_offsets(cu_q, cu_k, is_causal, q.size(0), k.size(0))
+        if max_q is None:
+            max_q = max((a for a, _ in lengths), default=0)
+        if max_k is None:
+            max_k = max((b for _, b in lengths), default=0)
+        cu_q_t = torch.tensor(cu_q, dtype=torch.int32, device=q.device)
+        cu_k_t = torch.tensor(cu_k, dtype=torch.int32, device=q.device)
+    else:
+        cu_q_t = torch.as_tensor(cu_seq_q, device=q.device).to(torch.int32)
+        cu_k_t = torch.as_tensor(cu_k_in, device=q.device).to(torch.int32)
+        if max_q is None:
+            max_q = int((cu_q_t[1:] - cu_q_t[:-1]).max().item())
+        if max_k is None:
+            max_k = int((cu_k_t[1:] - cu_k_t[:-1]).max().item())
+    if attn_mask is not None and packed_mask is not None:
+        raise ValueError("kohakutt_amd: sdpa_varlen takes attn_mask or packed_mask, not both")
+    if attn_mask is not None and (attn_mask.dim() != 1 or attn_mask.size(0) != k.size(0)):
+        raise ValueError(
+            f"kohakutt_amd.sdpa_varlen: attn_mask must be [{k.size(0)}] (one value per "
+            f"packed key), got {tuple(attn_mask.shape)}"
+        )
+    out, _ = torch.ops.ktt._sdpa_varlen(
+        q,
+        k,
+        v,
+        cu_q_t,
+        cu_k_t,
+        int(max_q),
+        int(max_k),
+        bool(is_causal),
+        None if scale is None else float(scale),
+        attn_mask,
+        packed_mask,
+    )
+    return out
+
+
+def _varlen_attn_gpu(query, key, value, cu_seq_q, cu_seq_k, max_q, max_k, is_causal=False):
+    """torch_attn::_varlen_attn on GPU tensors: (output [Tq, H, D], log-sum-exp [H, Tq],
+    rng state), as the reference's ``varlen._forward`` (``varlen.py:62-104``)."""
+    out, lse = torch.ops.ktt._sdpa_varlen(
+        query,
+        key,
+        value,
+        cu_seq_q,
+        cu_seq_k,
+        int(max_q),
+        int(max_k),
+        bool(is_causal),
+        None,
+        None,
+        None,
+    )
+    return out, lse, torch.zeros((2,), dtype=torch.uint64, device=query.device)
+
+
+def install_varlen_kernel() -> bool:
+    """Registers the GPU kernel of ``torch_attn::_varlen_attn`` when this torch has the
+    op (``torch.nn.attention.varlen``); returns whether it did."""
+    try:
+        from torch.nn.attention import varlen as _tv  # noqa: F401
+    except ImportError:
+        return False
+    op = getattr(torch.ops.torch_attn, "_varlen_attn", None)
+    if op is None:
+        return False
+    torch.library.register_kernel("torch_attn::_varlen_attn", "cuda", _varlen_attn_gpu)
+    return True

@@ -1,0 +1,122 @@
+"""The C ABI library (include/kohakutt_amd.h) on the CPU: it loads, exports every
+function the header declares, and rejects malformed calls on the host -- before any
+launch -- with a status and a kmi_last_error message (the reference's C ABI error model,
+ktt_capi.h / capi.cpp:19,58-79).  No call here reaches a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kohakutt_amd import capi
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "kohakutt_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kmi_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_exports():
+    assert _declared() == sorted(capi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define KMI_ABI_VERSION (\d+)", HEADER.read_text())
+    assert capi.lib().kmi_abi_version() == int(m.group(1))
+
+
+def test_struct_layout_matches_header_field_order():
+    text = HEADER.read_text()
+    start = text.index("{", text.index("typedef struct kmi_attn_args")) + 1
+    body = text[start : text.index("} kmi_attn_args;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = []
+    for decl in body.split(";"):
+        for part in decl.split(","):
+            idents = re.findall(r"[A-Za-z_]\w*", re.sub(r"\[.*?\]", "", part))
+            if idents:
+                names.append(idents[-1])
+    assert names == [f[0] for f in capi.AttnArgs._fields_]
+
+
+def _args(**kw):
+    a = capi.AttnArgs()
+    a.q = a.k = a.v = a.out = 0x1000
+    a.dtype = capi.KMI_BF16
+    a.batch, a.heads_q, a.heads_kv, a.seq_q, a.seq_k, a.head_dim = 1, 4, 2, 8, 8, 64
+    for f in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        getattr(a, f)[:] = [4 * 8 * 64, 8 * 64, 64]
+    a.scale = 0.125
+    for k_, v_ in kw.items():
+        setattr(a, k_, v_)
+    return a
+
+
+@pytest.mark.parametrize(
+    "kw,msg",
+    [
+        (dict(head_dim=80), "head_dim must be 64 or 128"),
+        (dict(dtype=capi.KMI_F32), "dtype must be BF16 or F16"),
+        (dict(heads_kv=3), "heads_kv must divide heads_q"),
+        (dict(q=0), "null q"),
+        (dict(q=0x1008), "16-byte aligned"),
+        (dict(seq_k=0), "sizes must be positive"),
+        (dict(mask_mode=capi.KMI_MASK_STRIDED), "mask_mode set without a mask"),
+        (dict(mask_mode=capi.KMI_MASK_PACKED, mask=0x2000, mask_dtype=capi.KMI_BOOL), "varlen only"),
+        (dict(cu_seqlens_q=0x3000), "go together"),
+    ],
+)
+def test_attention_rejects_malformed_calls(kw, msg):
+    a = _args(**kw)
+    status = capi.lib().kmi_attn_fwd(ctypes.byref(a), None, 0, None)
+    assert status == capi.KMI_EINVAL
+    assert msg in capi.lib().kmi_last_error().decode()
+    with pytest.raises(capi.KmiError, match=msg):
+        capi.workspace_bytes(a)
+
+
+def test_workspace_sizes_follow_the_split_plan():
+    # decode-shaped: split-KV partials (fp32 O and lse per split)
+    a = _args(batch=8, heads_q=16, heads_kv=2, seq_q=1, seq_k=4096, head_dim=128)
+    n = capi.workspace_bytes(a)
+    assert n > 0 and n % (16 * 8 * 129 * 4) == 0
+    # prefill-shaped: no split
+    b = _args(batch=1, heads_q=14, heads_kv=2, seq_q=2048, seq_k=2048)
+    assert capi.workspace_bytes(b) == 0
+
+
+def test_missing_workspace_is_refused_before_launch():
+    a = _args(batch=8, heads_q=16, heads_kv=2, seq_q=1, seq_k=4096, head_dim=128)
+    status = capi.lib().kmi_attn_fwd(ctypes.byref(a), None, 0, None)
+    assert status == capi.KMI_EWORKSPACE
+    assert "workspace" in capi.lib().kmi_last_error().decode()
+
+
+def test_empty_query_is_a_no_op():
+    a = _args(seq_q=0)
+    assert capi.lib().kmi_attn_fwd(ctypes.byref(a), None, 0, None) == capi.KMI_OK
+
+
+def test_norms_reject_malformed_calls():
+    lib = capi.lib()
+    assert lib.kmi_rms_norm_fwd(0x1000, None, None, 0x2000, None, 4, 64, 9, 0, 0, 1e-6, None) == capi.KMI_EINVAL
+    assert "x dtype" in lib.kmi_last_error().decode()
+    assert lib.kmi_layer_norm_fwd(None, None, None, None, None, None, 4, 64, capi.KMI_BF16, 0, 0, 1e-5,
+                                  None) == capi.KMI_EINVAL
+    assert "null x or y" in lib.kmi_last_error().decode()
+    assert lib.kmi_layer_norm_fwd(0x1000, 0x3000, None, 0x2000, None, None, 4, 64, capi.KMI_BF16, 7, 0, 1e-5,
+                                  None) == capi.KMI_EINVAL
+    # zero rows: nothing to do, nothing launched
+    assert lib.kmi_rms_norm_fwd(None, None, None, None, None, 0, 64, capi.KMI_BF16, 0, 0, 1e-6, None) == capi.KMI_OK

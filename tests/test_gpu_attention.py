@@ -1,0 +1,318 @@
+"""GPU parity of the attention kernels against the float64 CPU oracle, with the
+reference's ruler: median relative error no worse than 1.5x torch CPU at the same dtype
+(``tests/hardware/ops/test_flash.py:15,56-145`` bound the same ratio by rel RMS).
+
+Every call goes through the torch op surface (F.scaled_dot_product_attention,
+torch.nn.attention.varlen.varlen_attn, kohakutt_amd.sdpa_varlen), which calls the C ABI;
+``counters()`` proves the kernels ran rather than a torch fallback."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import attn_cases as C
+from oracle import attention as oatt
+
+pytestmark = pytest.mark.gpu
+
+
+def _ran(native, n=1):
+    c = native.counters()
+    assert c["attention"] == n, c
+
+
+def _check(gpu, cpu, ref, what, factor=1.5):
+    ok, sg, sc = C.ruler_ok(gpu, cpu, torch.from_numpy(np.ascontiguousarray(ref)), factor)
+    print(f"{what}: gpu rel_median {sg['rel_median']:.3e} cpu {sc['rel_median']:.3e}", flush=True)
+    assert ok, (what, sg, sc)
+
+
+def _dense_case(native, dev, q, k, v, mask=None, causal=False, scale=None, rows=None):
+    native.reset_counters()
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    md = mask.to(dev) if mask is not None else None
+    out = F.scaled_dot_product_attention(
+        qd, kd, vd, attn_mask=md, is_causal=causal, scale=scale, enable_gqa=q.size(1) != k.size(1)
+    )
+    torch.cuda.synchronize()
+    _ran(native)
+    out = out.cpu()
+    if rows is not None:
+        q = q[:, :, rows]
+        out = out[:, :, rows]
+        if mask is not None and mask.size(-2) > 1:
+            mask = mask[..., rows, :]
+    m64 = None if mask is None else (mask.numpy() if mask.dtype == torch.bool else C.f64(mask))
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), m64, causal, scale)
+    cpu = C.torch_cpu_sdpa(q, k, v, mask, causal, scale)
+    return out, cpu, ref
+
+
+@pytest.mark.parametrize(
+    "b,hq,hk,sq,sk,d,causal",
+    [
+        (1, 4, 4, 64, 64, 64, False),
+        (2, 3, 3, 37, 37, 64, False),
+        (1, 4, 2, 70, 70, 64, True),
+        (1, 6, 1, 130, 130, 128, True),  # MQA
+        (2, 8, 2, 33, 300, 128, False),
+        (1, 4, 4, 40, 100, 64, True),  # causal Sq < Sk: top-left
+        (1, 4, 2, 100, 40, 64, True),  # causal Sq > Sk: rows past Sk see every key
+        (1, 2, 2, 1, 513, 64, False),
+        (3, 16, 2, 1, 1000, 128, False),  # decode-shaped, split-KV
+    ],
+)
+def test_dense_shapes(native, dev, b, hq, hk, sq, sk, d, causal):
+    g = C.gen(b * 1000 + sq * 7 + sk)
+    q = C.randn(g, b, hq, sq, d)
+    k = C.randn(g, b, hk, sk, d)
+    v = C.randn(g, b, hk, sk, d)
+    out, cpu, ref = _dense_case(native, dev, q, k, v, causal=causal)
+    _check(out, cpu, ref, f"dense {b}x{hq}/{hk}x{sq}x{sk}x{d} causal={causal}")
+
+
+def test_fp16_and_scale(native, dev):
+    g = C.gen(5)
+    q = C.randn(g, 2, 4, 90, 64, dtype=torch.float16)
+    k = C.randn(g, 2, 2, 90, 64, dtype=torch.float16)
+    v = C.randn(g, 2, 2, 90, 64, dtype=torch.float16)
+    out, cpu, ref = _dense_case(native, dev, q, k, v, causal=True, scale=0.3)
+    _check(out, cpu, ref, "fp16 scale 0.3")
+
+
+def test_fp32_inputs_cast_like_reference(native, dev):
+    g = C.gen(6)
+    q = torch.randn(1, 4, 50, 64, generator=g)
+    k = torch.randn(1, 4, 50, 64, generator=g)
+    v = torch.randn(1, 4, 50, 64, generator=g)
+    native.reset_counters()
+    out = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev)).cpu()
+    _ran(native)
+    assert out.dtype == torch.float32
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v))
+    cpu = C.torch_cpu_sdpa(q.bfloat16(), k.bfloat16(), v.bfloat16()).float()
+    _check(out, cpu, ref, "fp32 cast to bf16")
+
+
+@pytest.mark.parametrize("mask_kind", ["bool_key", "bool_full", "add_bf16", "add_f32_bcast_heads"])
+def test_masks(native, dev, mask_kind):
+    g = C.gen(11)
+    b, h, s, d = 2, 4, 96, 64
+    q = C.randn(g, b, h, s, d)
+    k = C.randn(g, b, 2, s, d)
+    v = C.randn(g, b, 2, s, d)
+    if mask_kind == "bool_key":
+        lengths = torch.tensor([17, 96])
+        mask = (torch.arange(s)[None, :] < lengths[:, None]).reshape(b, 1, 1, s)
+    elif mask_kind == "bool_full":
+        mask = torch.rand(b, h, s, s, generator=g) > 0.3
+        mask[..., 0] = True
+    elif mask_kind == "add_bf16":
+        mask = (torch.randn(b, h, s, s, generator=g)).bfloat16()
+    else:
+        mask = torch.randn(b, 1, s, s, generator=g).masked_fill(torch.rand(b, 1, s, s, generator=g) < 0.2, float("-inf"))
+        mask[..., 0] = 0.0
+    out, cpu, ref = _dense_case(native, dev, q, k, v, mask=mask)
+    _check(out, cpu, ref, f"mask {mask_kind}")
+
+
+def test_fully_masked_row_is_softmax_of_raw_scores(native, dev):
+    """Decision D1: as the reference, a row whose every key is masked attends over its
+    raw scores (the clamp to -5e5 leaves their differences); torch CPU gives zeros."""
+    g = C.gen(12)
+    q = C.randn(g, 1, 2, 64, 64)
+    k = C.randn(g, 1, 2, 80, 64)
+    v = C.randn(g, 1, 2, 80, 64)
+    mask = torch.zeros(1, 1, 64, 80)
+    mask[..., 3, :] = float("-inf")
+    mask[..., 9, ::2] = float("-inf")
+    native.reset_counters()
+    out = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev), attn_mask=mask.to(dev)).cpu()
+    _ran(native)
+    unmasked, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v))
+    got = out[0, :, 3].double().numpy()
+    assert np.isfinite(got).all()
+    assert np.abs(got - unmasked[0, :, 3]).max() < 2e-2
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), mask.numpy())
+    assert np.abs(out.double().numpy() - ref).max() < 2e-2
+
+
+def test_large_logits_masked_keys_contribute_nothing(native, dev):
+    """Masked keys whose logits dwarf the kept ones still get exactly zero weight
+    (test_flash.py:120-145 pins this up to logits of 1e5)."""
+    g = C.gen(13)
+    d = 64
+    q = C.randn(g, 1, 1, 32, d)
+    k = C.randn(g, 1, 1, 128, d)
+    v = C.randn(g, 1, 1, 128, d)
+    k[..., 64:, :] = (q[0, 0].float().mean(0) * 2000).bfloat16()  # huge scores on masked keys
+    keep = torch.zeros(1, 1, 1, 128, dtype=torch.bool)
+    keep[..., :64] = True
+    native.reset_counters()
+    out = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev), attn_mask=keep.to(dev)).cpu()
+    _ran(native)
+    ref, _ = oatt.sdpa(C.f64(q[..., :, :]), C.f64(k[..., :64, :]), C.f64(v[..., :64, :]))
+    assert np.abs(out.double().numpy() - ref).max() < 2e-2
+
+
+def test_split_kv_matches_single_pass(native, dev):
+    """Decode shapes split the keys across workgroups; the merged result matches the
+    oracle and the per-(batch, head) rows stay isolated."""
+    g = C.gen(14)
+    q = C.randn(g, 4, 8, 1, 128)
+    k = C.randn(g, 4, 1, 3000, 128)
+    v = C.randn(g, 4, 1, 3000, 128)
+    out, cpu, ref = _dense_case(native, dev, q, k, v)
+    _check(out, cpu, ref, "split-KV MQA decode")
+    # isolation: changing batch 1 leaves batch 0 bit-identical
+    k2 = k.clone()
+    k2[1] = -k2[1]
+    out2 = F.scaled_dot_product_attention(q.to(dev), k2.to(dev), v.to(dev), enable_gqa=True).cpu()
+    assert torch.equal(out2[0], out[0]) and torch.equal(out2[2:], out[2:])
+
+
+def test_repeat_calls_bit_identical(native, dev):
+    cfg = C.config1()
+    q, k, v = cfg["q"].to(dev), cfg["k"].to(dev), cfg["v"].to(dev)
+    a = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+    b = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+    assert torch.equal(a, b)
+
+
+def test_config1_causal_gqa_prefill(native, dev):
+    cfg = C.config1()
+    out, cpu, ref = _dense_case(native, dev, cfg["q"], cfg["k"], cfg["v"], causal=True)
+    _check(out, cpu, ref, "C1 causal GQA 1x14/2x2048x64")
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_config2_vit(native, dev, batch):
+    cfg = C.config2(batch)
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    if batch > 4:
+        native.reset_counters()
+        full = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev)).cpu()
+        _ran(native)
+        q, k, v, full = q[:4], k[:4], v[:4], full[:4]
+        ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v))
+        _check(full, C.torch_cpu_sdpa(q, k, v), ref, f"C2 ViT B={batch} (first 4)")
+    else:
+        out, cpu, ref = _dense_case(native, dev, q, k, v)
+        _check(out, cpu, ref, "C2 ViT B=1")
+
+
+def test_config3_decode_padding_mask(native, dev):
+    cfg = C.config3()
+    out, cpu, ref = _dense_case(native, dev, cfg["q"], cfg["k"], cfg["v"], mask=cfg["mask"])
+    _check(out, cpu, ref, "C3 decode 8x16/2x4096x128 bool mask")
+
+
+def test_config5_self_and_cross(native, dev):
+    cfg = C.config5()
+    rows = torch.arange(0, 4096, 16)
+    out, cpu, ref = _dense_case(native, dev, cfg["q"], cfg["k"], cfg["v"], rows=rows)
+    _check(out, cpu, ref, "C5 self 2x10x4096x64 (every 16th row)")
+    out, cpu, ref = _dense_case(native, dev, cfg["q"], cfg["ck"], cfg["cv"])
+    _check(out, cpu, ref, "C5 cross 4096q x 77kv")
+
+
+# ---------------------------------------------------------------- varlen
+
+
+def _varlen_cpu_bf16(q, k, v, cu, causal):
+    """torch CPU SDPA per sequence at the inputs' dtype (the reference's CPU plan for
+    config 4), bottom-right causal as an explicit mask."""
+    outs = []
+    g = q.size(1) // k.size(1)
+    for a, b in zip(cu[:-1], cu[1:]):
+        qs = q[a:b].transpose(0, 1)[None]
+        ks = k[a:b].transpose(0, 1)[None].repeat_interleave(g, 1)
+        vs = v[a:b].transpose(0, 1)[None].repeat_interleave(g, 1)
+        mask = None
+        if causal:
+            n = b - a
+            mask = torch.ones(n, n, dtype=torch.bool).tril()
+        outs.append(F.scaled_dot_product_attention(qs, ks, vs, attn_mask=mask)[0].transpose(0, 1))
+    return torch.cat(outs)
+
+
+def test_config4_varlen_causal(native, dev):
+    from torch.nn.attention.varlen import varlen_attn
+
+    cfg = C.config4()
+    cu = cfg["cu"]
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    native.reset_counters()
+    mx = max(cfg["lengths"])
+    out = varlen_attn(q.to(dev), k.to(dev), v.to(dev), cu_t, cu_t, mx, mx, is_causal=True).cpu()
+    _ran(native)
+    ref, _ = oatt.sdpa_varlen(C.f64(q), C.f64(k), C.f64(v), cu, is_causal=True)
+    _check(out, _varlen_cpu_bf16(q, k, v, cu, True), ref, "C4 varlen causal (varlen_attn)")
+    native.reset_counters()
+    out2 = native.sdpa_varlen(q.to(dev), k.to(dev), v.to(dev), cu, is_causal=True).cpu()
+    _ran(native)
+    assert torch.equal(out, out2)
+
+
+def test_config4_varlen_packed_mask(native, dev):
+    cfg = C.config4()
+    cu = cfg["cu"]
+    q, k, v, pm = cfg["q"], cfg["k"], cfg["v"], cfg["packed_mask"]
+    native.reset_counters()
+    out = native.sdpa_varlen(q.to(dev), k.to(dev), v.to(dev), cu, is_causal=True, packed_mask=pm.to(dev)).cpu()
+    _ran(native)
+    ref, _ = oatt.sdpa_varlen(C.f64(q), C.f64(k), C.f64(v), cu, is_causal=True, attn_mask=pm.numpy())
+    # CPU bf16 per sequence with the same additive mask (fully-masked row excluded: torch
+    # CPU zeroes it, the reference attends over raw scores).
+    outs, off = [], 0
+    for a, b in zip(cu[:-1], cu[1:]):
+        n = b - a
+        m = pm[off : off + n * n].reshape(1, 1, n, n).bfloat16()
+        off += n * n
+        qs = q[a:b].transpose(0, 1)[None]
+        ks = k[a:b].transpose(0, 1)[None].repeat_interleave(2, 1)
+        vs = v[a:b].transpose(0, 1)[None].repeat_interleave(2, 1)
+        outs.append(F.scaled_dot_product_attention(qs, ks, vs, attn_mask=m)[0].transpose(0, 1))
+    cpu = torch.cat(outs)
+    keep = torch.ones(q.size(0), dtype=torch.bool)
+    keep[5] = False
+    _check(out[keep], cpu[keep], ref[keep.numpy()], "C4 varlen masked run")
+    assert np.abs(out[5].double().numpy() - ref[5]).max() < 2e-2
+
+
+def test_varlen_key_mask_and_neighbour_independence(native, dev):
+    g = C.gen(21)
+    cu = [0, 40, 41, 170, 300]
+    t = cu[-1]
+    q = C.randn(g, t, 4, 64)
+    k = C.randn(g, t, 2, 64)
+    v = C.randn(g, t, 2, 64)
+    km = torch.rand(t, generator=g) > 0.2
+    for a in cu[:-1]:
+        km[a] = True
+    out = native.sdpa_varlen(q.to(dev), k.to(dev), v.to(dev), cu, attn_mask=km.to(dev)).cpu()
+    ref, _ = oatt.sdpa_varlen(C.f64(q), C.f64(k), C.f64(v), cu, key_mask=km.numpy())
+    assert np.abs(out.double().numpy() - ref).max() < 2e-2
+    # a sequence's output does not depend on its neighbours' tokens
+    q2, k2, v2 = q.clone(), k.clone(), v.clone()
+    q2[:40] = 0
+    k2[170:] = 1
+    v2[41:170] = -v2[41:170]
+    out2 = native.sdpa_varlen(q2.to(dev), k2.to(dev), v2.to(dev), cu, attn_mask=km.to(dev)).cpu()
+    assert torch.equal(out[40:41], out2[40:41])
+
+
+def test_varlen_cross_lengths_bottom_right(native, dev):
+    g = C.gen(22)
+    cu_q = [0, 10, 30, 31]
+    cu_k = [0, 50, 70, 200]
+    q = C.randn(g, 31, 8, 128)
+    k = C.randn(g, 200, 2, 128)
+    v = C.randn(g, 200, 2, 128)
+    out = native.sdpa_varlen(q.to(dev), k.to(dev), v.to(dev), cu_q, cu_k, is_causal=True).cpu()
+    ref, _ = oatt.sdpa_varlen(C.f64(q), C.f64(k), C.f64(v), cu_q, cu_k, is_causal=True)
+    assert np.abs(out.double().numpy() - ref).max() < 2e-2

@@ -1,0 +1,134 @@
+"""GPU parity of LayerNorm / RMSNorm against float64, with the reference's bar
+(``tests/hardware/ops/test_norm.py:25-38,95-113``): relative RMS error of y no worse than
+1.02x torch CPU at the same dtype (plus a 2e-6 floor for fp32), fp32 statistics within
+1e-6 relative of float64, repeat calls bit-identical (``test_norm.py:186-192``)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import attn_cases as C
+from oracle import norms as onorm
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 33), (5, 70), (32, 64), (77, 1000), (2, 40, 4096), (3, 16384), (4096, 768), (65536, 64),
+          (300, 4097), (2, 3, 50, 1280)]
+SLACK = 1.02
+
+
+def _rel(a, ref):
+    a = torch.as_tensor(a).double().flatten()
+    ref = torch.as_tensor(ref).double().flatten()
+    return ((a - ref).norm() / ref.norm().clamp_min(1e-300)).item()
+
+
+def _check(name, gpu, cpu, ref, dtype):
+    assert torch.isfinite(gpu).all(), name
+    t, c = _rel(gpu, ref), _rel(cpu, ref)
+    floor = 2e-6 if dtype == torch.float32 else 0.0
+    print(f"{name}: gpu {t:.3e} cpu {c:.3e}", flush=True)
+    assert t <= SLACK * c + floor, (name, t, c)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("affine", [True, False])
+def test_layer_norm(native, dev, shape, dtype, affine):
+    g = C.gen(hash((shape, affine)) % 10000)
+    x = (torch.randn(*shape, generator=g) * 3 + 0.5).to(dtype)
+    w = (1 + 0.1 * torch.randn(shape[-1], generator=g)).to(dtype) if affine else None
+    b = (0.1 * torch.randn(shape[-1], generator=g)).to(dtype) if affine else None
+    native.reset_counters()
+    y, mean, rstd = torch.ops.aten.native_layer_norm(
+        x.to(dev), [shape[-1]], None if w is None else w.to(dev), None if b is None else b.to(dev), 1e-5)
+    torch.cuda.synchronize()
+    assert native.counters()["norms"] == 1
+    assert mean.dtype == torch.float32 and rstd.dtype == torch.float32
+    yr, mr, rr = onorm.layer_norm(C.f64(x), None if w is None else C.f64(w), None if b is None else C.f64(b), 1e-5)
+    cpu = F.layer_norm(x, [shape[-1]], w, b, 1e-5)
+    _check(f"LN {shape} {dtype} affine={affine}", y.cpu(), cpu, torch.from_numpy(yr), dtype)
+    assert np.allclose(mean.cpu().double().numpy(), mr, rtol=1e-6, atol=1e-6 * np.abs(mr).max())
+    assert np.allclose(rstd.cpu().double().numpy(), rr, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_rms_norm(native, dev, shape, dtype):
+    g = C.gen(hash(shape) % 10000 + 7)
+    x = (torch.randn(*shape, generator=g) * 2).to(dtype)
+    w = (1 + 0.1 * torch.randn(shape[-1], generator=g)).to(dtype)
+    native.reset_counters()
+    y = F.rms_norm(x.to(dev), [shape[-1]], w.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert native.counters()["norms"] == 1
+    yr, _ = onorm.rms_norm(C.f64(x), C.f64(w), eps=1e-6)
+    # the CPU same-dtype reference: fp32 math, one rounding (as the kernels)
+    cpu = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()).to(dtype)
+    _check(f"RMS {shape} {dtype}", y.cpu(), cpu, torch.from_numpy(yr), dtype)
+
+
+def test_ktt_rms_norm_bias_and_stats(native, dev):
+    g = C.gen(31)
+    x = C.randn(g, 7, 896)
+    w = C.randn(g, 896)
+    b = C.randn(g, 896)
+    y = torch.ops.ktt.rms_norm(x.to(dev), w.to(dev), b.to(dev), 1e-6).cpu()
+    yr, _ = onorm.rms_norm(C.f64(x), C.f64(w), C.f64(b), eps=1e-6)
+    cpu = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float() + b.float()).bfloat16()
+    _check("ktt.rms_norm bias", y, cpu, torch.from_numpy(yr), torch.bfloat16)
+
+
+def test_rms_norm_backward_matches_float64(native, dev):
+    g = C.gen(32)
+    x = torch.randn(16, 256, generator=g, dtype=torch.float64)
+    w = 1 + 0.1 * torch.randn(256, generator=g, dtype=torch.float64)
+    gy = torch.randn(16, 256, generator=g, dtype=torch.float64)
+    xd = x.float().to(dev).requires_grad_()
+    wd = w.float().to(dev).requires_grad_()
+    F.rms_norm(xd, [256], wd, 1e-6).backward(gy.float().to(dev))
+    xr = x.clone().requires_grad_()
+    wr = w.clone().requires_grad_()
+    F.rms_norm(xr, [256], wr, 1e-6).backward(gy)
+    assert torch.allclose(xd.grad.cpu().double(), xr.grad, rtol=1e-4, atol=1e-5)
+    assert torch.allclose(wd.grad.cpu().double(), wr.grad, rtol=1e-4, atol=1e-4)
+
+
+def test_layer_norm_backward_uses_fp32_stats(native, dev):
+    g = C.gen(33)
+    x = torch.randn(8, 512, generator=g, dtype=torch.float64)
+    w = 1 + 0.1 * torch.randn(512, generator=g, dtype=torch.float64)
+    b = 0.1 * torch.randn(512, generator=g, dtype=torch.float64)
+    gy = torch.randn(8, 512, generator=g, dtype=torch.float64)
+    xd = x.float().to(dev).requires_grad_()
+    F.layer_norm(xd, [512], w.float().to(dev), b.float().to(dev), 1e-5).backward(gy.float().to(dev))
+    xr = x.clone().requires_grad_()
+    F.layer_norm(xr, [512], w, b, 1e-5).backward(gy)
+    assert torch.allclose(xd.grad.cpu().double(), xr.grad, rtol=1e-4, atol=1e-5)
+
+
+def test_norm_configs_and_repeat_bit_identical(native, dev):
+    c1, c2, c3, c5 = C.config1(), C.config2(), C.config3(), C.config5()
+    for name, x, w, b, eps, kind in [
+        ("C1 rms [1,2048,896]", c1["x"], c1["w"], None, 1e-6, "rms"),
+        ("C2 LN [1,197,768]", c2["x"], c2["w"], c2["b"], 1e-6, "ln"),
+        ("C3 rms [8,1,2048]", c3["x"], c3["w"], None, 1e-6, "rms"),
+        ("C5 LN [2,4096,640]", c5["x"], c5["w"], c5["b"], 1e-5, "ln"),
+    ]:
+        xd, wd = x.to(dev), w.to(dev)
+        W = x.size(-1)
+        if kind == "rms":
+            y = F.rms_norm(xd, [W], wd, eps)
+            y2 = F.rms_norm(xd, [W], wd, eps)
+            yr, _ = onorm.rms_norm(C.f64(x), C.f64(w), eps=eps)
+            cpu = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps) * w.float()).bfloat16()
+        else:
+            y = F.layer_norm(xd, [W], wd, b.to(dev), eps)
+            y2 = F.layer_norm(xd, [W], wd, b.to(dev), eps)
+            yr, _, _ = onorm.layer_norm(C.f64(x), C.f64(w), C.f64(b), eps)
+            cpu = F.layer_norm(x, [W], w, b, eps)
+        assert torch.equal(y, y2), name
+        _check(name, y.cpu(), cpu, torch.from_numpy(yr), torch.bfloat16)

@@ -1,0 +1,72 @@
+"""Host-side logic on the CPU: the package imports without a GPU, leaves CPU tensors to
+torch, validates varlen offsets with the reference's errors, and reports refusals."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import kohakutt_amd
+from kohakutt_amd import attention as katt
+from oracle import norms as N
+
+
+def test_cpu_tensors_keep_torch_paths():
+    kohakutt_amd.reset_counters()
+    q = torch.randn(1, 2, 8, 64)
+    out = F.scaled_dot_product_attention(q, q, q)
+    y = F.layer_norm(q, [64])
+    z = F.rms_norm(q, [64])
+    assert out.shape == q.shape and y.shape == q.shape and z.shape == q.shape
+    c = kohakutt_amd.counters()
+    assert c["attention"] == 0 and c["norms"] == 0
+
+
+def test_refusal_reasons():
+    q = torch.randn(1, 2, 8, 64, dtype=torch.bfloat16)
+    assert "GPU" in kohakutt_amd.sdpa_refusal(q, q, q)
+
+
+def test_ktt_rms_norm_composite_on_cpu():
+    x = torch.randn(3, 40, dtype=torch.float64)
+    w = torch.randn(40, dtype=torch.float64)
+    b = torch.randn(40, dtype=torch.float64)
+    y = kohakutt_amd.rms_norm(x, w, b, 1e-6)
+    yr, _ = N.rms_norm(x.numpy(), w.numpy(), b.numpy(), 1e-6)
+    assert np.abs(y.numpy() - yr).max() < 1e-6
+
+
+@pytest.mark.parametrize(
+    "cu_q,cu_k,causal,msg",
+    [
+        ([0], [0], False, "cumulative offsets"),
+        ([0, 3], [0, 3, 4], False, "cumulative offsets"),
+        ([0, 3, 2], [0, 3, 5], False, "must not decrease"),
+        ([0, 3], [0, 0], False, "needs keys"),
+        ([0, 5], [0, 4], True, "leaves queries without keys"),
+    ],
+)
+def test_varlen_offsets_validated_like_reference(cu_q, cu_k, causal, msg):
+    with pytest.raises(ValueError, match=msg):
+        katt.check_offsets(cu_q, cu_k, causal)
+
+
+def test_varlen_offsets_must_end_at_totals():
+    with pytest.raises(ValueError, match="must end"):
+        katt.check_offsets([0, 3, 5], [0, 3, 5], False, total_q=6, total_k=5)
+    assert katt.check_offsets([0, 3, 5], [0, 4, 9], True, 5, 9) == [(3, 4), (2, 5)]
+
+
+def test_set_enabled_round_trip():
+    kohakutt_amd.set_enabled(attention=False, norms=False)
+    c = kohakutt_amd.counters()
+    assert not c["attention_enabled"] and not c["norms_enabled"]
+    kohakutt_amd.set_enabled()
+    c = kohakutt_amd.counters()
+    assert c["attention_enabled"] and c["norms_enabled"]
+
+
+def test_varlen_kernel_registered_for_gpu():
+    assert katt.install_varlen_kernel()
