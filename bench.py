@@ -1,0 +1,434 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention + norm hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--rows a,b,...] [--no-cpu]
+
+Prints ONE JSON line on stdout.  The headline (``value``) is the BASELINE metric's named
+target: causal GQA prefill attention of config 1 (Qwen2.5-0.5B shape, B=1, S=2048,
+Hq=14, Hkv=2, D=64, bf16) in TFLOP/s of algorithmic work (4*D*Hq*S(S+1)/2 FLOPs per
+call).  ``rows`` carries every other config (norms, ViT, decode, varlen, SDXL) and
+labelled bandwidth sweeps, each with its roofline fraction.
+
+Timing (per row): inputs are synthetic (seeded CPU randn cast to bf16, then copied to
+HBM); K distinct input sets rotate through the K timed calls and a 512 MiB buffer is
+rewritten before each timed region, so every timed call reads its inputs from HBM, not
+the 256 MiB Infinity Cache.  ``ms_per_step`` is the per-call time of a HIP graph of the K
+calls replayed once (bracketed by synchronize); the kernel time behind ``roofline`` is
+the mean of per-call HIP event pairs recorded on the launch stream in eager mode.
+
+``cpu_baseline``: the reference's CPU path (torch CPU SDPA / norms at bf16) on the host
+cores of the same box, a bounded sample timed in the same process, rank 0 only.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for p in (REPO / "kohaku-tt_amd", REPO, REPO / "tests"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+FLUSH_BYTES = 512 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--rows", default="all", help="comma list of row names, or 'all'")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline timings")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="headline CPU sample length")
+    ap.add_argument("--profile-loop", type=int, default=0,
+                    help="only run the named rows' calls this many times (for rocprofv3)")
+    ap.add_argument("--calibrate-copy", type=int, default=0,
+                    help="only run a plain device copy of this many MiB, --steps times (for rocprofv3)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- rows
+
+class Row:
+    """One benchmark row: ``make(n)`` returns n call closures over distinct input sets
+    on the GPU and the CPU reference closure; ``work`` is FLOPs (mfma) or bytes (hbm)
+    per call; ``flops`` / ``bytes`` both when known."""
+
+    def __init__(self, name, label, bound, flops, nbytes, make, kernel):
+        self.name, self.label, self.bound = name, label, bound
+        self.flops, self.bytes = flops, nbytes
+        self.make, self.kernel = make, kernel
+
+
+def _rotate(dev, tensors, n):
+    """n independent device copies of the CPU tensors (the first is the upload)."""
+    import torch
+
+    first = [t.to(dev) if isinstance(t, torch.Tensor) else t for t in tensors]
+    sets = [first]
+    for _ in range(n - 1):
+        sets.append([t.clone() if isinstance(t, torch.Tensor) else t for t in first])
+    return sets
+
+
+def build_rows():
+    import torch
+    import torch.nn.functional as F
+
+    import attn_cases as C
+
+    rows = {}
+
+    def sdpa_row(name, label, bound, q, k, v, mask=None, causal=False, pairs=None):
+        b, hq, sq, d = q.shape
+        sk = k.size(2)
+        if pairs is None:
+            pairs = C.causal_pairs(b, sq) if causal else b * sq * sk
+        flops = C.attn_flops(d, hq, pairs)
+        nbytes = (q.numel() + k.numel() + v.numel() + q.numel()) * 2 + (0 if mask is None else mask.numel() * mask.element_size())
+        gqa = hq != k.size(1)
+
+        def make(dev, n):
+            sets = _rotate(dev, [q, k, v, mask], n)
+            return [
+                (lambda s=s: F.scaled_dot_product_attention(s[0], s[1], s[2], attn_mask=s[3], is_causal=causal,
+                                                            enable_gqa=gqa))
+                for s in sets
+            ]
+
+        def cpu():
+            kk, vv = k, v
+            if gqa:
+                kk, vv = k.repeat_interleave(hq // k.size(1), 1), v.repeat_interleave(hq // k.size(1), 1)
+            return lambda: F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask, is_causal=causal)
+
+        rows[name] = Row(name, label, bound, flops, nbytes, (make, cpu), "attn_fwd_kernel")
+
+    def norm_row(name, label, x, w, b, eps, kind):
+        rows_, width = x.numel() // x.size(-1), x.size(-1)
+        nbytes = 2 * x.numel() * x.element_size() + width * w.element_size() * (1 if b is None else 2)
+        nbytes += rows_ * 4 * (2 if kind == "ln" else 0)
+
+        def make(dev, n):
+            sets = _rotate(dev, [x, w, b], n)
+            if kind == "ln":
+                return [(lambda s=s: F.layer_norm(s[0], [width], s[1], s[2], eps)) for s in sets]
+            return [(lambda s=s: F.rms_norm(s[0], [width], s[1], eps)) for s in sets]
+
+        def cpu():
+            if kind == "ln":
+                return lambda: F.layer_norm(x, [width], w, b, eps)
+            return lambda: F.rms_norm(x, [width], w, eps)
+
+        rows[name] = Row(name, label, "hbm", None, nbytes, (make, cpu), "norm_rows_wave")
+
+    c1 = C.config1()
+    sdpa_row("c1_attn", "C1 causal GQA prefill 1x14/2x2048x64", "mfma", c1["q"], c1["k"], c1["v"], causal=True)
+    norm_row("c1_rms", "C1 rms_norm [1,2048,896]", c1["x"], c1["w"], None, 1e-6, "rms")
+
+    c2 = C.config2(1)
+    norm_row("c2_ln", "C2 layer_norm [1,197,768]", c2["x"], c2["w"], c2["b"], 1e-6, "ln")
+    sdpa_row("c2_attn_b1", "C2 ViT MHA 1x12x197x64", "hbm", c2["q"], c2["k"], c2["v"])
+    c2b = C.config2(32)
+    sdpa_row("c2_attn_b32", "C2 ViT MHA 32x12x197x64", "hbm", c2b["q"], c2b["k"], c2b["v"])
+
+    c3 = C.config3()
+    lens = c3["lengths"]
+    d3 = 128
+    dec_bytes = int(lens.sum()) * 2 * d3 * 2 * 2 + 2 * (8 * 16 * d3 * 2) + 8 * 4096
+    sdpa_row("c3_decode", "C3 decode 8x16/2x1x4096x128 bool mask", "hbm", c3["q"], c3["k"], c3["v"], mask=c3["mask"],
+             pairs=int(lens.sum()) * 1)
+    rows["c3_decode"].bytes = dec_bytes
+    rows["c3_decode"].flops = C.attn_flops(d3, 16, int(lens.sum()))
+    norm_row("c3_rms", "C3 rms_norm [8,1,2048]", c3["x"], c3["w"], None, 1e-6, "rms")
+
+    c4 = C.config4()
+    cu, L = c4["cu"], c4["lengths"]
+    pairs = sum(n * (n + 1) // 2 for n in L)
+    t = cu[-1]
+    v4_bytes = (t * 16 * 128 * 2) * 2 + (t * 8 * 128 * 2) * 2
+
+    def varlen_row(name, label, masked):
+        mask = c4["packed_mask"] if masked else None
+
+        def make(dev, n):
+            cu_t = torch.tensor(cu, dtype=torch.int32)
+            sets = _rotate(dev, [c4["q"], c4["k"], c4["v"], cu_t, mask], n)
+            mx = max(L)
+            return [
+                (lambda s=s: torch.ops.ktt._sdpa_varlen(s[0], s[1], s[2], s[3], s[3], mx, mx, True, None, None, s[4]))
+                for s in sets
+            ]
+
+        def cpu():
+            q, k, v = c4["q"], c4["k"], c4["v"]
+            m = c4["packed_mask"]
+
+            def run():
+                off = 0
+                for a, b in zip(cu[:-1], cu[1:]):
+                    n = b - a
+                    qs = q[a:b].transpose(0, 1)[None]
+                    ks = k[a:b].transpose(0, 1)[None].repeat_interleave(2, 1)
+                    vs = v[a:b].transpose(0, 1)[None].repeat_interleave(2, 1)
+                    if masked:
+                        mm = m[off: off + n * n].reshape(1, 1, n, n).bfloat16()
+                        off += n * n
+                        F.scaled_dot_product_attention(qs, ks, vs, attn_mask=mm)
+                    else:
+                        F.scaled_dot_product_attention(qs, ks, vs, is_causal=True)
+
+            return run
+
+        extra = 4 * sum(n * n for n in L) if masked else 0
+        rows[name] = Row(name, label, "mfma", C.attn_flops(128, 16, pairs), v4_bytes + extra, (make, cpu),
+                         "attn_fwd_kernel")
+
+    varlen_row("c4_varlen", f"C4 varlen causal GQA 8 seqs T={t} 16/8x128", False)
+    varlen_row("c4_varlen_masked", "C4 varlen causal + packed additive mask", True)
+
+    c5 = C.config5()
+    norm_row("c5_ln", "C5 layer_norm [2,4096,640]", c5["x"], c5["w"], c5["b"], 1e-5, "ln")
+    sdpa_row("c5_self", "C5 SDXL self 2x10x4096x64", "mfma", c5["q"], c5["k"], c5["v"])
+    sdpa_row("c5_cross", "C5 SDXL cross 2x10x4096q/77kv x64", "hbm", c5["q"], c5["ck"], c5["cv"])
+
+    # labelled bandwidth-saturating sweep rows (not BASELINE configs)
+    g = C.gen(2000)
+    xs = C.randn(g, 8192, 8192)
+    ws = (1 + 0.02 * torch.randn(8192, generator=g)).bfloat16()
+    bs = (0.02 * torch.randn(8192, generator=g)).bfloat16()
+    norm_row("sweep_rms_8192", "sweep: rms_norm [8192,8192]", xs, ws, None, 1e-6, "rms")
+    norm_row("sweep_ln_8192", "sweep: layer_norm [8192,8192]", xs, ws, bs, 1e-5, "ln")
+    qd = C.randn(g, 64, 16, 1, 128)
+    kd = C.randn(g, 64, 2, 8192, 128)
+    vd = C.randn(g, 64, 2, 8192, 128)
+    sdpa_row("sweep_decode", "sweep: decode 64x16/2x1x8192x128 (no mask)", "hbm", qd, kd, vd)
+    rows["sweep_decode"].bytes = (kd.numel() + vd.numel()) * 2 + 2 * qd.numel() * 2
+    return rows
+
+
+# ---------------------------------------------------------------- measurement
+
+def flush(buf):
+    buf.add_(1)
+
+
+def measure(row, dev, steps, warmup, flush_buf):
+    import torch
+
+    make, _ = row.make
+    n_sets = max(1, steps)
+    calls = make(dev, n_sets)
+    for i in range(warmup):
+        calls[i % n_sets]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    # kernel time: per-call event pairs on the launch stream (eager)
+    flush(flush_buf)
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        pairs[i][0].record(stream)
+        calls[i % n_sets]()
+        pairs[i][1].record(stream)
+    torch.cuda.synchronize()
+    kernel_ms = statistics.mean(a.elapsed_time(b) for a, b in pairs)
+    # eager wall per call
+    flush(flush_buf)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        calls[i % n_sets]()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    # graph of the K calls, replayed once
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        calls[0]()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            calls[i % n_sets]()
+    graph.replay()
+    torch.cuda.synchronize()
+    flush(flush_buf)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    graph_ms = e0.elapsed_time(e1) / steps
+    del graph, calls
+    torch.cuda.synchronize()
+    return kernel_ms, graph_ms, eager_ms
+
+
+def summarize(row, kernel_ms, graph_ms, eager_ms):
+    out = {"row": row.name, "label": row.label, "bound": row.bound, "ms_per_call": round(graph_ms, 5),
+           "kernel_ms": round(kernel_ms, 5), "eager_ms_per_call": round(eager_ms, 5)}
+    if row.flops:
+        out["gflop"] = round(row.flops / 1e9, 4)
+        out["tflops"] = round(row.flops / (graph_ms * 1e-3) / 1e12, 2)
+        out["frac_mfma"] = round(out["tflops"] / PEAK_TFLOPS, 4)
+    if row.bytes:
+        out["mbytes"] = round(row.bytes / 1e6, 3)
+        out["gbps"] = round(row.bytes / (graph_ms * 1e-3) / 1e9, 1)
+        out["frac_hbm"] = round(out["gbps"] / PEAK_GBPS, 4)
+    return out
+
+
+def cpu_time(fn, seconds, min_calls=5):
+    """Median seconds per call of fn over a bounded sample (>= min_calls, ~seconds)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_calls or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 10000:
+            break
+    return statistics.median(times), len(times)
+
+
+def traffic_for(row_name):
+    """HBM bytes per launch of the row's dominant kernel from the committed rocprofv3
+    counter summary (profiles/traffic.json), or None."""
+    p = REPO / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(row_name, {}).get("bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding of the path is a design note, not a measured configuration.",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    import kohakutt_amd
+
+    dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {args.calibrate_copy} MiB x {args.steps}")
+        return 0
+
+    rows = build_rows()
+    names = list(rows) if args.rows == "all" else [r.strip() for r in args.rows.split(",")]
+    if args.profile_loop:
+        for name in names:
+            calls = rows[name].make[0](dev, min(args.profile_loop, 16))
+            for i in range(args.profile_loop):
+                calls[i % len(calls)]()
+            torch.cuda.synchronize()
+            log(f"profiled {name} x {args.profile_loop}")
+        return 0
+
+    flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+    kohakutt_amd.reset_counters()
+    results = {}
+    for name in names:
+        row = rows[name]
+        km, gm, em = measure(row, dev, args.steps, args.warmup, flush_buf)
+        results[name] = summarize(row, km, gm, em)
+        log(json.dumps(results[name]))
+    counters = kohakutt_amd.counters()
+    assert counters["attention_declined"] == 0, counters
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cpu_rows = {}
+    if not args.no_cpu:
+        for name in names:
+            if name.startswith("sweep_"):
+                continue
+            row = rows[name]
+            secs = args.cpu_seconds if name == "c1_attn" else 1.0
+            med, n = cpu_time(row.make[1](), secs)
+            work = row.flops if row.bound == "mfma" and row.flops else row.bytes
+            unit_scale = 1e12 if row.bound == "mfma" and row.flops else 1e9
+            cpu_rows[name] = {"ms_per_call": round(med * 1e3, 4), "calls": n,
+                              ("tflops" if unit_scale == 1e12 else "gbps"): round(work / med / unit_scale, 4)}
+            results[name]["cpu_ms_per_call"] = cpu_rows[name]["ms_per_call"]
+            log(f"cpu {name}: {cpu_rows[name]}")
+
+    head = results.get("c1_attn")
+    if head is None:
+        print(json.dumps({"rows": list(results.values())}))
+        return 0
+    hrow = rows["c1_attn"]
+    achieved = hrow.flops / (head["kernel_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": "attn TFLOP/s (% bf16 MFMA peak) prefill; decode+norm HBM GB/s (% peak)",
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_call"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs cast to bf16, BASELINE config shapes)",
+        "config": {
+            "workload": "BASELINE configs[0] attention: causal GQA prefill, Qwen2.5-0.5B shape "
+                        "B=1 S=2048 Hq=14 Hkv=2 D=64, F.scaled_dot_product_attention(is_causal, enable_gqa)",
+            "batch": 1, "seq_len": 2048, "heads_q": 14, "heads_kv": 2, "head_dim": 64, "causal": True,
+            "timing": "HIP graph of K calls over K distinct HBM-resident input sets, MALL flushed",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": traffic_for("c1_attn"),
+            "kernel": "attn_fwd_kernel<bf16,64,*>",
+            "kernel_ms": head["kernel_ms"],
+        },
+        "cpu_baseline": None,
+        "rows": [r for k, r in results.items() if k != "c1_attn"],
+    }
+    if "c1_attn" in cpu_rows:
+        c = cpu_rows["c1_attn"]
+        line["cpu_baseline"] = {
+            "value": c["tflops"], "unit": "TFLOP/s", "cores": cores, "kind": "reference",
+            "sample": f"torch CPU bf16 F.scaled_dot_product_attention (the reference's CPU path) on the "
+                      f"C1 shape, {c['calls']} calls over ~{args.cpu_seconds:.0f} s, median "
+                      f"{c['ms_per_call']} ms/call, {cores} threads",
+        }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

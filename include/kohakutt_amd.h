@@ -98,6 +98,8 @@ typedef struct kmi_attn_args {
     int32_t mask_dtype;
     int32_t mask_mode;
     int64_t mask_stride[4];
+    /* KMI_MASK_PACKED: elements in the mask; reads past it count as masked. */
+    int64_t mask_numel;
     const int32_t* cu_seqlens_q;
     const int32_t* cu_seqlens_k;
     /* varlen: packed token counts Tq / Tk.  The kernels clamp every offset into

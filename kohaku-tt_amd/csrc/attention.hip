@@ -51,6 +51,7 @@ struct AttnParams {
     int64_t qs[3], ks[3], vs[3], os[3], ls[3];
     const void* mask;
     int64_t ms[4];
+    int64_t mask_numel;
     const int32_t* cu_q;
     const int32_t* cu_k;
     int mask_dtype, mask_mode;
@@ -315,8 +316,12 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                     for (int i = 0; i < 4; ++i) {
                         const int kk = key0 + 16 * kb + 4 * g4 + i;
                         float val = s[kb][b][i] * p.scale_log2;
-                        if (p.mask_mode != KMI_MASK_NONE && kk < lk)
-                            val += kLog2e * mask_logit(mptr, p.mask_dtype, mrow[b] + kk * m_key);
+                        if (p.mask_mode != KMI_MASK_NONE && kk < lk) {
+                            const int64_t mi = mrow[b] + kk * m_key;
+                            val += kLog2e * ((p.mask_mode == KMI_MASK_PACKED && mi >= p.mask_numel)
+                                                 ? kMaskedLogit
+                                                 : mask_logit(mptr, p.mask_dtype, mi));
+                        }
                         if ((need_tail && kk >= lk) || (need_causal && kk > pos[b] + coff)) val = -INFINITY;
                         x[kb][i] = val;
                         mt = fmaxf(mt, val);
@@ -477,6 +482,8 @@ const char* check_args(const kmi_attn_args* a) {
         if (a->mask_dtype < KMI_BF16 || a->mask_dtype > KMI_BOOL) return "bad mask dtype";
         if (a->mask_mode == KMI_MASK_PACKED && !varlen) return "packed masks are varlen only";
         if (a->mask_mode != KMI_MASK_STRIDED && a->mask_mode != KMI_MASK_PACKED) return "bad mask mode";
+        if (a->mask_mode == KMI_MASK_PACKED && a->mask_numel <= 0) return "packed masks need mask_numel";
+        if (a->mask_mode == KMI_MASK_PACKED && a->mask_stride[1] != 0) return "packed masks are shared by the heads";
     }
     return nullptr;
 }
@@ -574,6 +581,7 @@ extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t work
     p.mask_mode = a->mask_mode;
     p.mask_dtype = a->mask_dtype;
     for (int i = 0; i < 4; ++i) p.ms[i] = a->mask_stride[i];
+    p.mask_numel = a->mask_numel;
     p.cu_q = a->cu_seqlens_q;
     p.cu_k = a->cu_seqlens_k;
     p.batch = static_cast<int>(a->batch);

@@ -368,23 +368,24 @@ std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, c
         a.mask_mode = KMI_MASK_STRIDED;
         a.mask_stride[3] = 1;
     } else if (mask_given(attn_mask)) {
-        // The block-packed mask must hold sum(Lq_i * Lk_i) values: the offsets are read
-        // on the host to check it (the kernels index the mask by them).
-        Tensor hq = cu_q_in.to(at::kCPU, at::kLong).contiguous(), hk = cu_k_in.to(at::kCPU, at::kLong).contiguous();
-        const int64_t* pq = hq.data_ptr<int64_t>();
-        const int64_t* pk = hk.data_ptr<int64_t>();
-        int64_t need = 0;
-        for (int64_t i = 0; i < nseq; ++i) {
-            const int64_t a0 = std::min(std::max<int64_t>(pq[i], 0), Tq), a1 = std::min(std::max(pq[i + 1], a0), Tq);
-            const int64_t b0 = std::min(std::max<int64_t>(pk[i], 0), Tk), b1 = std::min(std::max(pk[i + 1], b0), Tk);
-            need += (a1 - a0) * (b1 - b0);
-        }
+        // The block-packed mask holds sum(Lq_i * Lk_i) values.  Host offsets are checked
+        // against it here; with device offsets the kernels treat reads past its end as
+        // masked (no host sync, so the call can be captured in a graph).
         m = *attn_mask;
-        TORCH_CHECK(m.numel() == need, "kohakutt_amd: sdpa_varlen packed mask must hold sum(Lq_i * Lk_i) = ", need,
-                    " values, got ", m.numel());
+        if (!cu_q_in.is_cuda() && !cu_k_in.is_cuda()) {
+            Tensor hq = cu_q_in.to(at::kLong).contiguous(), hk = cu_k_in.to(at::kLong).contiguous();
+            const int64_t* pq = hq.data_ptr<int64_t>();
+            const int64_t* pk = hk.data_ptr<int64_t>();
+            int64_t need = 0;
+            for (int64_t i = 0; i < nseq; ++i) need += (pq[i + 1] - pq[i]) * (pk[i + 1] - pk[i]);
+            TORCH_CHECK(m.numel() == need, "kohakutt_amd: sdpa_varlen packed mask must hold sum(Lq_i * Lk_i) = ",
+                        need, " values, got ", m.numel());
+        }
         if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
         m = m.to(q.device()).contiguous().view({-1});
+        TORCH_CHECK(m.numel() > 0, "kohakutt_amd: sdpa_varlen packed mask is empty");
         a.mask_mode = KMI_MASK_PACKED;
+        a.mask_numel = m.numel();
     }
     if (m.defined()) {
         a.mask = m.data_ptr();

@@ -114,6 +114,11 @@ def sdpa_varlen(
             max_q = max((a for a, _ in lengths), default=0)
         if max_k is None:
             max_k = max((b for _, b in lengths), default=0)
+        if packed_mask is not None and packed_mask.numel() != sum(a * b for a, b in lengths):
+            raise ValueError(
+                "kohakutt_amd.sdpa_varlen: packed_mask must hold sum(Lq_i * Lk_i) = "
+                f"{sum(a * b for a, b in lengths)} values, got {packed_mask.numel()}"
+            )
         cu_q_t = torch.tensor(cu_q, dtype=torch.int32, device=q.device)
         cu_k_t = torch.tensor(cu_k, dtype=torch.int32, device=q.device)
     else:

@@ -57,6 +57,7 @@ class AttnArgs(ctypes.Structure):
         ("mask_dtype", ctypes.c_int32),
         ("mask_mode", ctypes.c_int32),
         ("mask_stride", _I64x4),
+        ("mask_numel", ctypes.c_int64),
         ("cu_seqlens_q", ctypes.c_void_p),
         ("cu_seqlens_k", ctypes.c_void_p),
         ("total_q", ctypes.c_int64),
