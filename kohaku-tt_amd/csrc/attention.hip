@@ -47,7 +47,7 @@ struct AttnParams {
     void* out;
     float* lse;
     float* part_o;    // [splits][rows_total][hq][D] fp32 (normalised partial outputs)
-    float* part_lse;  // [splits][rows_total][hq] fp32, base-2 log-sum-exp
+    float* part_lse;  // [splits][rows_total][hq][2] fp32: base-2 log-sum-exp, raw-mode flag
     int64_t qs[3], ks[3], vs[3], os[3], ls[3];
     const void* mask;
     int64_t ms[4];
@@ -268,10 +268,13 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         }
     };
 
+    const bool has_mask = p.mask_mode != KMI_MASK_NONE;
     f32x4 o[DB][NQB];
     float m_run[NQB], l_run[NQB];
+    bool raw[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
+        raw[b] = has_mask;
         m_run[b] = -INFINITY;
         l_run[b] = 0.f;
 #pragma unroll
@@ -310,21 +313,56 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
             for (int b = 0; b < NQB; ++b) {
                 float x[KB][4];
                 float mt = -INFINITY;
+                bool keep_any = false;
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int kk = key0 + 16 * kb + 4 * g4 + i;
                         float val = s[kb][b][i] * p.scale_log2;
-                        if (p.mask_mode != KMI_MASK_NONE && kk < lk) {
+                        const bool vis = !((need_tail && kk >= lk) || (need_causal && kk > pos[b] + coff));
+                        if (!vis) {
+                            val = -INFINITY;
+                        } else if (has_mask) {
                             const int64_t mi = mrow[b] + kk * m_key;
-                            val += kLog2e * ((p.mask_mode == KMI_MASK_PACKED && mi >= p.mask_numel)
+                            const float ml = (p.mask_mode == KMI_MASK_PACKED && mi >= p.mask_numel)
                                                  ? kMaskedLogit
-                                                 : mask_logit(mptr, p.mask_dtype, mi));
+                                                 : mask_logit(mptr, p.mask_dtype, mi);
+                            if (ml > kMaskedLogit) {
+                                val += kLog2e * ml;
+                                keep_any = true;
+                            } else {
+                                val = -INFINITY;
+                            }
                         }
-                        if ((need_tail && kk >= lk) || (need_causal && kk > pos[b] + coff)) val = -INFINITY;
                         x[kb][i] = val;
                         mt = fmaxf(mt, val);
+                    }
+                }
+                if (has_mask) {
+                    // A row runs over its raw scores (mask ignored: the reference's result
+                    // for a row whose every key is masked) until its first kept key; then
+                    // it drops that state and masked keys get exactly zero weight.
+                    int ka = keep_any ? 1 : 0;
+                    ka |= __shfl_xor(ka, 16, kWave);
+                    ka |= __shfl_xor(ka, 32, kWave);
+                    if (raw[b] && ka) {
+                        raw[b] = false;
+                        m_run[b] = -INFINITY;
+                        l_run[b] = 0.f;
+                    }
+                    if (raw[b]) {
+                        mt = -INFINITY;
+#pragma unroll
+                        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int kk = key0 + 16 * kb + 4 * g4 + i;
+                                const bool vis = !((need_tail && kk >= lk) || (need_causal && kk > pos[b] + coff));
+                                x[kb][i] = vis ? s[kb][b][i] * p.scale_log2 : -INFINITY;
+                                mt = fmaxf(mt, x[kb][i]);
+                            }
+                        }
                     }
                 }
                 mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
@@ -386,7 +424,10 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
             for (int d = 0; d < DB; ++d) {
                 *reinterpret_cast<f32x4*>(dst + 16 * d + 4 * g4) = o[d][b] * inv;
             }
-            if (g4 == 0) p.part_lse[prow] = lse2;
+            if (g4 == 0) {
+                p.part_lse[2 * prow] = lse2;
+                p.part_lse[2 * prow + 1] = raw[b] ? 1.f : 0.f;
+            }
         } else {
             T* dst = static_cast<T*>(p.out) + ob_off + head[b] * p.os[1] + static_cast<int64_t>(q0 + pos[b]) * p.os[2];
 #pragma unroll
@@ -411,8 +452,19 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     if (item >= p.rows_total * p.hq) return;
     const int64_t row = item / p.hq;
     const int h = static_cast<int>(item % p.hq);
+    // Splits in masked mode (they met a kept key) win; a row with no kept key in any
+    // split merges the raw-score partials of every split.
+    const int64_t stride = p.rows_total * p.hq;
+    bool any_masked = false;
+    for (int s = 0; s < p.splits; ++s) {
+        const float* e = p.part_lse + 2 * (s * stride + item);
+        if (e[1] == 0.f && e[0] != -INFINITY) any_masked = true;
+    }
     float m = -INFINITY;
-    for (int s = 0; s < p.splits; ++s) m = fmaxf(m, p.part_lse[s * p.rows_total * p.hq + item]);
+    for (int s = 0; s < p.splits; ++s) {
+        const float* e = p.part_lse + 2 * (s * stride + item);
+        if (!any_masked || e[1] == 0.f) m = fmaxf(m, e[0]);
+    }
     constexpr int PER = D / 64;
     float acc[PER];
 #pragma unroll
@@ -420,8 +472,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     float wsum = 0.f;
     if (m != -INFINITY) {
         for (int s = 0; s < p.splits; ++s) {
-            const int64_t idx = s * p.rows_total * p.hq + item;
-            const float w = __builtin_amdgcn_exp2f(p.part_lse[idx] - m);
+            const int64_t idx = s * stride + item;
+            const float* e = p.part_lse + 2 * idx;
+            if (any_masked && e[1] != 0.f) continue;
+            const float w = __builtin_amdgcn_exp2f(e[0] - m);
             wsum += w;
             const float* src = p.part_o + idx * D;
 #pragma unroll
@@ -515,7 +569,7 @@ Plan make_plan(const kmi_attn_args* a) {
 // Split partials are indexed by query row: b * Sq + i (dense) or the packed token (varlen).
 size_t ws_bytes_for(const kmi_attn_args* a, const Plan& pl) {
     if (pl.splits <= 1) return 0;
-    return static_cast<size_t>(pl.splits) * pl.rows_total * a->heads_q * (a->head_dim + 1) * sizeof(float);
+    return static_cast<size_t>(pl.splits) * pl.rows_total * a->heads_q * (a->head_dim + 2) * sizeof(float);
 }
 
 template <typename T, int D, int NQB>
