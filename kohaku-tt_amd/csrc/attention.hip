@@ -28,6 +28,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 namespace kmi {
@@ -39,6 +40,7 @@ constexpr int NTHREADS = NWAVES * kWave;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kMaskedLogit = -5e5f;
+constexpr float kLazy = 8.f;  // log2 units a row max may grow before O is rescaled
 
 struct AttnParams {
     const void* q;
@@ -81,16 +83,27 @@ struct Mfma<f16> {
     }
 };
 
-// Mask value (logit units, clamped at the masked logit) of element `i`.
-__device__ __forceinline__ float mask_logit(const void* m, int dtype, int64_t i) {
-    float x;
-    switch (dtype) {
-        case KMI_BOOL: return static_cast<const uint8_t*>(m)[i] ? 0.f : kMaskedLogit;
-        case KMI_BF16: x = to_f32(static_cast<const bf16*>(m)[i]); break;
-        case KMI_F16: x = to_f32(static_cast<const f16*>(m)[i]); break;
-        default: x = static_cast<const float*>(m)[i];
+// Mask element types, a template parameter of the kernel (no mask code in the
+// mask-free variants).
+enum MaskKind { MK_NONE = 0, MK_BOOL = 1, MK_BF16 = 2, MK_F16 = 3, MK_F32 = 4 };
+
+// Mask value of element `i` in logit units, clamped at the masked logit (bool: keep -> 0,
+// drop -> -5e5; -inf and NaN -> -5e5).
+template <int MK>
+__device__ __forceinline__ float mask_value(const void* m, int64_t i) {
+    if constexpr (MK == MK_BOOL) {
+        return static_cast<const uint8_t*>(m)[i] ? 0.f : kMaskedLogit;
+    } else {
+        float x;
+        if constexpr (MK == MK_BF16) {
+            x = to_f32(static_cast<const bf16*>(m)[i]);
+        } else if constexpr (MK == MK_F16) {
+            x = to_f32(static_cast<const f16*>(m)[i]);
+        } else {
+            x = static_cast<const float*>(m)[i];
+        }
+        return fmaxf(x, kMaskedLogit);
     }
-    return fmaxf(x, kMaskedLogit);  // -inf -> -5e5
 }
 
 // Position of key `kk` (0..BN-1) in a transposed V row: within each 32-key chunk the
@@ -100,7 +113,7 @@ __device__ __forceinline__ int vpos(int kk) {
     return (kk & ~31) + 8 * ((c & 15) >> 2) + ((c >> 4) << 2) + (c & 3);
 }
 
-template <typename T, int D, int NQB>
+template <typename T, int D, int NQB, int MK>
 __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
     typedef typename Mfma<T>::v8 v8;
     constexpr int BM = NWAVES * 16 * NQB;
@@ -109,9 +122,12 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     constexpr int DC = D / 32;  // 32-wide chunks of the head dim
     constexpr int DB = D / 16;  // 16-wide blocks of the head dim
     constexpr int KB = BN / 16;
-    constexpr int VPT = BN * D / 8 / NTHREADS;  // 16-byte K vectors per thread per tile
-    constexpr int UPT = VPT / 2;                // (2 keys x 8 dims) V units per thread
-    static_assert(VPT >= 2 && VPT % 2 == 0, "tile shape");
+    constexpr int VPR = D / 8;             // 16-byte vectors per key row
+    constexpr int RPI = NTHREADS / VPR;    // key rows one pass of the block covers
+    constexpr int KIT = BN / RPI;          // K passes per tile
+    constexpr int VIT = BN / (2 * RPI);    // V passes per tile (two keys per thread)
+    static_assert(KIT >= 1 && VIT >= 1 && BN % (2 * RPI) == 0, "tile shape");
+    constexpr bool MASKED = MK != MK_NONE;
 
     extern __shared__ __align__(16) unsigned char smem[];
     T* k_lds = reinterpret_cast<T*>(smem);
@@ -124,14 +140,15 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int l16 = lane & 15;
 
     // Work item: heaviest query tiles first (causal), then (sequence, K/V head), split.
-    int64_t lin = blockIdx.x;
-    const int split = static_cast<int>(lin % p.splits);
+    int lin = blockIdx.x;
+    const int split = lin % p.splits;
     lin /= p.splits;
-    const int bh = static_cast<int>(lin % (p.batch * p.hkv));
-    int xt = static_cast<int>(lin / (p.batch * p.hkv));
+    const int units = p.batch * p.hkv;
+    const int bh = lin % units;
+    int xt = lin / units;
     if (p.causal) xt = p.nx - 1 - xt;
     const int seq = bh / p.hkv;
-    const int kvh = bh % p.hkv;
+    const int kvh = bh - seq * p.hkv;
     const int G = p.group;
 
     int q0 = 0, lq = p.seq_q, k0 = 0, lk = p.seq_k;
@@ -151,7 +168,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int r_begin = xt * BM;
     if (r_begin >= vrows || lk <= 0) return;
     const int r_end = min(vrows, r_begin + BM);
-    const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys < i + 1 + coff
+    const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys <= i + coff
     int kend = lk;
     if (p.causal) kend = max(0, min(lk, (r_end - 1) / G + 1 + coff));
     const int ntiles = (kend + BN - 1) / BN;
@@ -160,31 +177,20 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         t_begin = split * p.tiles_per_split;
         t_end = min(ntiles, t_begin + p.tiles_per_split);
     }
-    const int first_pos = r_begin / G;  // smallest query position in the tile
-
-    // Mask addressing: per-sequence base.
-    const void* mptr = p.mask;
-    int64_t m_seq = 0;
-    if (p.mask_mode == KMI_MASK_STRIDED) {
-        m_seq = p.cu_q ? (static_cast<int64_t>(q0) * p.ms[2] + static_cast<int64_t>(k0) * p.ms[3])
-                       : seq * p.ms[0];
-    } else if (p.mask_mode == KMI_MASK_PACKED) {
-        for (int s = 0; s < seq; ++s) {
-            const int a0 = min(max(p.cu_q[s], 0), p.total_q), a1 = min(max(p.cu_q[s + 1], a0), p.total_q);
-            const int b0 = min(max(p.cu_k[s], 0), p.total_k), b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
-            m_seq += static_cast<int64_t>(a1 - a0) * (b1 - b0);
-        }
-    }
-    const int64_t m_key = p.mask_mode == KMI_MASK_PACKED ? 1 : p.ms[3];
 
     // This lane's rows: Q fragments (B operand of S^T = K Q^T) and row metadata.
     const T* qp = static_cast<const T*>(p.q);
-    const T* kp = static_cast<const T*>(p.k);
-    const T* vp = static_cast<const T*>(p.v);
     v8 qf[NQB][DC];
-    int pos[NQB], head[NQB];
+    int pos[NQB], head[NQB], lim[NQB];
     bool valid[NQB];
     int64_t mrow[NQB];
+    int64_t m_key = 0, m_end = 0;
+    const void* mptr = p.mask;
+    if constexpr (MASKED) {
+        // Packed masks are bounded by their element count; strided ones by their shape.
+        m_end = p.mask_mode == KMI_MASK_PACKED ? p.mask_numel : INT64_MAX;
+        m_key = p.mask_mode == KMI_MASK_PACKED ? 1 : p.ms[3];
+    }
     const int wave_row0 = r_begin + wave * 16 * NQB;
     const bool wave_active = wave_row0 < r_end;
 #pragma unroll
@@ -193,7 +199,8 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         valid[b] = r < r_end;
         const int rr = valid[b] ? r : r_begin;
         pos[b] = rr / G;
-        head[b] = kvh * G + rr % G;
+        head[b] = kvh * G + (rr - pos[b] * G);
+        lim[b] = p.causal ? min(lk, pos[b] + coff + 1) : lk;  // keys [0, lim) are visible
         const T* src = qp + qb_off + head[b] * p.qs[1] + static_cast<int64_t>(q0 + pos[b]) * p.qs[2];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
@@ -204,42 +211,58 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                 for (int j = 0; j < 8; ++j) qf[b][c][j] = static_cast<T>(0.f);
             }
         }
-        if (p.mask_mode == KMI_MASK_PACKED) {
-            mrow[b] = m_seq + head[b] * p.ms[1] + static_cast<int64_t>(pos[b]) * lk;
-        } else {
-            mrow[b] = m_seq + head[b] * p.ms[1] + static_cast<int64_t>(pos[b]) * p.ms[2];
+        if constexpr (MASKED) {
+            if (p.mask_mode == KMI_MASK_PACKED) {
+                int64_t m_seq = 0;
+                for (int s = 0; s < seq; ++s) {
+                    const int a0 = min(max(p.cu_q[s], 0), p.total_q);
+                    const int a1 = min(max(p.cu_q[s + 1], a0), p.total_q);
+                    const int b0 = min(max(p.cu_k[s], 0), p.total_k);
+                    const int b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
+                    m_seq += static_cast<int64_t>(a1 - a0) * (b1 - b0);
+                }
+                mrow[b] = m_seq + static_cast<int64_t>(pos[b]) * lk;
+            } else {
+                const int64_t m_seq = p.cu_q ? (static_cast<int64_t>(q0) * p.ms[2] + static_cast<int64_t>(k0) * p.ms[3])
+                                             : seq * p.ms[0];
+                mrow[b] = m_seq + head[b] * p.ms[1] + static_cast<int64_t>(pos[b]) * p.ms[2];
+            }
         }
     }
 
-    // K / V tile prefetch registers.
-    u32x4 kreg[VPT];
-    u32x4 vreg[UPT][2];
+    // K / V sources of this thread: key row `krow` (+ RPI per pass) of each tile.
+    const int krow = tid / VPR, dg = tid - (tid / VPR) * VPR;
+    const T* kbase = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * p.ks[2] + 8 * dg;
+    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + 2 * krow) * p.vs[2] + 8 * dg;
+    const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
+
+    u32x4 kreg[KIT];
+    u32x4 vreg[VIT][2];
     auto load_tile = [&](int t) {
         const int key0 = t * BN;
+        const T* ksrc = kbase + static_cast<int64_t>(key0) * ks2;
+        const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
+        if (key0 + BN <= lk) {
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int u = tid + NTHREADS * i;
-            const int key = u / (D / 8), dg = u % (D / 8);
-            const int kk = key0 + key;
-            if (kk < lk) {
-                kreg[i] = *reinterpret_cast<const u32x4*>(
-                    kp + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + kk) * p.ks[2] + 8 * dg);
-            } else {
-                kreg[i] = u32x4{0u, 0u, 0u, 0u};
+            for (int i = 0; i < KIT; ++i) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPI) * ks2);
+#pragma unroll
+            for (int i = 0; i < VIT; ++i) {
+                vreg[i][0] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPI) * vs2);
+                vreg[i][1] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPI + 1) * vs2);
             }
-        }
+        } else {
 #pragma unroll
-        for (int i = 0; i < UPT; ++i) {
-            const int u = tid + NTHREADS * i;
-            const int kpair = u / (D / 8), dg = u % (D / 8);
+            for (int i = 0; i < KIT; ++i) {
+                kreg[i] = u32x4{0u, 0u, 0u, 0u};
+                if (key0 + krow + i * RPI < lk) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPI) * ks2);
+            }
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int kk = key0 + 2 * kpair + e;
-                if (kk < lk) {
-                    vreg[i][e] = *reinterpret_cast<const u32x4*>(
-                        vp + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + kk) * p.vs[2] + 8 * dg);
-                } else {
+            for (int i = 0; i < VIT; ++i) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
                     vreg[i][e] = u32x4{0u, 0u, 0u, 0u};
+                    if (key0 + 2 * (krow + i * RPI) + e < lk)
+                        vreg[i][e] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPI + e) * vs2);
                 }
             }
         }
@@ -248,16 +271,10 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         T* kl = k_lds + buf * BN * KP;
         T* vl = v_lds + buf * D * VP;
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int u = tid + NTHREADS * i;
-            const int key = u / (D / 8), dg = u % (D / 8);
-            *reinterpret_cast<u32x4*>(kl + key * KP + 8 * dg) = kreg[i];
-        }
+        for (int i = 0; i < KIT; ++i) *reinterpret_cast<u32x4*>(kl + (krow + i * RPI) * KP + 8 * dg) = kreg[i];
 #pragma unroll
-        for (int i = 0; i < UPT; ++i) {
-            const int u = tid + NTHREADS * i;
-            const int kpair = u / (D / 8), dg = u % (D / 8);
-            const int col = vpos(2 * kpair);
+        for (int i = 0; i < VIT; ++i) {
+            const int col = vpos(2 * (krow + i * RPI));
             const uint16_t* a = reinterpret_cast<const uint16_t*>(&vreg[i][0]);
             const uint16_t* b = reinterpret_cast<const uint16_t*>(&vreg[i][1]);
 #pragma unroll
@@ -268,18 +285,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         }
     };
 
-    const bool has_mask = p.mask_mode != KMI_MASK_NONE;
     f32x4 o[DB][NQB];
     float m_run[NQB], l_run[NQB];
     bool raw[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
-        raw[b] = has_mask;
+        raw[b] = MASKED;
         m_run[b] = -INFINITY;
         l_run[b] = 0.f;
 #pragma unroll
         for (int d = 0; d < DB; ++d) o[d][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    const float c2 = p.scale_log2;
 
     if (t_begin < t_end) {
         load_tile(t_begin);
@@ -306,40 +323,34 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                 }
             }
             const int key0 = t * BN;
-            const bool need_causal = p.causal && (key0 + BN - 1 > first_pos + coff);
-            const bool need_tail = key0 + BN > lk;
             v8 pf[NQB][BN / 32];
 #pragma unroll
             for (int b = 0; b < NQB; ++b) {
                 float x[KB][4];
-                float mt = -INFINITY;
                 bool keep_any = false;
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int kk = key0 + 16 * kb + 4 * g4 + i;
-                        float val = s[kb][b][i] * p.scale_log2;
-                        const bool vis = !((need_tail && kk >= lk) || (need_causal && kk > pos[b] + coff));
-                        if (!vis) {
-                            val = -INFINITY;
-                        } else if (has_mask) {
-                            const int64_t mi = mrow[b] + kk * m_key;
-                            const float ml = (p.mask_mode == KMI_MASK_PACKED && mi >= p.mask_numel)
-                                                 ? kMaskedLogit
-                                                 : mask_logit(mptr, p.mask_dtype, mi);
-                            if (ml > kMaskedLogit) {
-                                val += kLog2e * ml;
-                                keep_any = true;
-                            } else {
-                                val = -INFINITY;
+                        float val = s[kb][b][i] * c2;
+                        const bool vis = kk < lim[b];
+                        if constexpr (MASKED) {
+                            if (vis) {
+                                const int64_t mi = mrow[b] + kk * m_key;
+                                const float ml = mi < m_end ? mask_value<MK>(mptr, mi) : kMaskedLogit;
+                                if (ml > kMaskedLogit) {
+                                    val += kLog2e * ml;
+                                    keep_any = true;
+                                } else {
+                                    val = -INFINITY;
+                                }
                             }
                         }
-                        x[kb][i] = val;
-                        mt = fmaxf(mt, val);
+                        x[kb][i] = vis ? val : -INFINITY;
                     }
                 }
-                if (has_mask) {
+                if constexpr (MASKED) {
                     // A row runs over its raw scores (mask ignored: the reference's result
                     // for a row whose every key is masked) until its first kept key; then
                     // it drops that state and masked keys get exactly zero weight.
@@ -352,25 +363,39 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                         l_run[b] = 0.f;
                     }
                     if (raw[b]) {
-                        mt = -INFINITY;
 #pragma unroll
                         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const int kk = key0 + 16 * kb + 4 * g4 + i;
-                                const bool vis = !((need_tail && kk >= lk) || (need_causal && kk > pos[b] + coff));
-                                x[kb][i] = vis ? s[kb][b][i] * p.scale_log2 : -INFINITY;
-                                mt = fmaxf(mt, x[kb][i]);
+                                x[kb][i] = kk < lim[b] ? s[kb][b][i] * c2 : -INFINITY;
                             }
                         }
                     }
                 }
+                float mt = -INFINITY;
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mt = fmaxf(mt, x[kb][i]);
+                }
                 mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
                 mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-                const float m_new = fmaxf(m_run[b], mt);
-                const float m_use = m_new == -INFINITY ? 0.f : m_new;
-                const float alpha = __builtin_amdgcn_exp2f(m_run[b] - m_use);
-                m_run[b] = m_new;
+                // Lazy rescale: the reference point moves only when a score would exceed it
+                // by more than 2^8 (P stays <= 256, exact in bf16's exponent range); O and l
+                // are rescaled only then, skipped when no row of the wavefront moved.
+                const bool move = mt > m_run[b] + kLazy;
+                float alpha = 1.f;
+                if (move) {
+                    alpha = __builtin_amdgcn_exp2f(m_run[b] - mt);
+                    m_run[b] = mt;
+                }
+                const float m_use = m_run[b] == -INFINITY ? 0.f : m_run[b];
+                if (__builtin_amdgcn_ballot_w64(move)) {
+                    l_run[b] *= alpha;
+#pragma unroll
+                    for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
+                }
                 float ls = 0.f;
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) {
@@ -381,25 +406,23 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                         ls += e;
                     }
                 }
-                l_run[b] = l_run[b] * alpha + ls;
+                l_run[b] += ls;
 #pragma unroll
-                for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
-#pragma unroll
-                for (int c2 = 0; c2 < BN / 32; ++c2) {
+                for (int cc = 0; cc < BN / 32; ++cc) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        pf[b][c2][i] = static_cast<T>(x[2 * c2][i]);
-                        pf[b][c2][4 + i] = static_cast<T>(x[2 * c2 + 1][i]);
+                        pf[b][cc][i] = static_cast<T>(x[2 * cc][i]);
+                        pf[b][cc][4 + i] = static_cast<T>(x[2 * cc + 1][i]);
                     }
                 }
             }
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
 #pragma unroll
-                for (int c2 = 0; c2 < BN / 32; ++c2) {
-                    const v8 a = *reinterpret_cast<const v8*>(vl + (16 * d + l16) * VP + 32 * c2 + 8 * g4);
+                for (int cc = 0; cc < BN / 32; ++cc) {
+                    const v8 a = *reinterpret_cast<const v8*>(vl + (16 * d + l16) * VP + 32 * cc + 8 * g4);
 #pragma unroll
-                    for (int b = 0; b < NQB; ++b) o[d][b] = Mfma<T>::run(a, pf[b][c2], o[d][b]);
+                    for (int b = 0; b < NQB; ++b) o[d][b] = Mfma<T>::run(a, pf[b][cc], o[d][b]);
                 }
             }
         }
@@ -542,13 +565,33 @@ const char* check_args(const kmi_attn_args* a) {
     return nullptr;
 }
 
+// KMI_ATTN_NQB=1|2|4 (read once) pins the 16-row blocks per wavefront; otherwise the
+// plan takes the most rows per wavefront (fewer LDS reads per MFMA: a wavefront reads each
+// K/V tile once for all its rows) that still gives every CU a workgroup.
+int nqb_override() {
+    static const int v = [] {
+        const char* e = std::getenv("KMI_ATTN_NQB");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
 Plan make_plan(const kmi_attn_args* a) {
     Plan pl{};
     const int64_t G = a->heads_q / a->heads_kv;
     const int64_t vrows = a->seq_q * G;
     const int64_t units = a->batch * a->heads_kv;
-    // Two 16-row blocks per wavefront when that still gives every CU two workgroups.
-    pl.nqb = (ceil_div(vrows, 128) * units >= 512) ? 2 : 1;
+    const int max_nqb = a->head_dim == 64 ? 4 : 2;
+    int nqb = 1;
+    for (int n = max_nqb; n >= 1; n /= 2) {
+        if (ceil_div(vrows, 64 * n) * units >= 256 || n == 1) {
+            nqb = n;
+            break;
+        }
+    }
+    const int forced = nqb_override();
+    if (forced == 1 || forced == 2 || (forced == 4 && a->head_dim == 64)) nqb = forced;
+    pl.nqb = nqb;
     const int64_t bm = 64 * pl.nqb;
     pl.nx = static_cast<int>(ceil_div(vrows, bm));
     const int64_t nk = ceil_div(a->seq_k, BN);
@@ -572,25 +615,43 @@ size_t ws_bytes_for(const kmi_attn_args* a, const Plan& pl) {
     return static_cast<size_t>(pl.splits) * pl.rows_total * a->heads_q * (a->head_dim + 2) * sizeof(float);
 }
 
-template <typename T, int D, int NQB>
+template <typename T, int D, int NQB, int MK>
 hipError_t launch_fwd(const AttnParams& p, int64_t grid, hipStream_t stream) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     const size_t lds = lds_bytes(D, sizeof(T));
     std::call_once(once, [&] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB>),
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     });
     if (attr_err != hipSuccess) return attr_err;
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS),
-                       lds, stream, p);
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds,
+                       stream, p);
     return hipGetLastError();
+}
+
+template <typename T, int D, int NQB>
+hipError_t launch_mask(const AttnParams& p, int64_t grid, hipStream_t stream) {
+    if (p.mask_mode == KMI_MASK_NONE) return launch_fwd<T, D, NQB, MK_NONE>(p, grid, stream);
+    switch (p.mask_dtype) {
+        case KMI_BOOL: return launch_fwd<T, D, NQB, MK_BOOL>(p, grid, stream);
+        case KMI_BF16: return launch_fwd<T, D, NQB, MK_BF16>(p, grid, stream);
+        case KMI_F16: return launch_fwd<T, D, NQB, MK_F16>(p, grid, stream);
+        default: return launch_fwd<T, D, NQB, MK_F32>(p, grid, stream);
+    }
 }
 
 template <typename T, int D>
 hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream) {
     const int64_t grid = static_cast<int64_t>(pl.nx) * p.batch * p.hkv * pl.splits;
-    hipError_t err = pl.nqb == 2 ? launch_fwd<T, D, 2>(p, grid, stream) : launch_fwd<T, D, 1>(p, grid, stream);
+    hipError_t err;
+    if (pl.nqb == 4 && D == 64) {
+        err = launch_mask<T, 64, 4>(p, grid, stream);
+    } else if (pl.nqb >= 2) {
+        err = launch_mask<T, D, 2>(p, grid, stream);
+    } else {
+        err = launch_mask<T, D, 1>(p, grid, stream);
+    }
     if (err != hipSuccess || pl.splits <= 1) return err;
     const int64_t items = p.rows_total * p.hq;
     hipLaunchKernelGGL((attn_merge_kernel<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 4))), dim3(256), 0,
