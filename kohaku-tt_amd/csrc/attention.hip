@@ -34,7 +34,6 @@
 namespace kmi {
 namespace {
 
-constexpr int BN = 64;  // keys per LDS tile
 constexpr int NWAVES = 4;
 constexpr int NTHREADS = NWAVES * kWave;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -106,32 +105,75 @@ __device__ __forceinline__ float mask_value(const void* m, int64_t i) {
     }
 }
 
-// Position of key `kk` (0..BN-1) in a transposed V row: within each 32-key chunk the
+// Position of key `kk` (0..31) in a transposed V row: within each 32-key chunk the
 // MFMA B operand of lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3 as slots 8g..8g+7.
 __device__ __forceinline__ int vpos(int kk) {
     const int c = kk & 31;
     return (kk & ~31) + 8 * ((c & 15) >> 2) + ((c >> 4) << 2) + (c & 3);
 }
 
+// Keys per wavefront tile.
+constexpr int WN = 32;
+
+template <int D, int NQB>
+struct Shape {
+    static constexpr int BM = 16 * NQB;        // rows of a workgroup (shared by its wavefronts)
+    static constexpr int KP = D + 8;           // K tile row pitch (elements)
+    static constexpr int VP = WN + 8;          // V^T tile row pitch (elements)
+    static constexpr int TILE = WN * KP + D * VP;  // elements of one wavefront's K + V^T tile
+    static constexpr int CP = D + 4;           // combine buffer row pitch (floats)
+    template <typename T>
+    static constexpr size_t lds_bytes() {
+        const size_t tiles = static_cast<size_t>(NWAVES) * TILE * sizeof(T);
+        const size_t comb = static_cast<size_t>(NWAVES) * BM * CP * sizeof(float);
+        return (tiles > comb ? tiles : comb) + static_cast<size_t>(NWAVES) * BM * 3 * sizeof(float);
+    }
+};
+
+// One workgroup owns BM rows of one (sequence, K/V head) and a key range; its four
+// wavefronts hold the same rows and take every fourth 32-key tile of the range, each
+// staging its own tiles (global -> registers -> its own LDS tile, one tile ahead) so no
+// block-wide barrier runs per tile.  The wavefronts' softmax states are merged once, in
+// LDS, in a fixed order.
+// Reductions over the four lanes that hold one query row (l, l^16, l^32, l^48): the
+// gfx950 row swaps exchange 16-lane rows (permlane16) and 32-lane halves (permlane32) in
+// registers, without the LDS crossbar a generic shuffle uses.
+__device__ __forceinline__ float row_max4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float row_sum4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Whether any of the four lanes of this lane's query row has `pred` set.
+__device__ __forceinline__ bool row_any4(bool pred, int l16) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64(pred) >> l16;
+    return (m & 0x0001000100010001ull) != 0;
+}
+
 template <typename T, int D, int NQB, int MK>
 __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
     typedef typename Mfma<T>::v8 v8;
-    constexpr int BM = NWAVES * 16 * NQB;
-    constexpr int KP = D + 8;   // K tile row pitch (elements)
-    constexpr int VP = BN + 8;  // V^T tile row pitch (elements)
+    typedef Shape<D, NQB> S;
+    constexpr int BM = S::BM, KP = S::KP, VP = S::VP, CP = S::CP;
     constexpr int DC = D / 32;  // 32-wide chunks of the head dim
     constexpr int DB = D / 16;  // 16-wide blocks of the head dim
-    constexpr int KB = BN / 16;
-    constexpr int VPR = D / 8;             // 16-byte vectors per key row
-    constexpr int RPI = NTHREADS / VPR;    // key rows one pass of the block covers
-    constexpr int KIT = BN / RPI;          // K passes per tile
-    constexpr int VIT = BN / (2 * RPI);    // V passes per tile (two keys per thread)
-    static_assert(KIT >= 1 && VIT >= 1 && BN % (2 * RPI) == 0, "tile shape");
+    constexpr int KB = WN / 16;
+    constexpr int VPR = D / 8;           // 16-byte vectors per key row
+    constexpr int RPP = kWave / VPR;     // key rows one wavefront pass covers
+    constexpr int KIT = WN / RPP;        // K passes per tile
+    constexpr int VIT = WN / (2 * RPP);  // V passes per tile (two keys per lane)
+    static_assert(KIT >= 1 && VIT >= 1 && WN % (2 * RPP) == 0, "tile shape");
     constexpr bool MASKED = MK != MK_NONE;
 
     extern __shared__ __align__(16) unsigned char smem[];
-    T* k_lds = reinterpret_cast<T*>(smem);
-    T* v_lds = k_lds + 2 * BN * KP;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -171,18 +213,21 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys <= i + coff
     int kend = lk;
     if (p.causal) kend = max(0, min(lk, (r_end - 1) / G + 1 + coff));
-    const int ntiles = (kend + BN - 1) / BN;
+    const int ntiles = (kend + WN - 1) / WN;
+    // Keys below lim_min are visible to every row of the workgroup: tiles past it need the
+    // per-element causal / tail test, the rest do not.
+    const int lim_min = p.causal ? min(lk, r_begin / G + coff + 1) : lk;
     int t_begin = 0, t_end = ntiles;
     if (p.splits > 1) {
         t_begin = split * p.tiles_per_split;
         t_end = min(ntiles, t_begin + p.tiles_per_split);
     }
 
-    // This lane's rows: Q fragments (B operand of S^T = K Q^T) and row metadata.
+    // This lane's rows (the same for every wavefront): Q fragments (B operand of
+    // S^T = K Q^T) and row metadata.
     const T* qp = static_cast<const T*>(p.q);
     v8 qf[NQB][DC];
-    int pos[NQB], head[NQB], lim[NQB];
-    bool valid[NQB];
+    int lim[NQB];
     int64_t mrow[NQB];
     int64_t m_key = 0, m_end = 0;
     const void* mptr = p.mask;
@@ -191,20 +236,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         m_end = p.mask_mode == KMI_MASK_PACKED ? p.mask_numel : INT64_MAX;
         m_key = p.mask_mode == KMI_MASK_PACKED ? 1 : p.ms[3];
     }
-    const int wave_row0 = r_begin + wave * 16 * NQB;
-    const bool wave_active = wave_row0 < r_end;
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
-        const int r = wave_row0 + 16 * b + l16;
-        valid[b] = r < r_end;
-        const int rr = valid[b] ? r : r_begin;
-        pos[b] = rr / G;
-        head[b] = kvh * G + (rr - pos[b] * G);
-        lim[b] = p.causal ? min(lk, pos[b] + coff + 1) : lk;  // keys [0, lim) are visible
-        const T* src = qp + qb_off + head[b] * p.qs[1] + static_cast<int64_t>(q0 + pos[b]) * p.qs[2];
+        const int r = r_begin + 16 * b + l16;
+        const bool valid = r < r_end;
+        const int rr = valid ? r : r_begin;
+        const int pos = rr / G;
+        const int head = kvh * G + (rr - pos * G);
+        lim[b] = p.causal ? min(lk, pos + coff + 1) : lk;  // keys [0, lim) are visible
+        const T* src = qp + qb_off + head * p.qs[1] + static_cast<int64_t>(q0 + pos) * p.qs[2];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
-            if (valid[b]) {
+            if (valid) {
                 qf[b][c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
             } else {
 #pragma unroll
@@ -221,60 +264,61 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                     const int b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
                     m_seq += static_cast<int64_t>(a1 - a0) * (b1 - b0);
                 }
-                mrow[b] = m_seq + static_cast<int64_t>(pos[b]) * lk;
+                mrow[b] = m_seq + static_cast<int64_t>(pos) * lk;
             } else {
                 const int64_t m_seq = p.cu_q ? (static_cast<int64_t>(q0) * p.ms[2] + static_cast<int64_t>(k0) * p.ms[3])
                                              : seq * p.ms[0];
-                mrow[b] = m_seq + head[b] * p.ms[1] + static_cast<int64_t>(pos[b]) * p.ms[2];
+                mrow[b] = m_seq + head * p.ms[1] + static_cast<int64_t>(pos) * p.ms[2];
             }
         }
     }
 
-    // K / V sources of this thread: key row `krow` (+ RPI per pass) of each tile.
-    const int krow = tid / VPR, dg = tid - (tid / VPR) * VPR;
-    const T* kbase = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * p.ks[2] + 8 * dg;
-    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + 2 * krow) * p.vs[2] + 8 * dg;
+    // This lane's K / V sources: key row `krow` (+ RPP per pass) of each tile.
+    const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
     const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
+    const T* kbase = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * ks2 + 8 * dg;
+    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + 2 * krow) * vs2 + 8 * dg;
+    T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
+    T* vl = kl + WN * KP;
 
     u32x4 kreg[KIT];
     u32x4 vreg[VIT][2];
     auto load_tile = [&](int t) {
-        const int key0 = t * BN;
+        const int key0 = t * WN;
         const T* ksrc = kbase + static_cast<int64_t>(key0) * ks2;
         const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
-        if (key0 + BN <= lk) {
+        if (key0 + WN <= lk) {
 #pragma unroll
-            for (int i = 0; i < KIT; ++i) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPI) * ks2);
+            for (int i = 0; i < KIT; ++i) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
 #pragma unroll
             for (int i = 0; i < VIT; ++i) {
-                vreg[i][0] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPI) * vs2);
-                vreg[i][1] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPI + 1) * vs2);
+                vreg[i][0] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPP) * vs2);
+                vreg[i][1] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPP + 1) * vs2);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < KIT; ++i) {
                 kreg[i] = u32x4{0u, 0u, 0u, 0u};
-                if (key0 + krow + i * RPI < lk) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPI) * ks2);
+                if (key0 + krow + i * RPP < lk) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
             }
 #pragma unroll
             for (int i = 0; i < VIT; ++i) {
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     vreg[i][e] = u32x4{0u, 0u, 0u, 0u};
-                    if (key0 + 2 * (krow + i * RPI) + e < lk)
-                        vreg[i][e] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPI + e) * vs2);
+                    if (key0 + 2 * (krow + i * RPP) + e < lk)
+                        vreg[i][e] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPP + e) * vs2);
                 }
             }
         }
     };
-    auto store_tile = [&](int buf) {
-        T* kl = k_lds + buf * BN * KP;
-        T* vl = v_lds + buf * D * VP;
+    // K rows as loaded; V transposed, keys in the order the PV B operand expects.
+    auto store_tile = [&]() {
 #pragma unroll
-        for (int i = 0; i < KIT; ++i) *reinterpret_cast<u32x4*>(kl + (krow + i * RPI) * KP + 8 * dg) = kreg[i];
+        for (int i = 0; i < KIT; ++i) *reinterpret_cast<u32x4*>(kl + (krow + i * RPP) * KP + 8 * dg) = kreg[i];
 #pragma unroll
         for (int i = 0; i < VIT; ++i) {
-            const int col = vpos(2 * (krow + i * RPI));
+            const int col = vpos(2 * (krow + i * RPP));
             const uint16_t* a = reinterpret_cast<const uint16_t*>(&vreg[i][0]);
             const uint16_t* b = reinterpret_cast<const uint16_t*>(&vreg[i][1]);
 #pragma unroll
@@ -298,171 +342,225 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     }
     const float c2 = p.scale_log2;
 
-    if (t_begin < t_end) {
-        load_tile(t_begin);
-        store_tile(0);
-    }
-    __syncthreads();
-    for (int t = t_begin; t < t_end; ++t) {
-        const int buf = (t - t_begin) & 1;
-        const bool has_next = t + 1 < t_end;
-        if (has_next) load_tile(t + 1);
-        if (wave_active) {
-            const T* kl = k_lds + buf * BN * KP;
-            const T* vl = v_lds + buf * D * VP;
-            f32x4 s[KB][NQB];
+    const int t_first = t_begin + wave;
+    if (t_first < t_end) load_tile(t_first);
+    for (int t = t_first; t < t_end; t += NWAVES) {
+        // The previous tile's LDS reads were issued before these writes; LDS runs one
+        // wavefront's instructions in order, so only the compiler must keep the order.
+        __asm__ volatile("" ::: "memory");
+        store_tile();
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (t + NWAVES < t_end) load_tile(t + NWAVES);
+        f32x4 s[KB][NQB];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+            for (int b = 0; b < NQB; ++b) s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                const v8 a = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
+#pragma unroll
+                for (int b = 0; b < NQB; ++b)
+                    if (r_begin + 16 * b < r_end) s[kb][b] = Mfma<T>::run(a, qf[b][c], s[kb][b]);
+            }
+        }
+        const int key0 = t * WN;
+        const bool edge = key0 + WN > lim_min;
+        v8 pf[NQB];
+#pragma unroll
+        for (int b = 0; b < NQB; ++b) {
+            if (r_begin + 16 * b >= r_end) continue;
+            // x: logits in base-2 units.  Mask-free rows keep the raw accumulators (the
+            // scale is folded into the exponent's FMA below), -inf where not visible.
+            float x[KB][4];
+            const int rel = lim[b] - key0 - 4 * g4;  // element (kb, i) is visible iff 16 kb + i < rel
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                for (int b = 0; b < NQB; ++b) s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int c = 0; c < DC; ++c) {
-                    const v8 a = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
-#pragma unroll
-                    for (int b = 0; b < NQB; ++b) s[kb][b] = Mfma<T>::run(a, qf[b][c], s[kb][b]);
-                }
+                for (int i = 0; i < 4; ++i) x[kb][i] = s[kb][b][i];
             }
-            const int key0 = t * BN;
-            v8 pf[NQB][BN / 32];
-#pragma unroll
-            for (int b = 0; b < NQB; ++b) {
-                float x[KB][4];
+            float xs = c2;  // multiplier of x in the exponent
+            if constexpr (MASKED) {
+                xs = 1.f;
                 bool keep_any = false;
+                float xm[KB][4];
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
+                        const bool vis = 16 * kb + i < rel;
                         const int kk = key0 + 16 * kb + 4 * g4 + i;
-                        float val = s[kb][b][i] * c2;
-                        const bool vis = kk < lim[b];
-                        if constexpr (MASKED) {
-                            if (vis) {
-                                const int64_t mi = mrow[b] + kk * m_key;
-                                const float ml = mi < m_end ? mask_value<MK>(mptr, mi) : kMaskedLogit;
-                                if (ml > kMaskedLogit) {
-                                    val += kLog2e * ml;
-                                    keep_any = true;
-                                } else {
-                                    val = -INFINITY;
-                                }
+                        float val = x[kb][i] * c2;
+                        float vm = -INFINITY;
+                        if (vis) {
+                            const int64_t mi = mrow[b] + kk * m_key;
+                            const float ml = mi < m_end ? mask_value<MK>(mptr, mi) : kMaskedLogit;
+                            if (ml > kMaskedLogit) {
+                                vm = val + kLog2e * ml;
+                                keep_any = true;
                             }
+                        } else {
+                            val = -INFINITY;
                         }
-                        x[kb][i] = vis ? val : -INFINITY;
+                        x[kb][i] = val;
+                        xm[kb][i] = vm;
                     }
                 }
-                if constexpr (MASKED) {
-                    // A row runs over its raw scores (mask ignored: the reference's result
-                    // for a row whose every key is masked) until its first kept key; then
-                    // it drops that state and masked keys get exactly zero weight.
-                    int ka = keep_any ? 1 : 0;
-                    ka |= __shfl_xor(ka, 16, kWave);
-                    ka |= __shfl_xor(ka, 32, kWave);
-                    if (raw[b] && ka) {
-                        raw[b] = false;
-                        m_run[b] = -INFINITY;
-                        l_run[b] = 0.f;
-                    }
-                    if (raw[b]) {
+                // A row runs over its raw scores (mask ignored: the reference's result for
+                // a row whose every key is masked) until its first kept key; then it drops
+                // that state and masked keys get exactly zero weight.
+                if (raw[b] && row_any4(keep_any, l16)) {
+                    raw[b] = false;
+                    m_run[b] = -INFINITY;
+                    l_run[b] = 0.f;
+                }
+                if (!raw[b]) {
 #pragma unroll
-                        for (int kb = 0; kb < KB; ++kb) {
+                    for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const int kk = key0 + 16 * kb + 4 * g4 + i;
-                                x[kb][i] = kk < lim[b] ? s[kb][b][i] * c2 : -INFINITY;
-                            }
-                        }
+                        for (int i = 0; i < 4; ++i) x[kb][i] = xm[kb][i];
                     }
                 }
-                float mt = -INFINITY;
+            } else if (edge) {
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) mt = fmaxf(mt, x[kb][i]);
-                }
-                mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-                mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-                // Lazy rescale: the reference point moves only when a score would exceed it
-                // by more than 2^8 (P stays <= 256, exact in bf16's exponent range); O and l
-                // are rescaled only then, skipped when no row of the wavefront moved.
-                const bool move = mt > m_run[b] + kLazy;
-                float alpha = 1.f;
-                if (move) {
-                    alpha = __builtin_amdgcn_exp2f(m_run[b] - mt);
-                    m_run[b] = mt;
-                }
-                const float m_use = m_run[b] == -INFINITY ? 0.f : m_run[b];
-                if (__builtin_amdgcn_ballot_w64(move)) {
-                    l_run[b] *= alpha;
-#pragma unroll
-                    for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
-                }
-                float ls = 0.f;
-#pragma unroll
-                for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float e = __builtin_amdgcn_exp2f(x[kb][i] - m_use);
-                        x[kb][i] = e;
-                        ls += e;
-                    }
-                }
-                l_run[b] += ls;
-#pragma unroll
-                for (int cc = 0; cc < BN / 32; ++cc) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        pf[b][cc][i] = static_cast<T>(x[2 * cc][i]);
-                        pf[b][cc][4 + i] = static_cast<T>(x[2 * cc + 1][i]);
-                    }
+                    for (int i = 0; i < 4; ++i) x[kb][i] = 16 * kb + i < rel ? x[kb][i] : -INFINITY;
                 }
             }
+            float mt = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                             fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+            mt = row_max4(mt) * xs;
+            // Lazy rescale: the reference point moves only when a score would exceed it by
+            // more than 2^8 (P stays <= 256, exact in bf16's exponent range); O and l are
+            // rescaled only then, skipped when no row of the wavefront moved.
+            const bool move = mt > m_run[b] + kLazy;
+            float alpha = 1.f;
+            if (move) {
+                alpha = __builtin_amdgcn_exp2f(m_run[b] - mt);
+                m_run[b] = mt;
+            }
+            const float neg_m = m_run[b] == -INFINITY ? 0.f : -m_run[b];
+            if (__builtin_amdgcn_ballot_w64(move)) {
+                l_run[b] *= alpha;
 #pragma unroll
-            for (int d = 0; d < DB; ++d) {
+                for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
+            }
+            float ls = 0.f;
 #pragma unroll
-                for (int cc = 0; cc < BN / 32; ++cc) {
-                    const v8 a = *reinterpret_cast<const v8*>(vl + (16 * d + l16) * VP + 32 * cc + 8 * g4);
+            for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                    for (int b = 0; b < NQB; ++b) o[d][b] = Mfma<T>::run(a, pf[b][cc], o[d][b]);
+                for (int i = 0; i < 4; ++i) {
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kb][i], xs, neg_m));
+                    x[kb][i] = e;
+                    ls += e;
                 }
+            }
+            l_run[b] += ls;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pf[b][i] = static_cast<T>(x[0][i]);
+                pf[b][4 + i] = static_cast<T>(x[1][i]);
             }
         }
-        if (has_next) store_tile(buf ^ 1);
-        __syncthreads();
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            const v8 a = *reinterpret_cast<const v8*>(vl + (16 * d + l16) * VP + 8 * g4);
+#pragma unroll
+            for (int b = 0; b < NQB; ++b)
+                if (r_begin + 16 * b < r_end) o[d][b] = Mfma<T>::run(a, pf[b], o[d][b]);
+        }
     }
 
-    if (!wave_active) return;
-    // Epilogue: l across the four lanes of a row, then O / l (or the split partial).
+    // Merge the wavefronts' states.  Row stats first: (m, l, raw) per wavefront and row.
+    __syncthreads();  // every wavefront is done with its tile buffer
+    float* stats = reinterpret_cast<float*>(smem + S::template lds_bytes<T>() - NWAVES * BM * 3 * sizeof(float));
+    float* comb = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
-        float l = l_run[b];
-        l += __shfl_xor(l, 16, kWave);
-        l += __shfl_xor(l, 32, kWave);
-        if (!valid[b]) continue;
-        const float inv = l > 0.f ? 1.f / l : 0.f;
-        const float lse2 = l > 0.f ? m_run[b] + log2f(l) : -INFINITY;
+        const float l = row_sum4(l_run[b]);
+        l_run[b] = l;
+        if (g4 == 0) {
+            float* st = stats + 3 * (wave * BM + 16 * b + l16);
+            st[0] = m_run[b];
+            st[1] = l;
+            st[2] = raw[b] ? 1.f : 0.f;
+        }
+    }
+    __syncthreads();
+    // Wavefronts in masked mode (they met a kept key) win; a row none of them kept a key
+    // for merges every wavefront's raw-score state.  Each wavefront scales its O by
+    // 2^(m_w - m) / l and writes it; the sum below runs in a fixed order.
+    float row_lse[NQB];
+    bool row_raw[NQB];
+#pragma unroll
+    for (int b = 0; b < NQB; ++b) {
+        const int row = 16 * b + l16;
+        bool any_masked = false;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+            const float* st = stats + 3 * (w * BM + row);
+            if (st[2] == 0.f && st[1] > 0.f) any_masked = true;
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+            const float* st = stats + 3 * (w * BM + row);
+            if ((!any_masked || st[2] == 0.f) && st[1] > 0.f) m = fmaxf(m, st[0]);
+        }
+        float lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+            const float* st = stats + 3 * (w * BM + row);
+            if ((!any_masked || st[2] == 0.f) && st[1] > 0.f) lt += st[1] * __builtin_amdgcn_exp2f(st[0] - m);
+        }
+        const bool mine = (!any_masked || !raw[b]) && l_run[b] > 0.f;
+        const float f = (mine && lt > 0.f) ? __builtin_amdgcn_exp2f(m_run[b] - m) / lt : 0.f;
+        row_lse[b] = lt > 0.f ? m + log2f(lt) : -INFINITY;
+        row_raw[b] = !any_masked && MASKED;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+            *reinterpret_cast<f32x4*>(comb + (wave * BM + row) * CP + 16 * d + 4 * g4) = o[d][b] * f;
+    }
+    __syncthreads();
+    // Output: thread -> (row, 4 consecutive head-dim columns), summed over wavefronts.
+    constexpr int VPRO = D / 4;  // float4 columns per row
+    for (int idx = tid; idx < BM * VPRO; idx += NTHREADS) {
+        const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
+        const int r = r_begin + row;
+        if (r >= r_end) continue;
+        f32x4 acc = *reinterpret_cast<const f32x4*>(comb + row * CP + col);
+#pragma unroll
+        for (int w = 1; w < NWAVES; ++w) acc += *reinterpret_cast<const f32x4*>(comb + (w * BM + row) * CP + col);
+        const int pos = r / G;
+        const int head = kvh * G + (r - pos * G);
         if (p.splits > 1) {
-            const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos[b]) * p.hq + head[b];
-            float* dst = p.part_o + prow * D;
-#pragma unroll
-            for (int d = 0; d < DB; ++d) {
-                *reinterpret_cast<f32x4*>(dst + 16 * d + 4 * g4) = o[d][b] * inv;
-            }
-            if (g4 == 0) {
-                p.part_lse[2 * prow] = lse2;
-                p.part_lse[2 * prow + 1] = raw[b] ? 1.f : 0.f;
-            }
+            const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
+            *reinterpret_cast<f32x4*>(p.part_o + prow * D + col) = acc;
         } else {
-            T* dst = static_cast<T*>(p.out) + ob_off + head[b] * p.os[1] + static_cast<int64_t>(q0 + pos[b]) * p.os[2];
+            typedef T v4 __attribute__((ext_vector_type(4)));
+            v4 w;
 #pragma unroll
-            for (int d = 0; d < DB; ++d) {
-                typedef T v4 __attribute__((ext_vector_type(4)));
-                v4 w;
+            for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(acc[i]);
+            T* dst = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2];
+            *reinterpret_cast<v4*>(dst + col) = w;
+        }
+    }
+    // Row statistics: the lanes of group 0 of wavefront 0 own rows 16 b + l16.
+    if (wave == 0 && g4 == 0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(o[d][b][i] * inv);
-                *reinterpret_cast<v4*>(dst + 16 * d + 4 * g4) = w;
+        for (int b = 0; b < NQB; ++b) {
+            const int r = r_begin + 16 * b + l16;
+            if (r >= r_end) continue;
+            const int pos = r / G;
+            const int head = kvh * G + (r - pos * G);
+            if (p.splits > 1) {
+                const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
+                p.part_lse[2 * prow] = row_lse[b];
+                p.part_lse[2 * prow + 1] = row_raw[b] ? 1.f : 0.f;
+            } else if (p.lse) {
+                p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] = row_lse[b] * kLn2;
             }
-            if (p.lse && g4 == 0)
-                p.lse[lb_off + head[b] * p.ls[1] + static_cast<int64_t>(q0 + pos[b]) * p.ls[2]] = lse2 * kLn2;
         }
     }
 }
@@ -522,9 +620,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
             wsum > 0.f ? (m + log2f(wsum)) * kLn2 : -INFINITY;
 }
 
-constexpr size_t lds_bytes(int d, size_t elem) {
-    return (2 * BN * (d + 8) + 2 * d * (BN + 8)) * elem;
-}
 
 struct Plan {
     int nqb, nx, splits, tiles_per_split;
@@ -565,9 +660,9 @@ const char* check_args(const kmi_attn_args* a) {
     return nullptr;
 }
 
-// KMI_ATTN_NQB=1|2|4 (read once) pins the 16-row blocks per wavefront; otherwise the
-// plan takes the most rows per wavefront (fewer LDS reads per MFMA: a wavefront reads each
-// K/V tile once for all its rows) that still gives every CU a workgroup.
+// KMI_ATTN_NQB=1|2|4 (read once) pins the 16-row blocks of a workgroup; by default a
+// workgroup holds 64 rows for head dim 64 and 32 for 128 (its wavefronts read each K/V
+// tile once for all those rows: 4 * rows FLOPs per LDS byte).
 int nqb_override() {
     static const int v = [] {
         const char* e = std::getenv("KMI_ATTN_NQB");
@@ -581,24 +676,19 @@ Plan make_plan(const kmi_attn_args* a) {
     const int64_t G = a->heads_q / a->heads_kv;
     const int64_t vrows = a->seq_q * G;
     const int64_t units = a->batch * a->heads_kv;
-    const int max_nqb = a->head_dim == 64 ? 4 : 2;
-    int nqb = 1;
-    for (int n = max_nqb; n >= 1; n /= 2) {
-        if (ceil_div(vrows, 64 * n) * units >= 256 || n == 1) {
-            nqb = n;
-            break;
-        }
-    }
+    int nqb = a->head_dim == 64 ? 4 : 2;
     const int forced = nqb_override();
     if (forced == 1 || forced == 2 || (forced == 4 && a->head_dim == 64)) nqb = forced;
     pl.nqb = nqb;
-    const int64_t bm = 64 * pl.nqb;
+    const int64_t bm = 16 * pl.nqb;
     pl.nx = static_cast<int>(ceil_div(vrows, bm));
-    const int64_t nk = ceil_div(a->seq_k, BN);
+    const int64_t nk = ceil_div(a->seq_k, WN);
     const int64_t base = static_cast<int64_t>(pl.nx) * units;
+    // Split the keys across workgroups when the query tiles alone leave most CUs idle
+    // (decode): at least 8 tiles (two per wavefront) per split.
     int64_t splits = 1;
     if (a->num_splits == 0) {
-        if (base < 128 && nk >= 8) splits = std::min<int64_t>(ceil_div(512, base), nk / 2);
+        if (base < 128 && nk >= 16) splits = std::min<int64_t>(ceil_div(512, base), nk / 8);
     } else {
         splits = std::max<int64_t>(1, std::min<int64_t>(a->num_splits, nk));
     }
@@ -619,7 +709,7 @@ template <typename T, int D, int NQB, int MK>
 hipError_t launch_fwd(const AttnParams& p, int64_t grid, hipStream_t stream) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
-    const size_t lds = lds_bytes(D, sizeof(T));
+    const size_t lds = Shape<D, NQB>::template lds_bytes<T>();
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));

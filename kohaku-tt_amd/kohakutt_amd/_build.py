@@ -43,6 +43,9 @@ HIP_FLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
     f"-I{INCLUDE}",
+    # MFMA accumulators in VGPRs (no AGPR <-> VGPR copies around the softmax).
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 
 
