@@ -14,22 +14,30 @@
 //     query r sees min(Lk, r + 1 + Lk - Lq) keys (varlen_plan.hpp:43-82).
 //
 // MI355X design (not the reference's Tensix reader/compute/writer split):
-//   - a 256-thread workgroup (4 wavefronts) owns BM = 64 * NQB "virtual rows" of one
+//   - a 256-thread workgroup (4 wavefronts) owns 16 * NQB "virtual rows" of one
 //     (sequence, K/V head): row r is query position r / G of query head kvh * G + r % G,
-//     so the G query heads of a GQA group share every K/V tile it stages in LDS;
+//     so the G query heads of a GQA group share every K/V tile;
+//   - the four wavefronts hold the same rows and split the key range (every fourth 32-key
+//     tile), each staging its own tiles global -> registers -> its own LDS region one tile
+//     ahead, so no block-wide barrier runs per tile; their online-softmax states are merged
+//     once at the end, in LDS, in a fixed order (deterministic);
 //   - S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_{bf16,f16}: with that
 //     orientation the S accumulator of a lane is already the B operand of the PV product
 //     (no cross-lane shuffles), and each lane owns one query row for the softmax state;
-//   - K tiles are stored row-major, V tiles transposed (with the key order the MFMA
-//     operand expects), both padded against LDS bank conflicts, double-buffered through
-//     registers so the next tile's HBM reads overlap this tile's MFMAs;
+//   - K and V tiles sit in LDS in their natural row layout (padded against bank conflicts);
+//     the V^T operand comes from gfx950's transposed LDS read;
+//   - the softmax runs on the raw accumulators (scale folded into the exponent's FMA),
+//     reduces rows with permlane swaps, and rescales O lazily;
 //   - causal work skips key tiles past the tile's last query and issues the heaviest
-//     query tiles first; masking is per element only on tiles that need it.
+//     query tiles first; causal / tail masking runs only on the tiles that need it;
+//   - decode-shaped calls split the key range across workgroups (fp32 partials merged by
+//     a second kernel).
 #include "common.hpp"
 
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 namespace kmi {
 namespace {
@@ -105,11 +113,38 @@ __device__ __forceinline__ float mask_value(const void* m, int64_t i) {
     }
 }
 
-// Position of key `kk` (0..31) in a transposed V row: within each 32-key chunk the
-// MFMA B operand of lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3 as slots 8g..8g+7.
-__device__ __forceinline__ int vpos(int kk) {
-    const int c = kk & 31;
-    return (kk & ~31) + 8 * ((c & 15) >> 2) + ((c >> 4) << 2) + (c & 3);
+// A prefetched mask element in logit units, clamped at the masked logit.
+template <int MK, typename R>
+__device__ __forceinline__ float mask_logit_of(R raw) {
+    if constexpr (MK == MK_BOOL) {
+        return raw ? 0.f : kMaskedLogit;
+    } else if constexpr (MK == MK_BF16) {
+        return fmaxf(to_f32(__builtin_bit_cast(bf16, raw)), kMaskedLogit);
+    } else if constexpr (MK == MK_F16) {
+        return fmaxf(to_f32(__builtin_bit_cast(f16, raw)), kMaskedLogit);
+    } else {
+        return fmaxf(static_cast<float>(raw), kMaskedLogit);
+    }
+}
+
+// V^T fragments come from V tiles kept in their natural [key][dim] layout through the
+// gfx950 transposed LDS read: within each 16-lane group, output lane j, slot s receives
+// element j % 4 of the 4-element chunk that source lane 4 s + j / 4 addressed.  Source lane
+// k of group g pointing at V[key(g, k / 4)][dim0 + 4 (k % 4)] therefore delivers
+// V[key(g, s)][dim0 + j] to lane j, slot s: the A operand of O^T = V^T P^T.
+template <typename T>
+__device__ __forceinline__ u32x2 lds_read_tr(const T* p) {
+    if constexpr (std::is_same<T, bf16>::value) {
+        typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+        const auto v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (__attribute__((address_space(3))) bf16x4_t*)(const_cast<T*>(p)));
+        return __builtin_bit_cast(u32x2, v);
+    } else {
+        typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 f16x4_t;
+        const auto v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (__attribute__((address_space(3))) f16x4_t*)(const_cast<T*>(p)));
+        return __builtin_bit_cast(u32x2, v);
+    }
 }
 
 // Keys per wavefront tile.
@@ -117,11 +152,11 @@ constexpr int WN = 32;
 
 template <int D, int NQB>
 struct Shape {
-    static constexpr int BM = 16 * NQB;        // rows of a workgroup (shared by its wavefronts)
-    static constexpr int KP = D + 8;           // K tile row pitch (elements)
-    static constexpr int VP = WN + 8;          // V^T tile row pitch (elements)
-    static constexpr int TILE = WN * KP + D * VP;  // elements of one wavefront's K + V^T tile
-    static constexpr int CP = D + 4;           // combine buffer row pitch (floats)
+    static constexpr int BM = 16 * NQB;  // rows of a workgroup (shared by its wavefronts)
+    static constexpr int KP = D + 8;     // K row pitch (elements): b128 reads of 16 rows hit distinct banks
+    static constexpr int VP = D + 16;    // V row pitch (elements): transposed b64 reads of 8 rows hit distinct banks
+    static constexpr int TILE = WN * KP + WN * VP;  // elements of one wavefront's K + V tile
+    static constexpr int CP = D + 4;     // merge buffer row pitch (floats)
     template <typename T>
     static constexpr size_t lds_bytes() {
         const size_t tiles = static_cast<size_t>(NWAVES) * TILE * sizeof(T);
@@ -130,11 +165,6 @@ struct Shape {
     }
 };
 
-// One workgroup owns BM rows of one (sequence, K/V head) and a key range; its four
-// wavefronts hold the same rows and take every fourth 32-key tile of the range, each
-// staging its own tiles (global -> registers -> its own LDS tile, one tile ahead) so no
-// block-wide barrier runs per tile.  The wavefronts' softmax states are merged once, in
-// LDS, in a fixed order.
 // Reductions over the four lanes that hold one query row (l, l^16, l^32, l^48): the
 // gfx950 row swaps exchange 16-lane rows (permlane16) and 32-lane halves (permlane32) in
 // registers, without the LDS crossbar a generic shuffle uses.
@@ -169,8 +199,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     constexpr int VPR = D / 8;           // 16-byte vectors per key row
     constexpr int RPP = kWave / VPR;     // key rows one wavefront pass covers
     constexpr int KIT = WN / RPP;        // K passes per tile
-    constexpr int VIT = WN / (2 * RPP);  // V passes per tile (two keys per lane)
-    static_assert(KIT >= 1 && VIT >= 1 && WN % (2 * RPP) == 0, "tile shape");
+    static_assert(KIT >= 1 && WN % RPP == 0, "tile shape");
     constexpr bool MASKED = MK != MK_NONE;
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -277,55 +306,61 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
     const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
     const T* kbase = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * ks2 + 8 * dg;
-    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + 2 * krow) * vs2 + 8 * dg;
+    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + krow) * vs2 + 8 * dg;
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
     T* vl = kl + WN * KP;
 
+    // Mask values of the staged tile, loaded with its K / V (raw element type; converted
+    // when the tile is computed, so the loads stay in flight meanwhile).
+    typedef typename std::conditional<MK == MK_BOOL, uint8_t,
+            typename std::conditional<MK == MK_BF16 || MK == MK_F16, uint16_t, float>::type>::type MRaw;
+    MRaw mpre[MASKED ? NQB : 1][KB][4];
+
     u32x4 kreg[KIT];
-    u32x4 vreg[VIT][2];
+    u32x4 vreg[KIT];
     auto load_tile = [&](int t) {
         const int key0 = t * WN;
         const T* ksrc = kbase + static_cast<int64_t>(key0) * ks2;
         const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
         if (key0 + WN <= lk) {
 #pragma unroll
-            for (int i = 0; i < KIT; ++i) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
-#pragma unroll
-            for (int i = 0; i < VIT; ++i) {
-                vreg[i][0] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPP) * vs2);
-                vreg[i][1] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPP + 1) * vs2);
+            for (int i = 0; i < KIT; ++i) {
+                kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
+                vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < KIT; ++i) {
                 kreg[i] = u32x4{0u, 0u, 0u, 0u};
-                if (key0 + krow + i * RPP < lk) kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
+                vreg[i] = u32x4{0u, 0u, 0u, 0u};
+                if (key0 + krow + i * RPP < lk) {
+                    kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
+                    vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
+                }
             }
+        }
+        if constexpr (MASKED) {
+            const MRaw* mp = static_cast<const MRaw*>(mptr);
 #pragma unroll
-            for (int i = 0; i < VIT; ++i) {
+            for (int b = 0; b < NQB; ++b) {
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    vreg[i][e] = u32x4{0u, 0u, 0u, 0u};
-                    if (key0 + 2 * (krow + i * RPP) + e < lk)
-                        vreg[i][e] = *reinterpret_cast<const u32x4*>(vsrc + (2 * i * RPP + e) * vs2);
+                for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kk = key0 + 16 * kb + 4 * g4 + i;
+                        const int64_t mi = mrow[b] + kk * m_key;
+                        mpre[b][kb][i] = (kk < lk && mi < m_end) ? mp[mi] : MRaw{};
+                    }
                 }
             }
         }
     };
-    // K rows as loaded; V transposed, keys in the order the PV B operand expects.
+    // K and V rows as loaded.
     auto store_tile = [&]() {
 #pragma unroll
-        for (int i = 0; i < KIT; ++i) *reinterpret_cast<u32x4*>(kl + (krow + i * RPP) * KP + 8 * dg) = kreg[i];
-#pragma unroll
-        for (int i = 0; i < VIT; ++i) {
-            const int col = vpos(2 * (krow + i * RPP));
-            const uint16_t* a = reinterpret_cast<const uint16_t*>(&vreg[i][0]);
-            const uint16_t* b = reinterpret_cast<const uint16_t*>(&vreg[i][1]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t pair = static_cast<uint32_t>(a[e]) | (static_cast<uint32_t>(b[e]) << 16);
-                *reinterpret_cast<uint32_t*>(vl + (8 * dg + e) * VP + col) = pair;
-            }
+        for (int i = 0; i < KIT; ++i) {
+            *reinterpret_cast<u32x4*>(kl + (krow + i * RPP) * KP + 8 * dg) = kreg[i];
+            *reinterpret_cast<u32x4*>(vl + (krow + i * RPP) * VP + 8 * dg) = vreg[i];
         }
     };
 
@@ -342,26 +377,94 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     }
     const float c2 = p.scale_log2;
 
-    const int t_first = t_begin + wave;
-    if (t_first < t_end) load_tile(t_first);
-    for (int t = t_first; t < t_end; t += NWAVES) {
+    // Key-mask tile skipping: with a mask that depends only on the key (a padding mask),
+    // tiles whose every key is masked contribute exactly nothing once the row is known to
+    // keep a key somewhere, so they are neither loaded nor computed.  A scan of the whole
+    // mask row establishes that first (a row with no kept key needs every raw score).
+    constexpr int FLAG_CAP = NWAVES * BM * 3 * static_cast<int>(sizeof(float));
+    uint8_t* tflag = smem + S::template lds_bytes<T>() - FLAG_CAP;
+    bool skip = false;
+    if constexpr (MASKED) {
+        constexpr int EPV = 16 / static_cast<int>(sizeof(MRaw));
+        const int ntl = t_end - t_begin;
+        const MRaw* mrow0 = static_cast<const MRaw*>(mptr) + mrow[0];
+        // Uniform across the workgroup: with zero head and query strides every row of the
+        // workgroup reads the same mask row.
+        const bool eligible = p.mask_mode == KMI_MASK_STRIDED && p.ms[1] == 0 && p.ms[2] == 0 &&
+                              m_key == 1 && ntl > 0 && ntl <= FLAG_CAP && lk % EPV == 0 &&
+                              (reinterpret_cast<uintptr_t>(mrow0) & 15) == 0;
+        if (eligible) {
+            for (int i = tid; i < ntl; i += NTHREADS) tflag[i] = 0;
+            __syncthreads();
+            bool keeps = false;
+            const int nv = lk / EPV;
+            for (int v0 = tid; v0 < nv; v0 += 2 * NTHREADS) {
+                u32x4 raw2[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int v = v0 + u * NTHREADS;
+                    raw2[u] = v < nv ? *reinterpret_cast<const u32x4*>(mrow0 + static_cast<int64_t>(v) * EPV)
+                                     : u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int v = v0 + u * NTHREADS;
+                    if (v >= nv) continue;
+                    const MRaw* e = reinterpret_cast<const MRaw*>(&raw2[u]);
+#pragma unroll
+                    for (int j = 0; j < EPV; ++j) {
+                        if (mask_logit_of<MK>(e[j]) > kMaskedLogit) {
+                            keeps = true;
+                            const int tile = (v * EPV + j) / WN;
+                            if (tile >= t_begin && tile < t_end) tflag[tile - t_begin] = 1;
+                        }
+                    }
+                }
+            }
+            skip = __syncthreads_or(keeps);
+        }
+    }
+    auto next_tile = [&](int t) {
+        if (skip) {
+            while (t < t_end && !tflag[t - t_begin]) t += NWAVES;
+        }
+        return t;
+    };
+
+    int t = next_tile(t_begin + wave);
+    if (t < t_end) load_tile(t);
+    while (t < t_end) {
         // The previous tile's LDS reads were issued before these writes; LDS runs one
         // wavefront's instructions in order, so only the compiler must keep the order.
         __asm__ volatile("" ::: "memory");
         store_tile();
+        MRaw mcur[MASKED ? NQB : 1][KB][4];
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int b = 0; b < NQB; ++b)
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mcur[b][kb][i] = mpre[b][kb][i];
+        }
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (t + NWAVES < t_end) load_tile(t + NWAVES);
+        const int t_next = next_tile(t + NWAVES);
+        if (t_next < t_end) load_tile(t_next);
+        // S^T = K Q^T: every K fragment of the tile first, then the MFMAs.
+        v8 kf[KB][DC];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+            for (int c = 0; c < DC; ++c) kf[kb][c] = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
+        }
         f32x4 s[KB][NQB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-            for (int b = 0; b < NQB; ++b) s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int b = 0; b < NQB; ++b) {
+                s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                const v8 a = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
-#pragma unroll
-                for (int b = 0; b < NQB; ++b)
-                    if (r_begin + 16 * b < r_end) s[kb][b] = Mfma<T>::run(a, qf[b][c], s[kb][b]);
+                for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
             }
         }
         const int key0 = t * WN;
@@ -369,7 +472,6 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         v8 pf[NQB];
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            if (r_begin + 16 * b >= r_end) continue;
             // x: logits in base-2 units.  Mask-free rows keep the raw accumulators (the
             // scale is folded into the exponent's FMA below), -inf where not visible.
             float x[KB][4];
@@ -389,12 +491,10 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const bool vis = 16 * kb + i < rel;
-                        const int kk = key0 + 16 * kb + 4 * g4 + i;
                         float val = x[kb][i] * c2;
                         float vm = -INFINITY;
                         if (vis) {
-                            const int64_t mi = mrow[b] + kk * m_key;
-                            const float ml = mi < m_end ? mask_value<MK>(mptr, mi) : kMaskedLogit;
+                            const float ml = mask_logit_of<MK>(mcur[b][kb][i]);
                             if (ml > kMaskedLogit) {
                                 vm = val + kLog2e * ml;
                                 keep_any = true;
@@ -463,13 +563,23 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                 pf[b][4 + i] = static_cast<T>(x[1][i]);
             }
         }
+        // O^T += V^T P^T.
+        v8 vf[DB];
+        {
+            const T* vsrc = vl + (4 * g4 + (l16 >> 2)) * VP + 4 * (l16 & 3);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                const u32x2 lo = lds_read_tr(vsrc + 16 * d);            // keys 4 g + s
+                const u32x2 hi = lds_read_tr(vsrc + 16 * VP + 16 * d);  // keys 16 + 4 g + s
+                vf[d] = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            }
+        }
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
-            const v8 a = *reinterpret_cast<const v8*>(vl + (16 * d + l16) * VP + 8 * g4);
 #pragma unroll
-            for (int b = 0; b < NQB; ++b)
-                if (r_begin + 16 * b < r_end) o[d][b] = Mfma<T>::run(a, pf[b], o[d][b]);
+            for (int b = 0; b < NQB; ++b) o[d][b] = Mfma<T>::run(vf[d], pf[b], o[d][b]);
         }
+        t = t_next;
     }
 
     // Merge the wavefronts' states.  Row stats first: (m, l, raw) per wavefront and row.
@@ -565,7 +675,10 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     }
 }
 
-// Merge of split-KV partials: one wavefront per (query row, head), lanes over D.
+// Merge of split-KV partials: one wavefront per (query row, head); lanes over splits for
+// the statistics, over head-dim columns for O (every split's loads independent).
+// Splits in masked mode (they met a kept key) win; a row with no kept key in any split
+// merges the raw-score partials of every split.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     const int lane = threadIdx.x & 63;
@@ -573,35 +686,87 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     if (item >= p.rows_total * p.hq) return;
     const int64_t row = item / p.hq;
     const int h = static_cast<int>(item % p.hq);
-    // Splits in masked mode (they met a kept key) win; a row with no kept key in any
-    // split merges the raw-score partials of every split.
     const int64_t stride = p.rows_total * p.hq;
-    bool any_masked = false;
-    for (int s = 0; s < p.splits; ++s) {
-        const float* e = p.part_lse + 2 * (s * stride + item);
-        if (e[1] == 0.f && e[0] != -INFINITY) any_masked = true;
-    }
-    float m = -INFINITY;
-    for (int s = 0; s < p.splits; ++s) {
-        const float* e = p.part_lse + 2 * (s * stride + item);
-        if (!any_masked || e[1] == 0.f) m = fmaxf(m, e[0]);
-    }
     constexpr int PER = D / 64;
     float acc[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) acc[j] = 0.f;
-    float wsum = 0.f;
-    if (m != -INFINITY) {
-        for (int s = 0; s < p.splits; ++s) {
-            const int64_t idx = s * stride + item;
-            const float* e = p.part_lse + 2 * idx;
-            if (any_masked && e[1] != 0.f) continue;
-            const float w = __builtin_amdgcn_exp2f(e[0] - m);
-            wsum += w;
-            const float* src = p.part_o + idx * D;
-#pragma unroll
-            for (int j = 0; j < PER; ++j) acc[j] += w * src[lane + 64 * j];
+    float m = -INFINITY, wsum = 0.f;
+    if (p.splits <= 32) {
+        // Every split's statistics (lane s) and O values in one round of loads.
+        float lse = -INFINITY, flag = 1.f;
+        if (lane < p.splits) {
+            const float* e = p.part_lse + 2 * (lane * stride + item);
+            lse = e[0];
+            flag = e[1];
         }
+        float v[32][PER];
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const float* src = p.part_o + (min(k, p.splits - 1) * stride + item) * D;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) v[k][j] = src[lane + 64 * j];
+        }
+        const bool any_masked = __builtin_amdgcn_ballot_w64(lane < p.splits && flag == 0.f && lse != -INFINITY) != 0;
+        if (any_masked && flag != 0.f) lse = -INFINITY;
+        m = wave_max(lse);
+        const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(lse - m);
+        wsum = wave_sum(w);
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            if (k >= p.splits) break;
+            const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k));
+#pragma unroll
+            for (int j = 0; j < PER; ++j) acc[j] += wk * v[k][j];
+        }
+    } else {
+    // Splits go 64 at a time: lane s holds split s0 + s's statistics (read once).
+    bool any_masked = false;
+    for (int s0 = 0; s0 < p.splits; s0 += kWave) {
+        const int s = s0 + lane;
+        if (s < p.splits) {
+            const float* e = p.part_lse + 2 * (s * stride + item);
+            if (e[1] == 0.f && e[0] != -INFINITY) any_masked = true;
+        }
+    }
+    any_masked = __builtin_amdgcn_ballot_w64(any_masked) != 0;
+    for (int s0 = 0; s0 < p.splits; s0 += kWave) {
+        const int s = s0 + lane;
+        float lse = -INFINITY;
+        if (s < p.splits) {
+            const float* e = p.part_lse + 2 * (s * stride + item);
+            if (!any_masked || e[1] == 0.f) lse = e[0];
+        }
+        const float m_chunk = wave_max(lse);
+        const float m_new = fmaxf(m, m_chunk);
+        if (m_new == -INFINITY) continue;
+        const float rescale = __builtin_amdgcn_exp2f(m - m_new);  // 0 while m was -inf
+        wsum *= rescale;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) acc[j] *= rescale;
+        m = m_new;
+        const float w = __builtin_amdgcn_exp2f(lse - m);
+        wsum += wave_sum(w);
+        const int n = min(kWave, p.splits - s0);
+        // Eight splits' O rows in flight at a time.
+        for (int k0 = 0; k0 < n; k0 += 8) {
+            float v[8][PER];
+            float wk[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int k = min(k0 + u, n - 1);
+                wk[u] = k0 + u < n ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k)) : 0.f;
+                const float* src = p.part_o + ((s0 + k) * stride + item) * D;
+#pragma unroll
+                for (int j = 0; j < PER; ++j) v[u][j] = src[lane + 64 * j];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                for (int j = 0; j < PER; ++j) acc[j] += wk[u] * v[u][j];
+            }
+        }
+    }
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
     int seq = 0, posn = static_cast<int>(row);
@@ -619,7 +784,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
         p.lse[lb_off + h * p.ls[1] + static_cast<int64_t>(posn) * p.ls[2]] =
             wsum > 0.f ? (m + log2f(wsum)) * kLn2 : -INFINITY;
 }
-
 
 struct Plan {
     int nqb, nx, splits, tiles_per_split;
@@ -677,6 +841,13 @@ Plan make_plan(const kmi_attn_args* a) {
     const int64_t vrows = a->seq_q * G;
     const int64_t units = a->batch * a->heads_kv;
     int nqb = a->head_dim == 64 ? 4 : 2;
+    // Fewer rows per workgroup when the larger tile would leave under two workgroups per
+    // CU, and short query tiles (decode: Sq x G rows per K/V head) take only what they have.
+    if (nqb == 4 && ceil_div(vrows, 64) * units < 512) nqb = 2;
+    while (nqb > 1 && vrows <= 16 * (nqb / 2)) nqb /= 2;
+    // Masked variants carry the prefetched mask values: one row block fewer keeps them
+    // at two wavefronts per SIMD.
+    if (a->mask_mode != KMI_MASK_NONE) nqb = std::min(nqb, a->head_dim == 64 ? 2 : 1);
     const int forced = nqb_override();
     if (forced == 1 || forced == 2 || (forced == 4 && a->head_dim == 64)) nqb = forced;
     pl.nqb = nqb;
@@ -685,10 +856,10 @@ Plan make_plan(const kmi_attn_args* a) {
     const int64_t nk = ceil_div(a->seq_k, WN);
     const int64_t base = static_cast<int64_t>(pl.nx) * units;
     // Split the keys across workgroups when the query tiles alone leave most CUs idle
-    // (decode): at least 8 tiles (two per wavefront) per split.
+    // (decode): about two workgroups per CU, at least one tile per wavefront per split.
     int64_t splits = 1;
     if (a->num_splits == 0) {
-        if (base < 128 && nk >= 16) splits = std::min<int64_t>(ceil_div(512, base), nk / 8);
+        if (base < 128 && nk >= 8) splits = std::min<int64_t>(ceil_div(512, base), nk / NWAVES);
     } else {
         splits = std::max<int64_t>(1, std::min<int64_t>(a->num_splits, nk));
     }
