@@ -121,12 +121,17 @@ Tensor kernel_operand(const Tensor& t) {
     return ok ? t : t.contiguous();
 }
 
-// The mask as a 4-D strided view broadcast to [B, H, Sq, Sk] (broadcast dims stride 0).
+// The mask as a 4-D strided view broadcast to [B, H, Sq, Sk]; every dim of size 1 gets
+// stride 0 (the kernels recognise a key-only padding mask by zero head and query strides).
 Tensor mask_operand(const Tensor& m, const Tensor& q, int64_t sk) {
     Tensor x = m;
     if (x.scalar_type() == at::kDouble) x = x.to(at::kFloat);
     while (x.dim() < 4) x = x.unsqueeze(0);
-    return x.expand({q.size(0), q.size(1), q.size(2), sk});
+    x = x.expand({q.size(0), q.size(1), q.size(2), sk});
+    std::vector<int64_t> strides(x.strides().begin(), x.strides().end());
+    for (int i = 0; i < 4; ++i)
+        if (x.size(i) == 1) strides[i] = 0;
+    return x.as_strided(x.sizes(), strides);
 }
 
 struct AttnOut {
