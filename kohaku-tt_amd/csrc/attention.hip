@@ -377,6 +377,11 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     }
     const float c2 = p.scale_log2;
 
+    // Each wavefront's first tile is requested before anything else waits on memory (its
+    // loads share one round trip with the Q fragments and the mask-row scan below).
+    const int t_spec = t_begin + wave;
+    if (t_spec < t_end) load_tile(t_spec);
+
     // Key-mask tile skipping: with a mask that depends only on the key (a padding mask),
     // tiles whose every key is masked contribute exactly nothing once the row is known to
     // keep a key somewhere, so they are neither loaded nor computed.  A scan of the whole
@@ -431,8 +436,8 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         return t;
     };
 
-    int t = next_tile(t_begin + wave);
-    if (t < t_end) load_tile(t);
+    int t = next_tile(t_spec);
+    if (t != t_spec && t < t_end) load_tile(t);
     while (t < t_end) {
         // The previous tile's LDS reads were issued before these writes; LDS runs one
         // wavefront's instructions in order, so only the compiler must keep the order.
@@ -669,9 +674,404 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                 p.part_lse[2 * prow] = row_lse[b];
                 p.part_lse[2 * prow + 1] = row_raw[b] ? 1.f : 0.f;
             } else if (p.lse) {
-                p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] = row_lse[b] * kLn2;
+                // A row without a kept key: its logits all carry the -5e5 clamp.
+                p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] =
+                    row_lse[b] * kLn2 + (row_raw[b] ? kMaskedLogit : 0.f);
             }
         }
+    }
+}
+
+// Decode: at most 16 "virtual rows" (Sq x G) per (sequence, K/V head).  The key tiles of a
+// unit are dealt round-robin to its wavefronts (wavefront slot s of S takes tiles s, s + S,
+// ...): K goes straight from global memory into MFMA A-operand registers, V through a
+// per-wavefront LDS tile read transposed, with the next tile's loads in flight during the
+// softmax.  With a mask shared by the rows (a padding mask), tiles whose keys are all
+// masked are skipped once a kept key among the first 64 proves that no row is fully
+// masked (their keys then carry exactly zero weight).  The four wavefronts of a workgroup
+// merge their (m, l, O) in LDS and write one fp32 partial; attn_merge_kernel combines the
+// workgroups' partials.
+template <typename T, int D, int MK>
+__global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams p) {
+    typedef typename Mfma<T>::v8 v8;
+    constexpr int DC = D / 32;
+    constexpr int DB = D / 16;
+    constexpr int KB = WN / 16;
+    constexpr int VPR = D / 8;
+    constexpr int RPP = kWave / VPR;
+    constexpr int KIT = WN / RPP;
+    constexpr int VP = D + 16;
+    constexpr int CP = D + 4;
+    constexpr bool MASKED = MK != MK_NONE;
+    constexpr int SCAN = 8;  // mask loads per lane of the skip scan: up to 2 * SCAN tiles
+    typedef typename std::conditional<MK == MK_BOOL, uint8_t,
+            typename std::conditional<MK == MK_BF16 || MK == MK_F16, uint16_t, float>::type>::type MRaw;
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g4 = lane >> 4;
+    const int l16 = lane & 15;
+
+    const int wg_per_unit = p.splits;
+    const int bh = blockIdx.x / wg_per_unit;
+    const int split = blockIdx.x - bh * wg_per_unit;
+    const int nslots = wg_per_unit * NWAVES;
+    const int slot = split * NWAVES + wave;
+    const int seq = bh / p.hkv;
+    const int kvh = bh - seq * p.hkv;
+    const int G = p.group;
+
+    int q0 = 0, lq = p.seq_q, k0 = 0, lk = p.seq_k;
+    int64_t qb_off = seq * p.qs[0], kb_off = seq * p.ks[0], vb_off = seq * p.vs[0];
+    int64_t row_base = static_cast<int64_t>(seq) * p.seq_q;
+    if (p.cu_q) {
+        q0 = min(max(p.cu_q[seq], 0), p.total_q);
+        lq = min(max(p.cu_q[seq + 1], q0), p.total_q) - q0;
+        k0 = min(max(p.cu_k[seq], 0), p.total_k);
+        lk = min(max(p.cu_k[seq + 1], k0), p.total_k) - k0;
+        lq = min(lq, p.seq_q);
+        qb_off = kb_off = vb_off = 0;
+        row_base = q0;
+    }
+    // Uniform over the workgroup: an empty sequence leaves before any barrier.
+    const int vrows = min(lq * G, 16);
+    if (vrows <= 0) return;
+    const int coff = p.cu_q ? (lk - lq) : 0;
+    int kend = max(lk, 0);
+    if (p.causal) kend = max(0, min(lk, (vrows - 1) / G + 1 + coff));
+    const int ntiles = (kend + WN - 1) / WN;
+    const int n_t = slot < ntiles ? (ntiles - 1 - slot) / nslots + 1 : 0;  // this wavefront's tiles
+
+    // This lane's row.
+    const bool valid = l16 < vrows;
+    const int rr = valid ? l16 : 0;
+    const int pos = rr / G;
+    const int head = kvh * G + (rr - pos * G);
+    const int lim = p.causal ? min(lk, pos + coff + 1) : lk;
+    v8 qf[DC];
+    {
+        const T* src = static_cast<const T*>(p.q) + qb_off + head * p.qs[1] + static_cast<int64_t>(q0 + pos) * p.qs[2];
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+            if (valid) {
+                qf[c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qf[c][j] = static_cast<T>(0.f);
+            }
+        }
+    }
+    int64_t mrow = 0, m_key = 0, m_end = 0;
+    bool shared_row = false;
+    if constexpr (MASKED) {
+        const bool packed = p.mask_mode == KMI_MASK_PACKED;
+        m_end = packed ? p.mask_numel : INT64_MAX;
+        m_key = packed ? 1 : p.ms[3];
+        if (packed) {
+            int64_t m_seq = 0;
+            for (int s = 0; s < seq; ++s) {
+                const int a0 = min(max(p.cu_q[s], 0), p.total_q);
+                const int a1 = min(max(p.cu_q[s + 1], a0), p.total_q);
+                const int b0 = min(max(p.cu_k[s], 0), p.total_k);
+                const int b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
+                m_seq += static_cast<int64_t>(a1 - a0) * (b1 - b0);
+            }
+            mrow = m_seq + static_cast<int64_t>(pos) * lk;
+        } else {
+            const int64_t m_seq = p.cu_q ? (static_cast<int64_t>(q0) * p.ms[2] + static_cast<int64_t>(k0) * p.ms[3])
+                                         : seq * p.ms[0];
+            mrow = m_seq + head * p.ms[1] + static_cast<int64_t>(pos) * p.ms[2];
+        }
+        // Every row of the wavefront reads the same mask row.
+        shared_row = (lq == 1 || (!packed && p.ms[2] == 0)) && (G == 1 || packed || p.ms[1] == 0);
+    }
+
+    // Tiles this wavefront runs: bit i of `live` stands for tile slot + i * nslots.
+    uint32_t live = 0xffffffffu;
+    const bool use_bits = MASKED && shared_row && n_t <= 2 * SCAN;
+    if constexpr (MASKED) {
+        if (use_bits) {
+            const MRaw* mp = static_cast<const MRaw*>(p.mask);
+            const int lim0 = p.causal ? min(lk, coff + 1) : lk;
+            const int pk = lane;
+            const MRaw first = (pk < lim0 && mrow + pk * m_key < m_end) ? mp[mrow + pk * m_key] : MRaw{};
+            MRaw sv[SCAN];
+#pragma unroll
+            for (int j = 0; j < SCAN; ++j) {
+                const int i = 2 * j + (lane >> 5);
+                const int key = (slot + i * nslots) * WN + (lane & 31);
+                const int64_t mi = mrow + static_cast<int64_t>(key) * m_key;
+                sv[j] = (i < n_t && key < lk && mi < m_end) ? mp[mi] : MRaw{};
+            }
+            const bool proof = __builtin_amdgcn_ballot_w64(pk < lim0 && mask_logit_of<MK>(first) > kMaskedLogit) != 0;
+            if (proof) {
+                live = 0;
+#pragma unroll
+                for (int j = 0; j < SCAN; ++j) {
+                    const int i = 2 * j + (lane >> 5);
+                    const int key = (slot + i * nslots) * WN + (lane & 31);
+                    const uint64_t b = __builtin_amdgcn_ballot_w64(i < n_t && key < lk &&
+                                                                   mask_logit_of<MK>(sv[j]) > kMaskedLogit);
+                    live |= (static_cast<uint32_t>(b) != 0u ? 1u : 0u) << (2 * j);
+                    live |= (static_cast<uint32_t>(b >> 32) != 0u ? 1u : 0u) << (2 * j + 1);
+                }
+            }
+        }
+    }
+    auto next_i = [&](int i) -> int {  // the first tile index after i that runs
+        if (!use_bits) return i + 1;
+        const uint32_t rest = live & (0xfffffffeu << i);
+        return rest ? __builtin_ctz(rest) : n_t;
+    };
+
+    // K fragments of a tile come straight from memory: lane (g4, l16) holds key
+    // 16 kb + l16, dims 32 c + 8 g4 .. + 7 -- the A operand of S^T = K Q^T.
+    const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
+    const T* kq = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + l16) * ks2 + 8 * g4;
+    const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
+    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + krow) * vs2 + 8 * dg;
+    T* vl = reinterpret_cast<T*>(smem) + wave * WN * VP;
+
+    v8 kreg[KB][DC];
+    u32x4 vreg[KIT];
+    MRaw mpre[MASKED ? KB : 1][4];
+    auto load_tile = [&](int i) {
+        const int key0 = (slot + i * nslots) * WN;
+        const bool full = key0 + WN <= lk;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const bool ok = full || key0 + 16 * kb + l16 < lk;
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                if (ok) {
+                    kreg[kb][c] = *reinterpret_cast<const v8*>(kq + static_cast<int64_t>(key0 + 16 * kb) * ks2 + 32 * c);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) kreg[kb][c][j] = static_cast<T>(0.f);
+                }
+            }
+        }
+        const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
+#pragma unroll
+        for (int i2 = 0; i2 < KIT; ++i2) {
+            vreg[i2] = u32x4{0u, 0u, 0u, 0u};
+            if (full || key0 + krow + i2 * RPP < lk) vreg[i2] = *reinterpret_cast<const u32x4*>(vsrc + (i2 * RPP) * vs2);
+        }
+        if constexpr (MASKED) {
+            const MRaw* mp = static_cast<const MRaw*>(p.mask);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int kk = key0 + 16 * kb + 4 * g4 + j;
+                    const int64_t mi = mrow + kk * m_key;
+                    mpre[kb][j] = (kk < lk && mi < m_end) ? mp[mi] : MRaw{};
+                }
+            }
+        }
+    };
+
+    f32x4 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    bool raw = MASKED;
+    const float c2 = p.scale_log2;
+
+    int i = use_bits ? (live ? __builtin_ctz(live) : n_t) : 0;
+    if (i < n_t) load_tile(i);
+    while (i < n_t) {
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int i2 = 0; i2 < KIT; ++i2) *reinterpret_cast<u32x4*>(vl + (krow + i2 * RPP) * VP + 8 * dg) = vreg[i2];
+        MRaw mcur[MASKED ? KB : 1][4];
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) mcur[kb][j] = mpre[kb][j];
+        }
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        f32x4 sacc[KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < DC; ++c) sacc[kb] = Mfma<T>::run(kreg[kb][c], qf[c], sacc[kb]);
+        }
+        // The K fragments are consumed: the next tile's loads overlap the softmax and PV.
+        const int key0 = (slot + i * nslots) * WN;
+        i = next_i(i);
+        if (i < n_t) load_tile(i);
+        const int rel = lim - key0 - 4 * g4;
+        float x[KB][4];
+        float xs = c2;
+        if constexpr (MASKED) {
+            xs = 1.f;
+            bool keep_any = false;
+            float xm[KB][4];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool vis = 16 * kb + j < rel;
+                    const float val = vis ? sacc[kb][j] * c2 : -INFINITY;
+                    float vm = -INFINITY;
+                    if (vis) {
+                        const float ml = mask_logit_of<MK>(mcur[kb][j]);
+                        if (ml > kMaskedLogit) {
+                            vm = val + kLog2e * ml;
+                            keep_any = true;
+                        }
+                    }
+                    x[kb][j] = val;
+                    xm[kb][j] = vm;
+                }
+            }
+            // Raw scores until the row's first kept key (the reference's fully-masked-row
+            // result), then masked keys get exactly zero weight.
+            if (raw && row_any4(keep_any, l16)) {
+                raw = false;
+                m_run = -INFINITY;
+                l_run = 0.f;
+#pragma unroll
+                for (int d = 0; d < DB; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            if (!raw) {
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[kb][j] = xm[kb][j];
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[kb][j] = 16 * kb + j < rel ? sacc[kb][j] : -INFINITY;
+        }
+        float mt = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                         fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+        mt = row_max4(mt) * xs;
+        const bool move = mt > m_run + kLazy;
+        float alpha = 1.f;
+        if (move) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mt);
+            m_run = mt;
+        }
+        const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+        if (__builtin_amdgcn_ballot_w64(move)) {
+            l_run *= alpha;
+#pragma unroll
+            for (int d = 0; d < DB; ++d) o[d] *= alpha;
+        }
+        v8 pf;
+        float ls = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kb][j], xs, neg_m));
+                ls += e;
+                pf[4 * kb + j] = static_cast<T>(e);
+            }
+        }
+        l_run += ls;
+        v8 vf[DB];
+        {
+            const T* vsrc = vl + (4 * g4 + (l16 >> 2)) * VP + 4 * (l16 & 3);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                const u32x2 lo = lds_read_tr(vsrc + 16 * d);
+                const u32x2 hi = lds_read_tr(vsrc + 16 * VP + 16 * d);
+                vf[d] = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) o[d] = Mfma<T>::run(vf[d], pf, o[d]);
+    }
+
+    // Merge of the four wavefronts in LDS (their V tiles are done with after the barrier):
+    // lane (g4, l16) holds dims 16 d + 4 g4 .. + 3 of row l16.
+    const float l = row_sum4(l_run);
+    __syncthreads();
+    float* comb = reinterpret_cast<float*>(smem);
+    float* st = comb + NWAVES * 16 * CP;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) *reinterpret_cast<f32x4*>(comb + (wave * 16 + l16) * CP + 16 * d + 4 * g4) = o[d];
+    if (g4 == 0) {
+        st[(wave * 16 + l16) * 3] = m_run;
+        st[(wave * 16 + l16) * 3 + 1] = l;
+        st[(wave * 16 + l16) * 3 + 2] = raw ? 1.f : 0.f;
+    }
+    __syncthreads();
+    // Wavefront w combines dims [w D / 4, (w + 1) D / 4) of the 16 rows: lane (g4, l16)
+    // takes D / 16 of them for row l16.  Rows that met a kept key in some wavefront merge
+    // those wavefronts only; the others merge every wavefront's raw-score statistics.
+    float mw[NWAVES], lw[NWAVES];
+    bool sel_masked = false;
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) {
+        mw[w] = st[(w * 16 + l16) * 3];
+        lw[w] = st[(w * 16 + l16) * 3 + 1];
+        if (st[(w * 16 + l16) * 3 + 2] == 0.f && lw[w] > 0.f) sel_masked = true;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) {
+        const bool sel = lw[w] > 0.f && ((st[(w * 16 + l16) * 3 + 2] == 0.f) == sel_masked);
+        if (!sel) lw[w] = 0.f;
+        if (sel) M = fmaxf(M, mw[w]);
+    }
+    float L = 0.f, wt[NWAVES];
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) {
+        wt[w] = lw[w] > 0.f ? __builtin_amdgcn_exp2f(mw[w] - M) : 0.f;
+        L += wt[w] * lw[w];
+    }
+    if (!valid) return;
+    constexpr int PER = D / 16;
+    const int c0 = wave * (D / 4) + g4 * PER;
+    float acc[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) {
+#pragma unroll
+        for (int j = 0; j < PER; j += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(comb + (w * 16 + l16) * CP + c0 + j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[j + e] += wt[w] * v[e];
+        }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    if (p.splits == 1) {
+        // One workgroup per unit: the merged rows are the output.
+        const int64_t ob_off = p.cu_q ? 0 : seq * p.os[0];
+        T* out = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2] + c0;
+#pragma unroll
+        for (int j = 0; j < PER; j += 4) {
+            typedef __attribute__((__vector_size__(4 * sizeof(T)))) T t4;
+            t4 w4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w4[e] = static_cast<T>(acc[j + e] * inv);
+            *reinterpret_cast<t4*>(out + j) = w4;
+        }
+        if (p.lse && wave == 0 && g4 == 0) {
+            const int64_t lb_off = p.cu_q ? 0 : seq * p.ls[0];
+            p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] =
+                L > 0.f ? (M + log2f(L)) * kLn2 + ((MASKED && !sel_masked) ? kMaskedLogit : 0.f) : -INFINITY;
+        }
+        return;
+    }
+    const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
+    float* dst = p.part_o + prow * D + c0;
+#pragma unroll
+    for (int j = 0; j < PER; j += 4)
+        *reinterpret_cast<f32x4*>(dst + j) = f32x4{acc[j] * inv, acc[j + 1] * inv, acc[j + 2] * inv, acc[j + 3] * inv};
+    if (wave == 0 && g4 == 0) {
+        p.part_lse[2 * prow] = L > 0.f ? M + log2f(L) : -INFINITY;
+        p.part_lse[2 * prow + 1] = (MASKED && !sel_masked) ? 1.f : 0.f;
     }
 }
 
@@ -692,6 +1092,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) acc[j] = 0.f;
     float m = -INFINITY, wsum = 0.f;
+    bool any_masked = false;  // some split met a kept key: raw-score partials drop out
     if (p.splits <= 32) {
         // Every split's statistics (lane s) and O values in one round of loads.
         float lse = -INFINITY, flag = 1.f;
@@ -707,21 +1108,20 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
 #pragma unroll
             for (int j = 0; j < PER; ++j) v[k][j] = src[lane + 64 * j];
         }
-        const bool any_masked = __builtin_amdgcn_ballot_w64(lane < p.splits && flag == 0.f && lse != -INFINITY) != 0;
+        any_masked = __builtin_amdgcn_ballot_w64(lane < p.splits && flag == 0.f && lse != -INFINITY) != 0;
         if (any_masked && flag != 0.f) lse = -INFINITY;
         m = wave_max(lse);
         const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(lse - m);
         wsum = wave_sum(w);
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
-            if (k >= p.splits) break;
-            const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k));
+            const float wl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k));
+            const float wk = k < p.splits ? wl : 0.f;
 #pragma unroll
             for (int j = 0; j < PER; ++j) acc[j] += wk * v[k][j];
         }
     } else {
     // Splits go 64 at a time: lane s holds split s0 + s's statistics (read once).
-    bool any_masked = false;
     for (int s0 = 0; s0 < p.splits; s0 += kWave) {
         const int s = s0 + lane;
         if (s < p.splits) {
@@ -782,10 +1182,11 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     for (int j = 0; j < PER; ++j) dst[lane + 64 * j] = static_cast<T>(acc[j] * inv);
     if (p.lse && lane == 0)
         p.lse[lb_off + h * p.ls[1] + static_cast<int64_t>(posn) * p.ls[2]] =
-            wsum > 0.f ? (m + log2f(wsum)) * kLn2 : -INFINITY;
+            wsum > 0.f ? (m + log2f(wsum)) * kLn2 + (any_masked ? 0.f : kMaskedLogit) : -INFINITY;
 }
 
 struct Plan {
+    bool decode;  // attn_decode_kernel: per-wavefront key ranges, fp32 partials + merge
     int nqb, nx, splits, tiles_per_split;
     int64_t rows_total;
     size_t ws_bytes;
@@ -835,6 +1236,15 @@ int nqb_override() {
     return v;
 }
 
+// KMI_ATTN_SPLITS=n (read once) pins the split-KV count of calls the plan would split.
+int splits_override() {
+    static const int v = [] {
+        const char* e = std::getenv("KMI_ATTN_SPLITS");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
 Plan make_plan(const kmi_attn_args* a) {
     Plan pl{};
     const int64_t G = a->heads_q / a->heads_kv;
@@ -859,12 +1269,30 @@ Plan make_plan(const kmi_attn_args* a) {
     // (decode): about two workgroups per CU, at least one tile per wavefront per split.
     int64_t splits = 1;
     if (a->num_splits == 0) {
-        if (base < 128 && nk >= 8) splits = std::min<int64_t>(ceil_div(512, base), nk / NWAVES);
+        if (base < 128 && nk >= 8) {
+            splits = std::min<int64_t>(ceil_div(512, base), nk / NWAVES);
+            if (splits_override() > 0) splits = std::min<int64_t>(splits_override(), nk);
+        }
     } else {
         splits = std::max<int64_t>(1, std::min<int64_t>(a->num_splits, nk));
     }
     pl.tiles_per_split = static_cast<int>(ceil_div(nk, splits));
     pl.splits = static_cast<int>(ceil_div(nk, pl.tiles_per_split));
+    // Decode (at most 16 rows per K/V head): four wavefronts per workgroup deal the key
+    // tiles round-robin and merge in LDS; about two workgroups per CU in all, at most 32
+    // per unit (the merge reads their partials in one round), at least one tile per
+    // wavefront.  One workgroup per unit writes the output directly.
+    pl.decode = vrows <= 16 && a->num_splits != 1;
+    if (pl.decode) {
+        const int64_t most = std::max<int64_t>(1, ceil_div(nk, NWAVES));
+        int64_t wgs = std::min<int64_t>({ceil_div(512, units), int64_t{32}, most});
+        if (a->num_splits > 1) wgs = std::min<int64_t>(a->num_splits, most);
+        if (splits_override() > 0) wgs = std::min<int64_t>(splits_override(), most);
+        pl.splits = static_cast<int>(wgs);
+        pl.tiles_per_split = static_cast<int>(ceil_div(nk, wgs));
+        pl.nqb = 1;
+        pl.nx = 1;
+    }
     pl.rows_total = a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q;
     pl.ws_bytes = 0;
     return pl;
@@ -902,11 +1330,35 @@ hipError_t launch_mask(const AttnParams& p, int64_t grid, hipStream_t stream) {
     }
 }
 
+template <typename T, int D, int MK>
+hipError_t launch_decode(const AttnParams& p, hipStream_t stream) {
+    const int64_t grid = static_cast<int64_t>(p.batch) * p.hkv * p.splits;
+    const size_t tiles = static_cast<size_t>(NWAVES) * WN * (D + 16) * sizeof(T);
+    const size_t comb = static_cast<size_t>(NWAVES) * 16 * (D + 4) * sizeof(float);
+    const size_t lds = std::max(tiles, comb) + static_cast<size_t>(NWAVES) * 16 * 3 * sizeof(float);
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, MK>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds, stream,
+                       p);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_decode_mask(const AttnParams& p, hipStream_t stream) {
+    if (p.mask_mode == KMI_MASK_NONE) return launch_decode<T, D, MK_NONE>(p, stream);
+    switch (p.mask_dtype) {
+        case KMI_BOOL: return launch_decode<T, D, MK_BOOL>(p, stream);
+        case KMI_BF16: return launch_decode<T, D, MK_BF16>(p, stream);
+        case KMI_F16: return launch_decode<T, D, MK_F16>(p, stream);
+        default: return launch_decode<T, D, MK_F32>(p, stream);
+    }
+}
+
 template <typename T, int D>
 hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream) {
     const int64_t grid = static_cast<int64_t>(pl.nx) * p.batch * p.hkv * pl.splits;
     hipError_t err;
-    if (pl.nqb == 4 && D == 64) {
+    if (pl.decode) {
+        err = launch_decode_mask<T, D>(p, stream);
+    } else if (pl.nqb == 4 && D == 64) {
         err = launch_mask<T, 64, 4>(p, grid, stream);
     } else if (pl.nqb >= 2) {
         err = launch_mask<T, D, 2>(p, grid, stream);
