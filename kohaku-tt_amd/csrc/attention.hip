@@ -157,10 +157,19 @@ struct Shape {
     static constexpr int VP = D + 16;    // V row pitch (elements): transposed b64 reads of 8 rows hit distinct banks
     static constexpr int TILE = WN * KP + WN * VP;  // elements of one wavefront's K + V tile
     static constexpr int CP = D + 4;     // merge buffer row pitch (floats)
+    // The merge runs over groups of MB row blocks whose buffer fits in the tile area
+    // (the buffer must not set the workgroup's LDS size, which bounds workgroups per CU).
+    template <typename T>
+    static constexpr int merge_blocks() {
+        const size_t tiles = static_cast<size_t>(NWAVES) * TILE * sizeof(T);
+        const size_t per = static_cast<size_t>(NWAVES) * 16 * CP * sizeof(float);
+        const int mb = static_cast<int>(tiles / per);
+        return mb < 1 ? 1 : (mb > NQB ? NQB : mb);
+    }
     template <typename T>
     static constexpr size_t lds_bytes() {
         const size_t tiles = static_cast<size_t>(NWAVES) * TILE * sizeof(T);
-        const size_t comb = static_cast<size_t>(NWAVES) * BM * CP * sizeof(float);
+        const size_t comb = static_cast<size_t>(NWAVES) * 16 * merge_blocks<T>() * CP * sizeof(float);
         return (tiles > comb ? tiles : comb) + static_cast<size_t>(NWAVES) * BM * 3 * sizeof(float);
     }
 };
@@ -206,7 +215,9 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // Uniform per wavefront (readfirstlane tells the compiler so: tile indices and
+    // addresses derived from it then live in scalar registers).
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g4 = lane >> 4;
     const int l16 = lane & 15;
 
@@ -364,18 +375,37 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         }
     };
 
+    // Running state per row block: O^T accumulators, the row sums as MFMA accumulators
+    // (every element of lacc[b] holds lane l16's row sum), the reference point m (base-2
+    // logit units), m + 8 (the lazy-rescale threshold) and -m for the exponent.
     f32x4 o[DB][NQB];
-    float m_run[NQB], l_run[NQB];
+    f32x4 lacc[NQB];
+    float m_run[NQB], m_thr[NQB], neg_m[NQB];
     bool raw[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
         raw[b] = MASKED;
         m_run[b] = -INFINITY;
-        l_run[b] = 0.f;
+        m_thr[b] = -INFINITY;
+        neg_m[b] = 0.f;
+        lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int d = 0; d < DB; ++d) o[d][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    const float c2 = p.scale_log2;
+    v8 ones;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = static_cast<T>(1.f);
+    // A negative scale flips the sign of Q (exact) so that the exponent's multiplier is
+    // positive and a larger score is a larger logit.
+    float c2 = p.scale_log2;
+    if (c2 < 0.f) {
+        c2 = -c2;
+#pragma unroll
+        for (int b = 0; b < NQB; ++b)
+#pragma unroll
+            for (int c = 0; c < DC; ++c)
+                qf[b][c] = __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, qf[b][c]) ^ 0x80008000u);
+    }
 
     // Each wavefront's first tile is requested before anything else waits on memory (its
     // loads share one round trip with the Q fragments and the mask-row scan below).
@@ -474,19 +504,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         }
         const int key0 = t * WN;
         const bool edge = key0 + WN > lim_min;
-        v8 pf[NQB];
+        // x: logits in base-2 units times 1 / xs.  Mask-free rows keep the raw accumulators
+        // (the scale is folded into the exponent's FMA below), -inf where not visible.
+        float x[NQB][KB][4];
+        float xs = c2;  // multiplier of x in the exponent (positive)
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            // x: logits in base-2 units.  Mask-free rows keep the raw accumulators (the
-            // scale is folded into the exponent's FMA below), -inf where not visible.
-            float x[KB][4];
             const int rel = lim[b] - key0 - 4 * g4;  // element (kb, i) is visible iff 16 kb + i < rel
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[kb][i] = s[kb][b][i];
+                for (int i = 0; i < 4; ++i) x[b][kb][i] = s[kb][b][i];
             }
-            float xs = c2;  // multiplier of x in the exponent
             if constexpr (MASKED) {
                 xs = 1.f;
                 bool keep_any = false;
@@ -496,7 +525,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const bool vis = 16 * kb + i < rel;
-                        float val = x[kb][i] * c2;
+                        float val = x[b][kb][i] * c2;
                         float vm = -INFINITY;
                         if (vis) {
                             const float ml = mask_logit_of<MK>(mcur[b][kb][i]);
@@ -507,7 +536,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                         } else {
                             val = -INFINITY;
                         }
-                        x[kb][i] = val;
+                        x[b][kb][i] = val;
                         xm[kb][i] = vm;
                     }
                 }
@@ -517,58 +546,52 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                 if (raw[b] && row_any4(keep_any, l16)) {
                     raw[b] = false;
                     m_run[b] = -INFINITY;
-                    l_run[b] = 0.f;
+                    m_thr[b] = -INFINITY;
+                    neg_m[b] = 0.f;
                 }
                 if (!raw[b]) {
 #pragma unroll
                     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) x[kb][i] = xm[kb][i];
+                        for (int i = 0; i < 4; ++i) x[b][kb][i] = xm[kb][i];
                     }
                 }
             } else if (edge) {
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) x[kb][i] = 16 * kb + i < rel ? x[kb][i] : -INFINITY;
+                    for (int i = 0; i < 4; ++i) x[b][kb][i] = 16 * kb + i < rel ? x[b][kb][i] : -INFINITY;
                 }
-            }
-            float mt = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
-                             fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
-            mt = row_max4(mt) * xs;
-            // Lazy rescale: the reference point moves only when a score would exceed it by
-            // more than 2^8 (P stays <= 256, exact in bf16's exponent range); O and l are
-            // rescaled only then, skipped when no row of the wavefront moved.
-            const bool move = mt > m_run[b] + kLazy;
-            float alpha = 1.f;
-            if (move) {
-                alpha = __builtin_amdgcn_exp2f(m_run[b] - mt);
-                m_run[b] = mt;
-            }
-            const float neg_m = m_run[b] == -INFINITY ? 0.f : -m_run[b];
-            if (__builtin_amdgcn_ballot_w64(move)) {
-                l_run[b] *= alpha;
-#pragma unroll
-                for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
-            }
-            float ls = 0.f;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kb][i], xs, neg_m));
-                    x[kb][i] = e;
-                    ls += e;
-                }
-            }
-            l_run[b] += ls;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pf[b][i] = static_cast<T>(x[0][i]);
-                pf[b][4 + i] = static_cast<T>(x[1][i]);
             }
         }
-        // O^T += V^T P^T.
+        // Lazy rescale: the reference point m moves only when a score would exceed it by
+        // more than 2^8 (P stays <= 256, exact in bf16's exponent range).  Each lane checks
+        // its own scores against that threshold; only a row block where some lane crosses
+        // it pays for the row reduction, the move and the O / l rescale.
+#pragma unroll
+        for (int b = 0; b < NQB; ++b) {
+            const float lmax = fmaxf(fmaxf(fmaxf(x[b][0][0], x[b][0][1]), fmaxf(x[b][0][2], x[b][0][3])),
+                                     fmaxf(fmaxf(x[b][1][0], x[b][1][1]), fmaxf(x[b][1][2], x[b][1][3])));
+            if (__builtin_amdgcn_ballot_w64(lmax * xs > m_thr[b])) {
+                const float mt = row_max4(lmax) * xs;
+                const bool move = mt > m_thr[b];
+                float alpha = 1.f;
+                if (move) {
+                    alpha = __builtin_amdgcn_exp2f(m_run[b] - mt);  // 0 while m was -inf
+                    m_run[b] = mt;
+                    m_thr[b] = mt + kLazy;
+                    neg_m[b] = -mt;
+                }
+                if (__builtin_amdgcn_ballot_w64(move)) {
+                    lacc[b] *= alpha;
+#pragma unroll
+                    for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
+                }
+            }
+        }
+        // O^T += V^T P^T, and l += P 1 (the row sums of the bf16 weights, as MFMA columns).
+        // The V fragments are requested first; the MFMAs of row block b then interleave
+        // with the exponentials of row block b + 1 (scheduling groups below).
         v8 vf[DB];
         {
             const T* vsrc = vl + (4 * g4 + (l16 >> 2)) * VP + 4 * (l16 & 3);
@@ -580,10 +603,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
             }
         }
 #pragma unroll
-        for (int d = 0; d < DB; ++d) {
+        for (int b = 0; b < NQB; ++b) {
+            v8 pf;
 #pragma unroll
-            for (int b = 0; b < NQB; ++b) o[d][b] = Mfma<T>::run(vf[d], pf[b], o[d][b]);
+            for (int i = 0; i < 4; ++i) {
+                pf[i] = static_cast<T>(__builtin_amdgcn_exp2f(__builtin_fmaf(x[b][0][i], xs, neg_m[b])));
+                pf[4 + i] = static_cast<T>(__builtin_amdgcn_exp2f(__builtin_fmaf(x[b][1][i], xs, neg_m[b])));
+            }
+            lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) o[d][b] = Mfma<T>::run(vf[d], pf, o[d][b]);
         }
+        __builtin_amdgcn_iglp_opt(2);
         t = t_next;
     }
 
@@ -591,9 +622,10 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     __syncthreads();  // every wavefront is done with its tile buffer
     float* stats = reinterpret_cast<float*>(smem + S::template lds_bytes<T>() - NWAVES * BM * 3 * sizeof(float));
     float* comb = reinterpret_cast<float*>(smem);
+    float l_run[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
-        const float l = row_sum4(l_run[b]);
+        const float l = lacc[b][0];
         l_run[b] = l;
         if (g4 == 0) {
             float* st = stats + 3 * (wave * BM + 16 * b + l16);
@@ -608,6 +640,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     // 2^(m_w - m) / l and writes it; the sum below runs in a fixed order.
     float row_lse[NQB];
     bool row_raw[NQB];
+    float fscale[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
         const int row = 16 * b + l16;
@@ -630,35 +663,46 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
             if ((!any_masked || st[2] == 0.f) && st[1] > 0.f) lt += st[1] * __builtin_amdgcn_exp2f(st[0] - m);
         }
         const bool mine = (!any_masked || !raw[b]) && l_run[b] > 0.f;
-        const float f = (mine && lt > 0.f) ? __builtin_amdgcn_exp2f(m_run[b] - m) / lt : 0.f;
+        fscale[b] = (mine && lt > 0.f) ? __builtin_amdgcn_exp2f(m_run[b] - m) / lt : 0.f;
         row_lse[b] = lt > 0.f ? m + log2f(lt) : -INFINITY;
         row_raw[b] = !any_masked && MASKED;
-#pragma unroll
-        for (int d = 0; d < DB; ++d)
-            *reinterpret_cast<f32x4*>(comb + (wave * BM + row) * CP + 16 * d + 4 * g4) = o[d][b] * f;
     }
-    __syncthreads();
-    // Output: thread -> (row, 4 consecutive head-dim columns), summed over wavefronts.
+    // Groups of MB row blocks: each wavefront writes its scaled O, then
+    // thread -> (row, 4 consecutive head-dim columns) sums the wavefronts in a fixed order.
+    constexpr int MB = S::template merge_blocks<T>();
+    constexpr int MROWS = 16 * MB;
     constexpr int VPRO = D / 4;  // float4 columns per row
-    for (int idx = tid; idx < BM * VPRO; idx += NTHREADS) {
-        const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
-        const int r = r_begin + row;
-        if (r >= r_end) continue;
-        f32x4 acc = *reinterpret_cast<const f32x4*>(comb + row * CP + col);
 #pragma unroll
-        for (int w = 1; w < NWAVES; ++w) acc += *reinterpret_cast<const f32x4*>(comb + (w * BM + row) * CP + col);
-        const int pos = r / G;
-        const int head = kvh * G + (r - pos * G);
-        if (p.splits > 1) {
-            const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
-            *reinterpret_cast<f32x4*>(p.part_o + prow * D + col) = acc;
-        } else {
-            typedef T v4 __attribute__((ext_vector_type(4)));
-            v4 w;
+    for (int b0 = 0; b0 < NQB; b0 += MB) {
+        if (b0 > 0) __syncthreads();  // the previous group's sums are read
 #pragma unroll
-            for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(acc[i]);
-            T* dst = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2];
-            *reinterpret_cast<v4*>(dst + col) = w;
+        for (int b = b0; b < b0 + MB && b < NQB; ++b) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                *reinterpret_cast<f32x4*>(comb + (wave * MROWS + 16 * (b - b0) + l16) * CP + 16 * d + 4 * g4) =
+                    o[d][b] * fscale[b];
+        }
+        __syncthreads();
+        for (int idx = tid; idx < MROWS * VPRO; idx += NTHREADS) {
+            const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
+            const int r = r_begin + 16 * b0 + row;
+            if (16 * b0 + row >= BM || r >= r_end) continue;
+            f32x4 acc = *reinterpret_cast<const f32x4*>(comb + row * CP + col);
+#pragma unroll
+            for (int w = 1; w < NWAVES; ++w) acc += *reinterpret_cast<const f32x4*>(comb + (w * MROWS + row) * CP + col);
+            const int pos = r / G;
+            const int head = kvh * G + (r - pos * G);
+            if (p.splits > 1) {
+                const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
+                *reinterpret_cast<f32x4*>(p.part_o + prow * D + col) = acc;
+            } else {
+                typedef T v4 __attribute__((ext_vector_type(4)));
+                v4 w;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(acc[i]);
+                T* dst = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2];
+                *reinterpret_cast<v4*>(dst + col) = w;
+            }
         }
     }
     // Row statistics: the lanes of group 0 of wavefront 0 own rows 16 b + l16.
@@ -709,7 +753,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
 
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4;
     const int l16 = lane & 15;
 
