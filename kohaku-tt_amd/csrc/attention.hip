@@ -170,7 +170,7 @@ struct Shape {
     static constexpr size_t lds_bytes() {
         const size_t tiles = static_cast<size_t>(NWAVES) * TILE * sizeof(T);
         const size_t comb = static_cast<size_t>(NWAVES) * 16 * merge_blocks<T>() * CP * sizeof(float);
-        return (tiles > comb ? tiles : comb) + static_cast<size_t>(NWAVES) * BM * 3 * sizeof(float);
+        return (tiles > comb ? tiles : comb) + static_cast<size_t>(NWAVES) * BM * 4 * sizeof(float);
     }
 };
 
@@ -261,6 +261,20 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     if (p.splits > 1) {
         t_begin = split * p.tiles_per_split;
         t_end = min(ntiles, t_begin + p.tiles_per_split);
+    }
+    // Causal workgroups differ in length up to the full key count: the long ones set the
+    // kernel's critical path, so their wavefronts take issue priority over shorter
+    // neighbours sharing a SIMD (which fill the gaps).
+    if (p.causal) {
+        const int full = (lk + WN - 1) / WN;
+        const int q4 = 4 * (t_end - t_begin);
+        if (q4 > 3 * full) {
+            __builtin_amdgcn_s_setprio(3);
+        } else if (q4 > 2 * full) {
+            __builtin_amdgcn_s_setprio(2);
+        } else if (q4 > full) {
+            __builtin_amdgcn_s_setprio(1);
+        }
     }
 
     // This lane's rows (the same for every wavefront): Q fragments (B operand of
@@ -416,7 +430,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     // tiles whose every key is masked contribute exactly nothing once the row is known to
     // keep a key somewhere, so they are neither loaded nor computed.  A scan of the whole
     // mask row establishes that first (a row with no kept key needs every raw score).
-    constexpr int FLAG_CAP = NWAVES * BM * 3 * static_cast<int>(sizeof(float));
+    constexpr int FLAG_CAP = NWAVES * BM * 4 * static_cast<int>(sizeof(float));
     uint8_t* tflag = smem + S::template lds_bytes<T>() - FLAG_CAP;
     bool skip = false;
     if constexpr (MASKED) {
@@ -618,21 +632,17 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         t = t_next;
     }
 
-    // Merge the wavefronts' states.  Row stats first: (m, l, raw) per wavefront and row.
+    // Merge the wavefronts' states.  Row stats first: (m, l, raw) per wavefront and row,
+    // one 16-byte record each, read back with one load per wavefront and combined without
+    // branches (every load of a row in flight at once).
     __syncthreads();  // every wavefront is done with its tile buffer
-    float* stats = reinterpret_cast<float*>(smem + S::template lds_bytes<T>() - NWAVES * BM * 3 * sizeof(float));
+    f32x4* stats = reinterpret_cast<f32x4*>(smem + S::template lds_bytes<T>() - NWAVES * BM * sizeof(f32x4));
     float* comb = reinterpret_cast<float*>(smem);
     float l_run[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
-        const float l = lacc[b][0];
-        l_run[b] = l;
-        if (g4 == 0) {
-            float* st = stats + 3 * (wave * BM + 16 * b + l16);
-            st[0] = m_run[b];
-            st[1] = l;
-            st[2] = raw[b] ? 1.f : 0.f;
-        }
+        l_run[b] = lacc[b][0];
+        if (g4 == 0) stats[wave * BM + 16 * b + l16] = f32x4{m_run[b], l_run[b], raw[b] ? 1.f : 0.f, 0.f};
     }
     __syncthreads();
     // Wavefronts in masked mode (they met a kept key) win; a row none of them kept a key
@@ -644,24 +654,22 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
         const int row = 16 * b + l16;
+        f32x4 sw[NWAVES];
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) sw[w] = stats[w * BM + row];
         bool any_masked = false;
 #pragma unroll
-        for (int w = 0; w < NWAVES; ++w) {
-            const float* st = stats + 3 * (w * BM + row);
-            if (st[2] == 0.f && st[1] > 0.f) any_masked = true;
-        }
+        for (int w = 0; w < NWAVES; ++w) any_masked = any_masked || (sw[w][2] == 0.f && sw[w][1] > 0.f);
         float m = -INFINITY;
+        bool sel[NWAVES];
 #pragma unroll
         for (int w = 0; w < NWAVES; ++w) {
-            const float* st = stats + 3 * (w * BM + row);
-            if ((!any_masked || st[2] == 0.f) && st[1] > 0.f) m = fmaxf(m, st[0]);
+            sel[w] = (!any_masked || sw[w][2] == 0.f) && sw[w][1] > 0.f;
+            m = fmaxf(m, sel[w] ? sw[w][0] : -INFINITY);
         }
         float lt = 0.f;
 #pragma unroll
-        for (int w = 0; w < NWAVES; ++w) {
-            const float* st = stats + 3 * (w * BM + row);
-            if ((!any_masked || st[2] == 0.f) && st[1] > 0.f) lt += st[1] * __builtin_amdgcn_exp2f(st[0] - m);
-        }
+        for (int w = 0; w < NWAVES; ++w) lt += sel[w] ? sw[w][1] * __builtin_amdgcn_exp2f(sw[w][0] - m) : 0.f;
         const bool mine = (!any_masked || !raw[b]) && l_run[b] > 0.f;
         fscale[b] = (mine && lt > 0.f) ? __builtin_amdgcn_exp2f(m_run[b] - m) / lt : 0.f;
         row_lse[b] = lt > 0.f ? m + log2f(lt) : -INFINITY;
