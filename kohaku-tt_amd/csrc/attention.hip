@@ -153,9 +153,12 @@ constexpr int WN = 32;
 template <int D, int NQB>
 struct Shape {
     static constexpr int BM = 16 * NQB;  // rows of a workgroup (shared by its wavefronts)
-    static constexpr int KP = D + 8;     // K row pitch (elements): b128 reads of 16 rows hit distinct banks
     static constexpr int VP = D + 16;    // V row pitch (elements): transposed b64 reads of 8 rows hit distinct banks
-    static constexpr int TILE = WN * KP + WN * VP;  // elements of one wavefront's K + V tile
+    static constexpr int KP = D + 8;     // K row pitch (elements): b128 reads of 16 rows hit distinct banks
+    // K fragments straight from memory into registers (KD) where the wavefront's 64 rows
+    // give each loaded fragment the most use; otherwise K is staged in LDS too.
+    static constexpr bool KD = D == 64 && NQB == 4;
+    static constexpr int TILE = (KD ? 0 : WN * KP) + WN * VP;  // elements of one wavefront's tile
     static constexpr int CP = D + 4;     // merge buffer row pitch (floats)
     // The merge runs over groups of MB row blocks whose buffer fits in the tile area
     // (the buffer must not set the workgroup's LDS size, which bounds workgroups per CU).
@@ -201,7 +204,8 @@ template <typename T, int D, int NQB, int MK>
 __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
     typedef typename Mfma<T>::v8 v8;
     typedef Shape<D, NQB> S;
-    constexpr int BM = S::BM, KP = S::KP, VP = S::VP, CP = S::CP;
+    constexpr int BM = S::BM, VP = S::VP, KP = S::KP, CP = S::CP;
+    constexpr bool KD = S::KD;
     constexpr int DC = D / 32;  // 32-wide chunks of the head dim
     constexpr int DB = D / 16;  // 16-wide blocks of the head dim
     constexpr int KB = WN / 16;
@@ -327,13 +331,17 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         }
     }
 
-    // This lane's K / V sources: key row `krow` (+ RPP per pass) of each tile.
+    // KD: K fragments come straight from memory into MFMA A-operand registers: lane
+    // (g4, l16) holds key 16 kb + l16, dims 32 c + 8 g4 .. + 7 of S^T = K Q^T.  Otherwise
+    // K rows are staged through the wavefront's LDS tile like V (key row `krow` + RPP
+    // per pass); V always is, for the transposed reads.
     const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
     const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
-    const T* kbase = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * ks2 + 8 * dg;
+    const T* kq = KD ? static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + l16) * ks2 + 8 * g4
+                     : static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * ks2 + 8 * dg;
     const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + krow) * vs2 + 8 * dg;
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
-    T* vl = kl + WN * KP;
+    T* vl = kl + (KD ? 0 : WN * KP);
 
     // Mask values of the staged tile, loaded with its K / V (raw element type; converted
     // when the tile is computed, so the loads stay in flight meanwhile).
@@ -341,27 +349,53 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
             typename std::conditional<MK == MK_BF16 || MK == MK_F16, uint16_t, float>::type>::type MRaw;
     MRaw mpre[MASKED ? NQB : 1][KB][4];
 
-    u32x4 kreg[KIT];
+    v8 kreg[KD ? KB : 1][KD ? DC : 1];
+    u32x4 kst[KD ? 1 : KIT];
     u32x4 vreg[KIT];
-    auto load_tile = [&](int t) {
+    auto load_k = [&](int t) {
         const int key0 = t * WN;
-        const T* ksrc = kbase + static_cast<int64_t>(key0) * ks2;
+        const T* ksrc = kq + static_cast<int64_t>(key0) * ks2;
+        const bool full = key0 + WN <= lk;  // uniform: the common case loads unconditionally
+        if constexpr (KD) {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int c = 0; c < DC; ++c) {
+                    if (full) {
+                        kreg[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
+                    } else if (key0 + 16 * kb + l16 < lk) {
+                        kreg[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) kreg[kb][c][j] = static_cast<T>(0.f);
+                    }
+                }
+            }
+        } else {
+            if (full) {
+#pragma unroll
+                for (int i = 0; i < KIT; ++i) kst[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
+            } else {
+#pragma unroll
+                for (int i = 0; i < KIT; ++i) {
+                    kst[i] = u32x4{0u, 0u, 0u, 0u};
+                    if (key0 + krow + i * RPP < lk) kst[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
+                }
+            }
+        }
+    };
+    // V rows and mask values of tile t.
+    auto load_v = [&](int t) {
+        const int key0 = t * WN;
         const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
         if (key0 + WN <= lk) {
 #pragma unroll
-            for (int i = 0; i < KIT; ++i) {
-                kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
-                vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
-            }
+            for (int i = 0; i < KIT; ++i) vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
         } else {
 #pragma unroll
             for (int i = 0; i < KIT; ++i) {
-                kreg[i] = u32x4{0u, 0u, 0u, 0u};
                 vreg[i] = u32x4{0u, 0u, 0u, 0u};
-                if (key0 + krow + i * RPP < lk) {
-                    kreg[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
-                    vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
-                }
+                if (key0 + krow + i * RPP < lk) vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
             }
         }
         if constexpr (MASKED) {
@@ -380,11 +414,15 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
             }
         }
     };
-    // K and V rows as loaded.
+    auto load_tile = [&](int t) {
+        load_k(t);
+        load_v(t);
+    };
+    // V (and staged K) rows as loaded.
     auto store_tile = [&]() {
 #pragma unroll
         for (int i = 0; i < KIT; ++i) {
-            *reinterpret_cast<u32x4*>(kl + (krow + i * RPP) * KP + 8 * dg) = kreg[i];
+            if constexpr (!KD) *reinterpret_cast<u32x4*>(kl + (krow + i * RPP) * KP + 8 * dg) = kst[i];
             *reinterpret_cast<u32x4*>(vl + (krow + i * RPP) * VP + 8 * dg) = vreg[i];
         }
     };
@@ -498,22 +536,38 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         }
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int t_next = next_tile(t + NWAVES);
-        if (t_next < t_end) load_tile(t_next);
-        // S^T = K Q^T: every K fragment of the tile first, then the MFMAs.
-        v8 kf[KB][DC];
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-            for (int c = 0; c < DC; ++c) kf[kb][c] = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
-        }
+        // S^T = K Q^T.  KD: from the K registers, whose next loads go out once they are
+        // consumed; otherwise from the LDS tile, with the whole next tile requested first.
         f32x4 s[KB][NQB];
+        if constexpr (KD) {
+            if (t_next < t_end) load_v(t_next);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
+            for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-            for (int b = 0; b < NQB; ++b) {
-                s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int b = 0; b < NQB; ++b) {
+                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
+                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kreg[kb][c], qf[b][c], s[kb][b]);
+                }
+            }
+            if (t_next < t_end) load_k(t_next);
+        } else {
+            if (t_next < t_end) load_tile(t_next);
+            v8 kf[KB][DC];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int c = 0; c < DC; ++c)
+                    kf[kb][c] = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
+            }
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int b = 0; b < NQB; ++b) {
+                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
+                }
             }
         }
         const int key0 = t * WN;
