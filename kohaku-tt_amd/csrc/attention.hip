@@ -686,103 +686,155 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         t = t_next;
     }
 
-    // Merge the wavefronts' states.  Row stats first: (m, l, raw) per wavefront and row,
-    // one 16-byte record each, read back with one load per wavefront and combined without
-    // branches (every load of a row in flight at once).
-    __syncthreads();  // every wavefront is done with its tile buffer
+    // Merge the wavefronts' states: (m, l, raw) per wavefront and row as 16-byte records
+    // (read back with one load per wavefront, combined without branches) and the O
+    // accumulators.  Wavefronts in masked mode (they met a kept key) win; a row none of
+    // them kept a key for merges every wavefront's raw-score state.  The sums run in a
+    // fixed wavefront order.
     f32x4* stats = reinterpret_cast<f32x4*>(smem + S::template lds_bytes<T>() - NWAVES * BM * sizeof(f32x4));
-    float* comb = reinterpret_cast<float*>(smem);
     float l_run[NQB];
 #pragma unroll
-    for (int b = 0; b < NQB; ++b) {
-        l_run[b] = lacc[b][0];
-        if (g4 == 0) stats[wave * BM + 16 * b + l16] = f32x4{m_run[b], l_run[b], raw[b] ? 1.f : 0.f, 0.f};
-    }
-    __syncthreads();
-    // Wavefronts in masked mode (they met a kept key) win; a row none of them kept a key
-    // for merges every wavefront's raw-score state.  Each wavefront scales its O by
-    // 2^(m_w - m) / l and writes it; the sum below runs in a fixed order.
-    float row_lse[NQB];
-    bool row_raw[NQB];
-    float fscale[NQB];
-#pragma unroll
-    for (int b = 0; b < NQB; ++b) {
-        const int row = 16 * b + l16;
-        f32x4 sw[NWAVES];
-#pragma unroll
-        for (int w = 0; w < NWAVES; ++w) sw[w] = stats[w * BM + row];
-        bool any_masked = false;
+    for (int b = 0; b < NQB; ++b) l_run[b] = lacc[b][0];
+    auto combine = [&](const f32x4 (&sw)[NWAVES], float (&wt)[NWAVES], float& m, float& lt, bool& any_masked) {
+        any_masked = false;
 #pragma unroll
         for (int w = 0; w < NWAVES; ++w) any_masked = any_masked || (sw[w][2] == 0.f && sw[w][1] > 0.f);
-        float m = -INFINITY;
+        m = -INFINITY;
         bool sel[NWAVES];
 #pragma unroll
         for (int w = 0; w < NWAVES; ++w) {
             sel[w] = (!any_masked || sw[w][2] == 0.f) && sw[w][1] > 0.f;
             m = fmaxf(m, sel[w] ? sw[w][0] : -INFINITY);
         }
-        float lt = 0.f;
+        lt = 0.f;
 #pragma unroll
-        for (int w = 0; w < NWAVES; ++w) lt += sel[w] ? sw[w][1] * __builtin_amdgcn_exp2f(sw[w][0] - m) : 0.f;
-        const bool mine = (!any_masked || !raw[b]) && l_run[b] > 0.f;
-        fscale[b] = (mine && lt > 0.f) ? __builtin_amdgcn_exp2f(m_run[b] - m) / lt : 0.f;
-        row_lse[b] = lt > 0.f ? m + log2f(lt) : -INFINITY;
-        row_raw[b] = !any_masked && MASKED;
-    }
-    // Groups of MB row blocks: each wavefront writes its scaled O, then
-    // thread -> (row, 4 consecutive head-dim columns) sums the wavefronts in a fixed order.
-    constexpr int MB = S::template merge_blocks<T>();
-    constexpr int MROWS = 16 * MB;
+        for (int w = 0; w < NWAVES; ++w) {
+            wt[w] = sel[w] ? __builtin_amdgcn_exp2f(sw[w][0] - m) : 0.f;
+            lt += wt[w] * sw[w][1];
+        }
+    };
+    auto write_row = [&](int r, int col, const f32x4& acc) {
+        const int pos = r / G;
+        const int head = kvh * G + (r - pos * G);
+        if (p.splits > 1) {
+            const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
+            *reinterpret_cast<f32x4*>(p.part_o + prow * D + col) = acc;
+        } else {
+            typedef T v4 __attribute__((ext_vector_type(4)));
+            v4 w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(acc[i]);
+            T* dst = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2];
+            *reinterpret_cast<v4*>(dst + col) = w;
+        }
+    };
+    auto write_lse = [&](int r, float row_lse, bool row_raw) {
+        const int pos = r / G;
+        const int head = kvh * G + (r - pos * G);
+        if (p.splits > 1) {
+            const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
+            p.part_lse[2 * prow] = row_lse;
+            p.part_lse[2 * prow + 1] = row_raw ? 1.f : 0.f;
+        } else if (p.lse) {
+            // A row without a kept key: its logits all carry the -5e5 clamp.
+            p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] =
+                row_lse * kLn2 + (row_raw ? kMaskedLogit : 0.f);
+        }
+    };
     constexpr int VPRO = D / 4;  // float4 columns per row
-#pragma unroll
-    for (int b0 = 0; b0 < NQB; b0 += MB) {
-        if (b0 > 0) __syncthreads();  // the previous group's sums are read
-#pragma unroll
-        for (int b = b0; b < b0 + MB && b < NQB; ++b) {
-#pragma unroll
-            for (int d = 0; d < DB; ++d)
-                *reinterpret_cast<f32x4*>(comb + (wave * MROWS + 16 * (b - b0) + l16) * CP + 16 * d + 4 * g4) =
-                    o[d][b] * fscale[b];
-        }
-        __syncthreads();
-        for (int idx = tid; idx < MROWS * VPRO; idx += NTHREADS) {
-            const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
-            const int r = r_begin + 16 * b0 + row;
-            if (16 * b0 + row >= BM || r >= r_end) continue;
-            f32x4 acc = *reinterpret_cast<const f32x4*>(comb + row * CP + col);
-#pragma unroll
-            for (int w = 1; w < NWAVES; ++w) acc += *reinterpret_cast<const f32x4*>(comb + (w * MROWS + row) * CP + col);
-            const int pos = r / G;
-            const int head = kvh * G + (r - pos * G);
-            if (p.splits > 1) {
-                const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
-                *reinterpret_cast<f32x4*>(p.part_o + prow * D + col) = acc;
-            } else {
-                typedef T v4 __attribute__((ext_vector_type(4)));
-                v4 w;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(acc[i]);
-                T* dst = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2];
-                *reinterpret_cast<v4*>(dst + col) = w;
-            }
-        }
-    }
-    // Row statistics: the lanes of group 0 of wavefront 0 own rows 16 b + l16.
-    if (wave == 0 && g4 == 0) {
+    constexpr bool OWN = static_cast<size_t>(S::TILE) * sizeof(T) >= static_cast<size_t>(NQB) * 16 * CP * sizeof(float);
+    if constexpr (OWN) {
+        // Each wavefront's O fits over its own tile area, which no other wavefront reads:
+        // one barrier (the mask-skip flags share the statistics area, so a skipping
+        // workgroup waits for every wavefront's loop first).
+        if (skip) __syncthreads();
+        float* mine = reinterpret_cast<float*>(smem + static_cast<size_t>(wave) * S::TILE * sizeof(T));
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            const int r = r_begin + 16 * b + l16;
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                *reinterpret_cast<f32x4*>(mine + (16 * b + l16) * CP + 16 * d + 4 * g4) = o[d][b];
+            if (g4 == 0) stats[wave * BM + 16 * b + l16] = f32x4{m_run[b], l_run[b], raw[b] ? 1.f : 0.f, 0.f};
+        }
+        __syncthreads();
+        // thread -> (row, 4 consecutive head-dim columns): weights of the wavefronts, their
+        // O sum, the normalised row.
+        for (int idx = tid; idx < BM * VPRO; idx += NTHREADS) {
+            const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
+            const int r = r_begin + row;
             if (r >= r_end) continue;
-            const int pos = r / G;
-            const int head = kvh * G + (r - pos * G);
-            if (p.splits > 1) {
-                const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
-                p.part_lse[2 * prow] = row_lse[b];
-                p.part_lse[2 * prow + 1] = row_raw[b] ? 1.f : 0.f;
-            } else if (p.lse) {
-                // A row without a kept key: its logits all carry the -5e5 clamp.
-                p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] =
-                    row_lse[b] * kLn2 + (row_raw[b] ? kMaskedLogit : 0.f);
+            f32x4 sw[NWAVES];
+            f32x4 ov[NWAVES];
+#pragma unroll
+            for (int w = 0; w < NWAVES; ++w) {
+                sw[w] = stats[w * BM + row];
+                ov[w] = *reinterpret_cast<const f32x4*>(
+                    reinterpret_cast<const float*>(smem + static_cast<size_t>(w) * S::TILE * sizeof(T)) + row * CP + col);
+            }
+            float wt[NWAVES], m, lt;
+            bool any_masked;
+            combine(sw, wt, m, lt, any_masked);
+            f32x4 acc = ov[0] * wt[0];
+#pragma unroll
+            for (int w = 1; w < NWAVES; ++w) acc += ov[w] * wt[w];
+            acc *= lt > 0.f ? 1.f / lt : 0.f;
+            write_row(r, col, acc);
+            if (col == 0) write_lse(r, lt > 0.f ? m + log2f(lt) : -INFINITY, !any_masked && MASKED);
+        }
+    } else {
+        __syncthreads();  // every wavefront is done with its tile buffer
+        float* comb = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int b = 0; b < NQB; ++b)
+            if (g4 == 0) stats[wave * BM + 16 * b + l16] = f32x4{m_run[b], l_run[b], raw[b] ? 1.f : 0.f, 0.f};
+        __syncthreads();
+        // Each wavefront scales its O by 2^(m_w - m) / l and writes it.
+        float row_lse[NQB];
+        bool row_raw[NQB];
+        float fscale[NQB];
+#pragma unroll
+        for (int b = 0; b < NQB; ++b) {
+            f32x4 sw[NWAVES];
+#pragma unroll
+            for (int w = 0; w < NWAVES; ++w) sw[w] = stats[w * BM + 16 * b + l16];
+            float wt[NWAVES], m, lt;
+            bool any_masked;
+            combine(sw, wt, m, lt, any_masked);
+            fscale[b] = lt > 0.f ? wt[wave] / lt : 0.f;
+            row_lse[b] = lt > 0.f ? m + log2f(lt) : -INFINITY;
+            row_raw[b] = !any_masked && MASKED;
+        }
+        // Groups of MB row blocks: each wavefront writes its scaled O, then
+        // thread -> (row, 4 consecutive head-dim columns) sums the wavefronts.
+        constexpr int MB = S::template merge_blocks<T>();
+        constexpr int MROWS = 16 * MB;
+#pragma unroll
+        for (int b0 = 0; b0 < NQB; b0 += MB) {
+            if (b0 > 0) __syncthreads();  // the previous group's sums are read
+#pragma unroll
+            for (int b = b0; b < b0 + MB && b < NQB; ++b) {
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+                    *reinterpret_cast<f32x4*>(comb + (wave * MROWS + 16 * (b - b0) + l16) * CP + 16 * d + 4 * g4) =
+                        o[d][b] * fscale[b];
+            }
+            __syncthreads();
+            for (int idx = tid; idx < MROWS * VPRO; idx += NTHREADS) {
+                const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
+                const int r = r_begin + 16 * b0 + row;
+                if (16 * b0 + row >= BM || r >= r_end) continue;
+                f32x4 acc = *reinterpret_cast<const f32x4*>(comb + row * CP + col);
+#pragma unroll
+                for (int w = 1; w < NWAVES; ++w) acc += *reinterpret_cast<const f32x4*>(comb + (w * MROWS + row) * CP + col);
+                write_row(r, col, acc);
+            }
+        }
+        // Row statistics: the lanes of group 0 of wavefront 0 own rows 16 b + l16.
+        if (wave == 0 && g4 == 0) {
+#pragma unroll
+            for (int b = 0; b < NQB; ++b) {
+                const int r = r_begin + 16 * b + l16;
+                if (r < r_end) write_lse(r, row_lse[b], row_raw[b]);
             }
         }
     }
