@@ -266,20 +266,6 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         t_begin = split * p.tiles_per_split;
         t_end = min(ntiles, t_begin + p.tiles_per_split);
     }
-    // Causal workgroups differ in length up to the full key count: the long ones set the
-    // kernel's critical path, so their wavefronts take issue priority over shorter
-    // neighbours sharing a SIMD (which fill the gaps).
-    if (p.causal) {
-        const int full = (lk + WN - 1) / WN;
-        const int q4 = 4 * (t_end - t_begin);
-        if (q4 > 3 * full) {
-            __builtin_amdgcn_s_setprio(3);
-        } else if (q4 > 2 * full) {
-            __builtin_amdgcn_s_setprio(2);
-        } else if (q4 > full) {
-            __builtin_amdgcn_s_setprio(1);
-        }
-    }
 
     // This lane's rows (the same for every wavefront): Q fragments (B operand of
     // S^T = K Q^T) and row metadata.
@@ -521,8 +507,9 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     int t = next_tile(t_spec);
     if (t != t_spec && t < t_end) load_tile(t);
     while (t < t_end) {
-        // The previous tile's LDS reads were issued before these writes; LDS runs one
-        // wavefront's instructions in order, so only the compiler must keep the order.
+        // LDS runs one wavefront's instructions in order: the previous tile's reads were
+        // issued before these writes and this tile's reads come after them, so only the
+        // compiler must keep the order (no wait for the writes).
         __asm__ volatile("" ::: "memory");
         store_tile();
         MRaw mcur[MASKED ? NQB : 1][KB][4];
@@ -534,7 +521,6 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
 #pragma unroll
                     for (int i = 0; i < 4; ++i) mcur[b][kb][i] = mpre[b][kb][i];
         }
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int t_next = next_tile(t + NWAVES);
         // S^T = K Q^T.  KD: from the K registers, whose next loads go out once they are
         // consumed; otherwise from the LDS tile, with the whole next tile requested first.
@@ -1040,6 +1026,8 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     int i = use_bits ? (live ? __builtin_ctz(live) : n_t) : 0;
     if (i < n_t) load_tile(i);
     while (i < n_t) {
+        // LDS keeps one wavefront's accesses in order (the previous tile's reads, these
+        // writes, this tile's reads): only the compiler must keep it.
         __asm__ volatile("" ::: "memory");
 #pragma unroll
         for (int i2 = 0; i2 < KIT; ++i2) *reinterpret_cast<u32x4*>(vl + (krow + i2 * RPP) * VP + 8 * dg) = vreg[i2];
@@ -1050,7 +1038,6 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
 #pragma unroll
                 for (int j = 0; j < 4; ++j) mcur[kb][j] = mpre[kb][j];
         }
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         f32x4 sacc[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
