@@ -8,10 +8,13 @@
 // Tensix cores and merges partial statistics (Chan); here a 64-lane wavefront owns one
 // row, keeps it in registers (one HBM read, one HBM write) and reduces across lanes.
 //
-// Fast path: rows whose width is a multiple of one 16-byte vector and whose pointers are
-// 16-byte aligned; each lane holds up to VPL vectors of the row.  Generic path: one
+// Vector paths (rows whose width is a multiple of one 16-byte vector, 16-byte aligned
+// pointers): one wavefront per row holding up to 4 vectors per lane, or for wider rows
+// one 256-thread block per row holding up to 8 vectors per thread.  Generic path: one
 // 256-thread block per row with element loads (any width and alignment).
 #include "common.hpp"
+
+#include <type_traits>
 
 namespace kmi {
 namespace {
@@ -36,7 +39,31 @@ __device__ __forceinline__ void store_pack(T* p, const float* in) {
     *reinterpret_cast<Pack<T, E>*>(p) = v;
 }
 
-// One wavefront per row, 4 rows per 256-thread block.  T: x / y; W: weight and bias.
+// The E = 16 / sizeof(T) elements of one 16-byte vector as fp32 (bf16: the high half of
+// an fp32; f16: converted; f32: as is).
+template <typename T>
+__device__ __forceinline__ void unpack(const u32x4& raw, float* out) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) out[k] = __uint_as_float(raw[k]);
+    } else if constexpr (std::is_same<T, bf16>::value) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            out[2 * k] = __uint_as_float(raw[k] << 16);
+            out[2 * k + 1] = __uint_as_float(raw[k] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            out[2 * k] = to_f32(__builtin_bit_cast(f16, static_cast<uint16_t>(raw[k] & 0xffffu)));
+            out[2 * k + 1] = to_f32(__builtin_bit_cast(f16, static_cast<uint16_t>(raw[k] >> 16)));
+        }
+    }
+}
+
+// One wavefront per row, 4 rows per 256-thread block.  T: x / y; W: weight and bias.  The
+// row stays in registers as loaded (packed) and is widened to fp32 in each pass, which
+// keeps the register count, and so the wavefronts in flight per SIMD, up.
 template <typename T, typename W, int VPL, bool LAYER>
 __global__ __launch_bounds__(256) void norm_rows_wave(
     const T* __restrict__ x, const W* __restrict__ weight, const W* __restrict__ bias,
@@ -48,19 +75,19 @@ __global__ __launch_bounds__(256) void norm_rows_wave(
     if (row >= rows) return;
     const int nvec = width / E;
     const T* xr = x + row * width;
-    float v[VPL][E];
-    float sum = 0.f;
+    u32x4 raw[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + kWave * i;
-        if (vi < nvec) {
-            load_pack<T, E>(xr + vi * E, v[i]);
-        } else {
+        raw[i] = vi < nvec ? *reinterpret_cast<const u32x4*>(xr + vi * E) : u32x4{0u, 0u, 0u, 0u};
+    }
+    float sum = 0.f;
 #pragma unroll
-            for (int j = 0; j < E; ++j) v[i][j] = 0.f;
-        }
+    for (int i = 0; i < VPL; ++i) {
+        float v[E];
+        unpack<T>(raw[i], v);
 #pragma unroll
-        for (int j = 0; j < E; ++j) sum += LAYER ? v[i][j] : v[i][j] * v[i][j];
+        for (int j = 0; j < E; ++j) sum += LAYER ? v[j] : v[j] * v[j];
     }
     sum = wave_sum(sum);
     const float inv_w = 1.f / static_cast<float>(width);
@@ -72,9 +99,11 @@ __global__ __launch_bounds__(256) void norm_rows_wave(
         for (int i = 0; i < VPL; ++i) {
             const int vi = lane + kWave * i;
             if (vi < nvec) {
+                float v[E];
+                unpack<T>(raw[i], v);
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
-                    const float c = v[i][j] - mean;
+                    const float c = v[j] - mean;
                     m2 += c * c;
                 }
             }
@@ -89,7 +118,8 @@ __global__ __launch_bounds__(256) void norm_rows_wave(
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + kWave * i;
         if (vi < nvec) {
-            float o[E], g[E], b[E];
+            float v[E], o[E], g[E], b[E];
+            unpack<T>(raw[i], v);
             if (weight) {
                 load_pack<W, E>(weight + vi * E, g);
             } else {
@@ -103,11 +133,99 @@ __global__ __launch_bounds__(256) void norm_rows_wave(
                 for (int j = 0; j < E; ++j) b[j] = 0.f;
             }
 #pragma unroll
-            for (int j = 0; j < E; ++j) o[j] = (v[i][j] - mean) * rstd * g[j] + b[j];
+            for (int j = 0; j < E; ++j) o[j] = (v[j] - mean) * rstd * g[j] + b[j];
             store_pack<T, E>(yr + vi * E, o);
         }
     }
     if (lane == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+// Wide rows: one 256-thread block per row, each thread holding VPT vectors; the four
+// wavefronts' partial sums meet in LDS in a fixed order.
+template <typename T, typename W, int VPT, bool LAYER>
+__global__ __launch_bounds__(256) void norm_rows_block(
+    const T* __restrict__ x, const W* __restrict__ weight, const W* __restrict__ bias,
+    T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
+    int width, float eps) {
+    constexpr int E = 16 / sizeof(T);
+    constexpr int NW = 4;
+    __shared__ float red[2][NW];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1), wave = tid >> 6;
+    const int64_t row = blockIdx.x;
+    const int nvec = width / E;
+    const T* xr = x + row * width;
+    u32x4 raw[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int vi = tid + 256 * i;
+        raw[i] = vi < nvec ? *reinterpret_cast<const u32x4*>(xr + vi * E) : u32x4{0u, 0u, 0u, 0u};
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        float v[E];
+        unpack<T>(raw[i], v);
+#pragma unroll
+        for (int j = 0; j < E; ++j) sum += LAYER ? v[j] : v[j] * v[j];
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red[0][wave] = sum;
+    __syncthreads();
+    sum = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    const float inv_w = 1.f / static_cast<float>(width);
+    float mean = 0.f, rstd;
+    if (LAYER) {
+        mean = sum * inv_w;
+        float m2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            if (tid + 256 * i < nvec) {
+                float v[E];
+                unpack<T>(raw[i], v);
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const float c = v[j] - mean;
+                    m2 += c * c;
+                }
+            }
+        }
+        m2 = wave_sum(m2);
+        if (lane == 0) red[1][wave] = m2;
+        __syncthreads();
+        m2 = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+        rstd = 1.f / sqrtf(fmaxf(m2 * inv_w, 0.f) + eps);
+    } else {
+        rstd = 1.f / sqrtf(sum * inv_w + eps);
+    }
+    T* yr = y + row * width;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int vi = tid + 256 * i;
+        if (vi < nvec) {
+            float v[E], o[E], g[E], b[E];
+            unpack<T>(raw[i], v);
+            if (weight) {
+                load_pack<W, E>(weight + vi * E, g);
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; ++j) g[j] = 1.f;
+            }
+            if (bias) {
+                load_pack<W, E>(bias + vi * E, b);
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; ++j) b[j] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < E; ++j) o[j] = (v[j] - mean) * rstd * g[j] + b[j];
+            store_pack<T, E>(yr + vi * E, o);
+        }
+    }
+    if (tid == 0) {
         if (mean_out) mean_out[row] = mean;
         if (rstd_out) rstd_out[row] = rstd;
     }
@@ -198,8 +316,31 @@ hipError_t launch_wave(const void* x, const void* w, const void* b, void* y, flo
         KMI_NORM_CASE(1)
         KMI_NORM_CASE(2)
         KMI_NORM_CASE(4)
+        default: return hipErrorInvalidValue;
+    }
+#undef KMI_NORM_CASE
+    return hipGetLastError();
+}
+
+template <typename T, typename W, bool LAYER>
+hipError_t launch_block(const void* x, const void* w, const void* b, void* y, float* mean,
+                        float* rstd, int64_t rows, int width, float eps, int vpt,
+                        hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(rows)), block(256);
+    auto* xp = static_cast<const T*>(x);
+    auto* wp = static_cast<const W*>(w);
+    auto* bp = static_cast<const W*>(b);
+    auto* yp = static_cast<T*>(y);
+#define KMI_NORM_CASE(N)                                                                   \
+    case N:                                                                                \
+        hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER>), grid, block, 0, stream, xp,  \
+                           wp, bp, yp, mean, rstd, width, eps);                            \
+        break;
+    switch (vpt) {
+        KMI_NORM_CASE(1)
+        KMI_NORM_CASE(2)
+        KMI_NORM_CASE(4)
         KMI_NORM_CASE(8)
-        KMI_NORM_CASE(16)
         default: return hipErrorInvalidValue;
     }
 #undef KMI_NORM_CASE
@@ -244,26 +385,29 @@ int norm_fwd(const char* name, const void* x, const void* w, const void* b, void
         (!w || !b || w_dtype == b_dtype);
     const int pdt = w ? w_dtype : (b ? b_dtype : x_dtype);
     const int64_t pbytes = static_cast<int64_t>(epv) * dtype_size(pdt);
-    const bool fast = width % epv == 0 && vpl_need <= 16 && params_ok &&
-                      aligned(x, 16) && aligned(y, 16) && aligned(w, pbytes) &&
-                      aligned(b, pbytes);
+    // Rows of up to 4 vectors per lane take one wavefront each; wider rows (up to 8
+    // vectors per thread of a 256-thread block) one block each.
+    const int64_t vpt_need = ceil_div(nvec, 256);
+    const bool vec_ok = width % epv == 0 && params_ok && aligned(x, 16) && aligned(y, 16) &&
+                        aligned(w, pbytes) && aligned(b, pbytes);
+    const bool by_wave = vec_ok && vpl_need <= 4;
+    const bool by_block = vec_ok && !by_wave && vpt_need <= 8;
     hipError_t err;
-    if (fast) {
-        int vpl = 1;
-        while (vpl < vpl_need) vpl <<= 1;
+    if (by_wave || by_block) {
+        int n = 1;
+        while (n < (by_wave ? vpl_need : vpt_need)) n <<= 1;
         const int wd = static_cast<int>(width);
         const bool pf32 = pdt == KMI_F32;
+        auto go = [&](auto tx, auto tw) {
+            typedef decltype(tx) TX;
+            typedef decltype(tw) TW;
+            return by_wave ? launch_wave<TX, TW, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, n, stream)
+                           : launch_block<TX, TW, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, n, stream);
+        };
         switch (x_dtype) {
-            case KMI_BF16:
-                err = pf32 ? launch_wave<bf16, float, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream)
-                           : launch_wave<bf16, bf16, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream);
-                break;
-            case KMI_F16:
-                err = pf32 ? launch_wave<f16, float, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream)
-                           : launch_wave<f16, f16, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream);
-                break;
-            default:
-                err = launch_wave<float, float, LAYER>(x, w, b, y, mean, rstd, rows, wd, e, vpl, stream);
+            case KMI_BF16: err = pf32 ? go(bf16{}, float{}) : go(bf16{}, bf16{}); break;
+            case KMI_F16: err = pf32 ? go(f16{}, float{}) : go(f16{}, f16{}); break;
+            default: err = go(float{}, float{});
         }
     } else {
         hipLaunchKernelGGL((norm_rows_generic<LAYER>), dim3(static_cast<unsigned>(rows)),

@@ -16,7 +16,7 @@ from oracle import norms as onorm
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 33), (5, 70), (32, 64), (77, 1000), (2, 40, 4096), (3, 16384), (4096, 768), (65536, 64),
-          (300, 4097), (2, 3, 50, 1280)]
+          (300, 4097), (2, 3, 50, 1280), (5, 2056), (7, 12288), (9, 8192)]
 SLACK = 1.02
 
 
