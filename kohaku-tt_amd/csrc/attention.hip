@@ -335,10 +335,11 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
             typename std::conditional<MK == MK_BF16 || MK == MK_F16, uint16_t, float>::type>::type MRaw;
     MRaw mpre[MASKED ? NQB : 1][KB][4];
 
-    v8 kreg[KD ? KB : 1][KD ? DC : 1];
+    typedef v8 KRegs[KD ? KB : 1][KD ? DC : 1];
+    KRegs kreg, kreg2;  // KD: two sets, each loaded two of this wavefront's tiles ahead
     u32x4 kst[KD ? 1 : KIT];
     u32x4 vreg[KIT];
-    auto load_k = [&](int t) {
+    auto load_k = [&](int t, KRegs& kr) {
         const int key0 = t * WN;
         const T* ksrc = kq + static_cast<int64_t>(key0) * ks2;
         const bool full = key0 + WN <= lk;  // uniform: the common case loads unconditionally
@@ -348,12 +349,12 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
 #pragma unroll
                 for (int c = 0; c < DC; ++c) {
                     if (full) {
-                        kreg[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
+                        kr[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
                     } else if (key0 + 16 * kb + l16 < lk) {
-                        kreg[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
+                        kr[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
                     } else {
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) kreg[kb][c][j] = static_cast<T>(0.f);
+                        for (int j = 0; j < 8; ++j) kr[kb][c][j] = static_cast<T>(0.f);
                     }
                 }
             }
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         }
     };
     auto load_tile = [&](int t) {
-        load_k(t);
+        load_k(t, kreg);
         load_v(t);
     };
     // V (and staged K) rows as loaded.
@@ -417,7 +418,11 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     // (every element of lacc[b] holds lane l16's row sum), the reference point m (base-2
     // logit units), m + 8 (the lazy-rescale threshold) and -m for the exponent.
     f32x4 o[DB][NQB];
-    f32x4 lacc[NQB];
+    // Row sums as MFMA columns where the 64-row tiles leave registers to spare; otherwise
+    // per-lane fp32 partial sums reduced across the row's four lanes at the end.
+    constexpr bool LMFMA = NQB == 4;
+    f32x4 lacc[LMFMA ? NQB : 1];
+    float lsum[LMFMA ? 1 : NQB];
     float m_run[NQB], m_thr[NQB], neg_m[NQB];
     bool raw[NQB];
 #pragma unroll
@@ -426,7 +431,11 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         m_run[b] = -INFINITY;
         m_thr[b] = -INFINITY;
         neg_m[b] = 0.f;
-        lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (LMFMA) {
+            lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            lsum[b] = 0.f;
+        }
 #pragma unroll
         for (int d = 0; d < DB; ++d) o[d][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -504,58 +513,9 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
         return t;
     };
 
-    int t = next_tile(t_spec);
-    if (t != t_spec && t < t_end) load_tile(t);
-    while (t < t_end) {
-        // LDS runs one wavefront's instructions in order: the previous tile's reads were
-        // issued before these writes and this tile's reads come after them, so only the
-        // compiler must keep the order (no wait for the writes).
-        __asm__ volatile("" ::: "memory");
-        store_tile();
-        MRaw mcur[MASKED ? NQB : 1][KB][4];
-        if constexpr (MASKED) {
-#pragma unroll
-            for (int b = 0; b < NQB; ++b)
-#pragma unroll
-                for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) mcur[b][kb][i] = mpre[b][kb][i];
-        }
-        const int t_next = next_tile(t + NWAVES);
-        // S^T = K Q^T.  KD: from the K registers, whose next loads go out once they are
-        // consumed; otherwise from the LDS tile, with the whole next tile requested first.
-        f32x4 s[KB][NQB];
-        if constexpr (KD) {
-            if (t_next < t_end) load_v(t_next);
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-                for (int b = 0; b < NQB; ++b) {
-                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kreg[kb][c], qf[b][c], s[kb][b]);
-                }
-            }
-            if (t_next < t_end) load_k(t_next);
-        } else {
-            if (t_next < t_end) load_tile(t_next);
-            v8 kf[KB][DC];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-                for (int c = 0; c < DC; ++c)
-                    kf[kb][c] = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
-            }
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-                for (int b = 0; b < NQB; ++b) {
-                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
-                }
-            }
-        }
+    // Softmax and PV of tile t from its S^T accumulators (and mask values).
+    typedef MRaw MCur[MASKED ? NQB : 1][KB][4];
+    auto consume = [&](const int t, const f32x4 (&s)[KB][NQB], const MCur& mcur) {
         const int key0 = t * WN;
         const bool edge = key0 + WN > lim_min;
         // x: logits in base-2 units times 1 / xs.  Mask-free rows keep the raw accumulators
@@ -637,7 +597,11 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
                     neg_m[b] = -mt;
                 }
                 if (__builtin_amdgcn_ballot_w64(move)) {
-                    lacc[b] *= alpha;
+                    if constexpr (LMFMA) {
+                        lacc[b] *= alpha;
+                    } else {
+                        lsum[b] *= alpha;
+                    }
 #pragma unroll
                     for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
                 }
@@ -659,17 +623,111 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
             v8 pf;
+            float ls = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                pf[i] = static_cast<T>(__builtin_amdgcn_exp2f(__builtin_fmaf(x[b][0][i], xs, neg_m[b])));
-                pf[4 + i] = static_cast<T>(__builtin_amdgcn_exp2f(__builtin_fmaf(x[b][1][i], xs, neg_m[b])));
+                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][0][i], xs, neg_m[b]));
+                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][1][i], xs, neg_m[b]));
+                if constexpr (!LMFMA) ls += e0 + e1;
+                pf[i] = static_cast<T>(e0);
+                pf[4 + i] = static_cast<T>(e1);
             }
-            lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
+            if constexpr (LMFMA) {
+                lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
+            } else {
+                lsum[b] += ls;
+            }
 #pragma unroll
             for (int d = 0; d < DB; ++d) o[d][b] = Mfma<T>::run(vf[d], pf, o[d][b]);
         }
         __builtin_amdgcn_iglp_opt(2);
-        t = t_next;
+    };
+    auto take_mask = [&](MCur& mcur) {
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int b = 0; b < NQB; ++b)
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mcur[b][kb][i] = mpre[b][kb][i];
+        }
+    };
+
+    int t = next_tile(t_spec);
+    if (t != t_spec && t < t_end) load_tile(t);
+    if constexpr (KD) {
+        // K fragments in registers.  32-row workgroups keep two sets: tile t's in one while
+        // the tile after next loads into the other (a full iteration of cover).  64-row
+        // workgroups have no registers to spare: the next tile's K loads into the set the
+        // S MFMAs just consumed.  V is one tile ahead either way.
+        constexpr bool K2 = NQB == 2;
+        int t1 = next_tile(t + NWAVES);
+        if (K2 && t < t_end && t1 < t_end) load_k(t1, kreg2);
+        auto step = [&](KRegs& kc) {
+            // LDS keeps one wavefront's accesses in order (the previous tile's reads,
+            // these writes, this tile's reads): only the compiler must keep it.
+            __asm__ volatile("" ::: "memory");
+            store_tile();
+            MCur mcur;
+            take_mask(mcur);
+            const int t_next = t1;
+            if (t_next < t_end) load_v(t_next);
+            f32x4 s[KB][NQB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int b = 0; b < NQB; ++b) {
+                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kc[kb][c], qf[b][c], s[kb][b]);
+                }
+            }
+            const int t_nn = t_next < t_end ? next_tile(t_next + NWAVES) : t_end;
+            if constexpr (K2) {
+                if (t_nn < t_end) load_k(t_nn, kc);
+            } else {
+                if (t_next < t_end) load_k(t_next, kc);
+            }
+            consume(t, s, mcur);
+            t = t_next;
+            t1 = t_nn;
+        };
+        while (t < t_end) {
+            step(kreg);
+            if (!K2 || t >= t_end) continue;
+            step(kreg2);
+        }
+    } else {
+        while (t < t_end) {
+            // LDS keeps one wavefront's accesses in order (the previous tile's reads,
+            // these writes, this tile's reads): only the compiler must keep it.
+            __asm__ volatile("" ::: "memory");
+            store_tile();
+            MCur mcur;
+            take_mask(mcur);
+            const int t_next = next_tile(t + NWAVES);
+            // S^T = K Q^T from the LDS tile, with the whole next tile requested first.
+            if (t_next < t_end) load_tile(t_next);
+            v8 kf[KB][DC];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int c = 0; c < DC; ++c)
+                    kf[kb][c] = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
+            }
+            f32x4 s[KB][NQB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int b = 0; b < NQB; ++b) {
+                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
+                }
+            }
+            consume(t, s, mcur);
+            t = t_next;
+        }
     }
 
     // Merge the wavefronts' states: (m, l, raw) per wavefront and row as 16-byte records
@@ -680,7 +738,13 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     f32x4* stats = reinterpret_cast<f32x4*>(smem + S::template lds_bytes<T>() - NWAVES * BM * sizeof(f32x4));
     float l_run[NQB];
 #pragma unroll
-    for (int b = 0; b < NQB; ++b) l_run[b] = lacc[b][0];
+    for (int b = 0; b < NQB; ++b) {
+        if constexpr (LMFMA) {
+            l_run[b] = lacc[b][0];
+        } else {
+            l_run[b] = row_sum4(lsum[b]);
+        }
+    }
     auto combine = [&](const f32x4 (&sw)[NWAVES], float (&wt)[NWAVES], float& m, float& lt, bool& any_masked) {
         any_masked = false;
 #pragma unroll
