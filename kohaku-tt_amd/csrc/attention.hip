@@ -35,6 +35,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <mutex>
 #include <type_traits>
@@ -69,6 +70,7 @@ struct AttnParams {
     float scale_log2;
     int splits, tiles_per_split;
     int nx;  // query tiles per (sequence, K/V head)
+    int npair;  // causal: the 2 npair shortest query tiles of a unit run two per workgroup
     int total_q, total_k;  // varlen packed token counts
     int64_t rows_total;
 };
@@ -201,7 +203,7 @@ __device__ __forceinline__ bool row_any4(bool pred, int l16) {
 }
 
 template <typename T, int D, int NQB, int MK>
-__global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
+__device__ __forceinline__ void attn_block(const AttnParams& p, const int split, const int bh, const int xt) {
     typedef typename Mfma<T>::v8 v8;
     typedef Shape<D, NQB> S;
     constexpr int BM = S::BM, VP = S::VP, KP = S::KP, CP = S::CP;
@@ -225,14 +227,6 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int g4 = lane >> 4;
     const int l16 = lane & 15;
 
-    // Work item: heaviest query tiles first (causal), then (sequence, K/V head), split.
-    int lin = blockIdx.x;
-    const int split = lin % p.splits;
-    lin /= p.splits;
-    const int units = p.batch * p.hkv;
-    const int bh = lin % units;
-    int xt = lin / units;
-    if (p.causal) xt = p.nx - 1 - xt;
     const int seq = bh / p.hkv;
     const int kvh = bh - seq * p.hkv;
     const int G = p.group;
@@ -890,6 +884,33 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     }
 }
 
+// Work items: heaviest query tiles first (causal), then (sequence, K/V head), split.  The
+// 2 npair shortest causal query tiles of each unit run two to a workgroup (shortest with
+// longest of that set, so no pair outlasts the heaviest tile), which keeps the grid within
+// one round of resident workgroups.
+template <typename T, int D, int NQB, int MK>
+__global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
+    int lin = blockIdx.x;
+    const int split = lin % p.splits;
+    lin /= p.splits;
+    const int units = p.batch * p.hkv;
+    const int bh = lin % units;
+    const int xi = lin / units;
+    if (!p.causal) {
+        attn_block<T, D, NQB, MK>(p, split, bh, xi);
+        return;
+    }
+    const int singles = p.nx - 2 * p.npair;
+    if (xi < singles) {
+        attn_block<T, D, NQB, MK>(p, split, bh, p.nx - 1 - xi);
+        return;
+    }
+    const int j = xi - singles;
+    attn_block<T, D, NQB, MK>(p, split, bh, 2 * p.npair - 1 - j);
+    __syncthreads();  // the second tile reuses the LDS
+    attn_block<T, D, NQB, MK>(p, split, bh, j);
+}
+
 // Decode: at most 16 "virtual rows" (Sq x G) per (sequence, K/V head).  The key tiles of a
 // unit are dealt round-robin to its wavefronts (wavefront slot s of S takes tiles s, s + S,
 // ...): K goes straight from global memory into MFMA A-operand registers, V through a
@@ -1513,16 +1534,44 @@ size_t ws_bytes_for(const kmi_attn_args* a, const Plan& pl) {
     return static_cast<size_t>(pl.splits) * pl.rows_total * a->heads_q * (a->head_dim + 2) * sizeof(float);
 }
 
+// Compute units of the current device (cached per device id).
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 template <typename T, int D, int NQB, int MK>
-hipError_t launch_fwd(const AttnParams& p, int64_t grid, hipStream_t stream) {
+hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
+    static int per_cu = 0;  // resident workgroups per CU
     const size_t lds = Shape<D, NQB>::template lds_bytes<T>();
+    const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK>);
     std::call_once(once, [&] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        attr_err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (attr_err == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NTHREADS, lds) != hipSuccess)
+            per_cu = 0;
     });
     if (attr_err != hipSuccess) return attr_err;
+    AttnParams p = p_in;
+    p.npair = 0;
+    // Causal grids up to twice the resident workgroups pair their shortest query tiles so
+    // that every workgroup starts at once (larger grids balance over their many rounds).
+    const int64_t units = static_cast<int64_t>(p.batch) * p.hkv;
+    const int64_t slots = static_cast<int64_t>(per_cu) * cu_count();
+    if (p.causal && p.splits == 1 && slots > 0 && grid > slots && grid <= 2 * slots) {
+        const int64_t extra = grid - slots;
+        p.npair = static_cast<int>(std::min<int64_t>(ceil_div(extra, units), p.nx / 2));
+        grid -= static_cast<int64_t>(p.npair) * units;
+    }
     hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds,
                        stream, p);
     return hipGetLastError();
