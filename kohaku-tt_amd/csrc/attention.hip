@@ -202,8 +202,11 @@ __device__ __forceinline__ bool row_any4(bool pred, int l16) {
     return (m & 0x0001000100010001ull) != 0;
 }
 
-template <typename T, int D, int NQB, int MK>
+// RS (row split, short key ranges): each wavefront owns its own 16 NQB rows and runs every
+// key tile itself -- no key split, no merge, no barrier; the workgroup holds 4 row blocks.
+template <typename T, int D, int NQB, int MK, bool RS>
 __device__ __forceinline__ void attn_block(const AttnParams& p, const int split, const int bh, const int xt) {
+    static_assert(!RS || MK == MK_NONE, "row split is for unmasked calls (no block barriers)");
     typedef typename Mfma<T>::v8 v8;
     typedef Shape<D, NQB> S;
     constexpr int BM = S::BM, VP = S::VP, KP = S::KP, CP = S::CP;
@@ -245,8 +248,9 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         row_base = q0;
     }
     const int vrows = lq * G;
-    const int r_begin = xt * BM;
+    const int r_begin = RS ? (xt * NWAVES + wave) * BM : xt * BM;
     if (r_begin >= vrows || lk <= 0) return;
+    constexpr int TS = RS ? 1 : NWAVES;  // tile stride of one wavefront
     const int r_end = min(vrows, r_begin + BM);
     const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys <= i + coff
     int kend = lk;
@@ -450,7 +454,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 
     // Each wavefront's first tile is requested before anything else waits on memory (its
     // loads share one round trip with the Q fragments and the mask-row scan below).
-    const int t_spec = t_begin + wave;
+    const int t_spec = t_begin + (RS ? 0 : wave);
     if (t_spec < t_end) load_tile(t_spec);
 
     // Key-mask tile skipping: with a mask that depends only on the key (a padding mask),
@@ -502,7 +506,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     }
     auto next_tile = [&](int t) {
         if (skip) {
-            while (t < t_end && !tflag[t - t_begin]) t += NWAVES;
+            while (t < t_end && !tflag[t - t_begin]) t += TS;
         }
         return t;
     };
@@ -655,7 +659,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         // workgroups have no registers to spare: the next tile's K loads into the set the
         // S MFMAs just consumed.  V is one tile ahead either way.
         constexpr bool K2 = NQB == 2;
-        int t1 = next_tile(t + NWAVES);
+        int t1 = next_tile(t + TS);
         if (K2 && t < t_end && t1 < t_end) load_k(t1, kreg2);
         auto step = [&](KRegs& kc) {
             // LDS keeps one wavefront's accesses in order (the previous tile's reads,
@@ -676,7 +680,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                     for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kc[kb][c], qf[b][c], s[kb][b]);
                 }
             }
-            const int t_nn = t_next < t_end ? next_tile(t_next + NWAVES) : t_end;
+            const int t_nn = t_next < t_end ? next_tile(t_next + TS) : t_end;
             if constexpr (K2) {
                 if (t_nn < t_end) load_k(t_nn, kc);
             } else {
@@ -699,7 +703,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             store_tile();
             MCur mcur;
             take_mask(mcur);
-            const int t_next = next_tile(t + NWAVES);
+            const int t_next = next_tile(t + TS);
             // S^T = K Q^T from the LDS tile, with the whole next tile requested first.
             if (t_next < t_end) load_tile(t_next);
             v8 kf[KB][DC];
@@ -724,6 +728,32 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         }
     }
 
+    if constexpr (RS) {
+        // The wavefront's rows are complete: normalise and write them (lane (g4, l16) holds
+        // dims 16 d + 4 g4 .. + 3 of row 16 b + l16).
+#pragma unroll
+        for (int b = 0; b < NQB; ++b) {
+            const int r = r_begin + 16 * b + l16;
+            const float l = LMFMA ? lacc[b][0] : row_sum4(lsum[b]);
+            if (r >= r_end) continue;
+            const int pos = r / G;
+            const int head = kvh * G + (r - pos * G);
+            const float inv = l > 0.f ? 1.f / l : 0.f;
+            T* dst = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2];
+            typedef T v4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                v4 w;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(o[d][b][i] * inv);
+                *reinterpret_cast<v4*>(dst + 16 * d + 4 * g4) = w;
+            }
+            if (p.lse && g4 == 0)
+                p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] =
+                    l > 0.f ? (m_run[b] + log2f(l)) * kLn2 : -INFINITY;
+        }
+        return;
+    }
     // Merge the wavefronts' states: (m, l, raw) per wavefront and row as 16-byte records
     // (read back with one load per wavefront, combined without branches) and the O
     // accumulators.  Wavefronts in masked mode (they met a kept key) win; a row none of
@@ -888,7 +918,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 // 2 npair shortest causal query tiles of each unit run two to a workgroup (shortest with
 // longest of that set, so no pair outlasts the heaviest tile), which keeps the grid within
 // one round of resident workgroups.
-template <typename T, int D, int NQB, int MK>
+template <typename T, int D, int NQB, int MK, bool RS>
 __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
     int lin = blockIdx.x;
     const int split = lin % p.splits;
@@ -897,18 +927,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int bh = lin % units;
     const int xi = lin / units;
     if (!p.causal) {
-        attn_block<T, D, NQB, MK>(p, split, bh, xi);
+        attn_block<T, D, NQB, MK, RS>(p, split, bh, xi);
         return;
     }
     const int singles = p.nx - 2 * p.npair;
     if (xi < singles) {
-        attn_block<T, D, NQB, MK>(p, split, bh, p.nx - 1 - xi);
+        attn_block<T, D, NQB, MK, RS>(p, split, bh, p.nx - 1 - xi);
         return;
     }
     const int j = xi - singles;
-    attn_block<T, D, NQB, MK>(p, split, bh, 2 * p.npair - 1 - j);
+    attn_block<T, D, NQB, MK, RS>(p, split, bh, 2 * p.npair - 1 - j);
     __syncthreads();  // the second tile reuses the LDS
-    attn_block<T, D, NQB, MK>(p, split, bh, j);
+    attn_block<T, D, NQB, MK, RS>(p, split, bh, j);
 }
 
 // Decode: at most 16 "virtual rows" (Sq x G) per (sequence, K/V head).  The key tiles of a
@@ -1417,6 +1447,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
 
 struct Plan {
     bool decode;  // attn_decode_kernel: per-wavefront key ranges, fp32 partials + merge
+    bool rs;      // row split: short key ranges, one row block per wavefront
     int nqb, nx, splits, tiles_per_split;
     int64_t rows_total;
     size_t ws_bytes;
@@ -1523,6 +1554,19 @@ Plan make_plan(const kmi_attn_args* a) {
         pl.nqb = 1;
         pl.nx = 1;
     }
+    // Short unmasked, non-causal key ranges (at most 8 tiles): each wavefront takes its own
+    // row block and every key tile, so no wavefront waits on a merge -- when that still
+    // gives every CU a workgroup.
+    if (!pl.decode && pl.splits == 1 && !a->causal && a->mask_mode == KMI_MASK_NONE && nk <= 8) {
+        int q = a->head_dim == 64 ? (ceil_div(vrows, 256) * units >= 512 ? 4 : 2) : 1;
+        if (forced == 1 || forced == 2 || (forced == 4 && a->head_dim == 64)) q = forced;
+        const int64_t nx_rs = ceil_div(vrows, NWAVES * 16 * q);
+        if (nx_rs * units >= 256) {
+            pl.rs = true;
+            pl.nqb = q;
+            pl.nx = static_cast<int>(nx_rs);
+        }
+    }
     pl.rows_total = a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q;
     pl.ws_bytes = 0;
     return pl;
@@ -1547,13 +1591,13 @@ int cu_count() {
     return n;
 }
 
-template <typename T, int D, int NQB, int MK>
+template <typename T, int D, int NQB, int MK, bool RS = false>
 hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     static int per_cu = 0;  // resident workgroups per CU
     const size_t lds = Shape<D, NQB>::template lds_bytes<T>();
-    const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK>);
+    const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK, RS>);
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (attr_err == hipSuccess &&
@@ -1572,7 +1616,7 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
         p.npair = static_cast<int>(std::min<int64_t>(ceil_div(extra, units), p.nx / 2));
         grid -= static_cast<int64_t>(p.npair) * units;
     }
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds,
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK, RS>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds,
                        stream, p);
     return hipGetLastError();
 }
@@ -1616,6 +1660,14 @@ hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream) {
     hipError_t err;
     if (pl.decode) {
         err = launch_decode_mask<T, D>(p, stream);
+    } else if (pl.rs) {
+        if (pl.nqb == 4 && D == 64) {
+            err = launch_fwd<T, 64, 4, MK_NONE, true>(p, grid, stream);
+        } else if (pl.nqb == 2) {
+            err = launch_fwd<T, D, 2, MK_NONE, true>(p, grid, stream);
+        } else {
+            err = launch_fwd<T, D, 1, MK_NONE, true>(p, grid, stream);
+        }
     } else if (pl.nqb == 4 && D == 64) {
         err = launch_mask<T, 64, 4>(p, grid, stream);
     } else if (pl.nqb >= 2) {

@@ -316,3 +316,39 @@ def test_varlen_cross_lengths_bottom_right(native, dev):
     out = native.sdpa_varlen(q.to(dev), k.to(dev), v.to(dev), cu_q, cu_k, is_causal=True).cpu()
     ref, _ = oatt.sdpa_varlen(C.f64(q), C.f64(k), C.f64(v), cu_q, cu_k, is_causal=True)
     assert np.abs(out.double().numpy() - ref).max() < 2e-2
+
+
+@pytest.mark.parametrize(
+    "b,hq,hk,sq,sk,d",
+    [
+        (16, 16, 4, 300, 200, 128),  # GQA, 7 key tiles: one row block per wavefront
+        (8, 8, 8, 512, 100, 64),
+        (32, 8, 2, 128, 256, 64),  # exactly 8 key tiles
+    ],
+)
+def test_short_key_ranges_output_and_lse(native, dev, b, hq, hk, sq, sk, d):
+    """Short unmasked key ranges run one row block per wavefront (no key split, no merge);
+    output and natural-log LSE match the oracle through the C ABI."""
+    from kohakutt_amd import capi
+
+    g = C.gen(500 + sq)
+    q, k, v = C.randn(g, b, hq, sq, d), C.randn(g, b, hk, sk, d), C.randn(g, b, hk, sk, d)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = torch.empty_like(qd)
+    lse = torch.empty(b, hq, sq, dtype=torch.float32, device=dev)
+    a = capi.AttnArgs(
+        q=qd.data_ptr(), k=kd.data_ptr(), v=vd.data_ptr(), out=out.data_ptr(), lse=lse.data_ptr(),
+        dtype=capi.KMI_BF16, causal=0, batch=b, heads_q=hq, heads_kv=hk, seq_q=sq, seq_k=sk,
+        head_dim=d, scale=d**-0.5,
+    )
+    a.q_stride[:] = qd.stride()[:3]
+    a.k_stride[:] = kd.stride()[:3]
+    a.v_stride[:] = vd.stride()[:3]
+    a.o_stride[:] = out.stride()[:3]
+    a.lse_stride[:] = lse.stride()
+    assert capi.workspace_bytes(a) == 0
+    capi.attn_fwd(a, 0, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref, ref_lse = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v))
+    _check(out.cpu(), C.torch_cpu_sdpa(q, k, v), ref, f"short keys {b}x{hq}/{hk}x{sq}x{sk}x{d}")
+    assert np.abs(lse.cpu().double().numpy() - ref_lse).max() < 2e-2
