@@ -152,15 +152,16 @@ __device__ __forceinline__ u32x2 lds_read_tr(const T* p) {
 // Keys per wavefront tile.
 constexpr int WN = 32;
 
-template <int D, int NQB>
+template <int D, int NQB, int TWIDTH = WN>
 struct Shape {
+    static constexpr int TW = TWIDTH;    // keys per wavefront tile
     static constexpr int BM = 16 * NQB;  // rows of a workgroup (shared by its wavefronts)
     static constexpr int VP = D + 16;    // V row pitch (elements): transposed b64 reads of 8 rows hit distinct banks
     static constexpr int KP = D + 8;     // K row pitch (elements): b128 reads of 16 rows hit distinct banks
     // K fragments straight from memory into registers (KD) where the wavefront's 64 rows
     // give each loaded fragment the most use; otherwise K is staged in LDS too.
     static constexpr bool KD = D == 64 && NQB == 4;
-    static constexpr int TILE = (KD ? 0 : WN * KP) + WN * VP;  // elements of one wavefront's tile
+    static constexpr int TILE = (KD ? 0 : TW * KP) + TW * VP;  // elements of one wavefront's tile
     static constexpr int CP = D + 4;     // merge buffer row pitch (floats)
     // The merge runs over groups of MB row blocks whose buffer fits in the tile area
     // (the buffer must not set the workgroup's LDS size, which bounds workgroups per CU).
@@ -204,20 +205,22 @@ __device__ __forceinline__ bool row_any4(bool pred, int l16) {
 
 // RS (row split, short key ranges): each wavefront owns its own 16 NQB rows and runs every
 // key tile itself -- no key split, no merge, no barrier; the workgroup holds 4 row blocks.
-template <typename T, int D, int NQB, int MK, bool RS>
+template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
 __device__ __forceinline__ void attn_block(const AttnParams& p, const int split, const int bh, const int xt) {
     static_assert(!RS || MK == MK_NONE, "row split is for unmasked calls (no block barriers)");
     typedef typename Mfma<T>::v8 v8;
-    typedef Shape<D, NQB> S;
+    typedef Shape<D, NQB, TWIDTH> S;
+    constexpr int TW = S::TW;   // keys per tile
+    constexpr int KH = TW / 32;  // 32-key chunks per tile (one PV MFMA each)
     constexpr int BM = S::BM, VP = S::VP, KP = S::KP, CP = S::CP;
     constexpr bool KD = S::KD;
     constexpr int DC = D / 32;  // 32-wide chunks of the head dim
     constexpr int DB = D / 16;  // 16-wide blocks of the head dim
-    constexpr int KB = WN / 16;
+    constexpr int KB = TW / 16;
     constexpr int VPR = D / 8;           // 16-byte vectors per key row
     constexpr int RPP = kWave / VPR;     // key rows one wavefront pass covers
-    constexpr int KIT = WN / RPP;        // K passes per tile
-    static_assert(KIT >= 1 && WN % RPP == 0, "tile shape");
+    constexpr int KIT = TW / RPP;        // K passes per tile
+    static_assert(KIT >= 1 && TW % RPP == 0, "tile shape");
     constexpr bool MASKED = MK != MK_NONE;
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -255,7 +258,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys <= i + coff
     int kend = lk;
     if (p.causal) kend = max(0, min(lk, (r_end - 1) / G + 1 + coff));
-    const int ntiles = (kend + WN - 1) / WN;
+    const int ntiles = (kend + TW - 1) / TW;
     // Keys below lim_min are visible to every row of the workgroup: tiles past it need the
     // per-element causal / tail test, the rest do not.
     const int lim_min = p.causal ? min(lk, r_begin / G + coff + 1) : lk;
@@ -325,7 +328,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                      : static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * ks2 + 8 * dg;
     const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + krow) * vs2 + 8 * dg;
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
-    T* vl = kl + (KD ? 0 : WN * KP);
+    T* vl = kl + (KD ? 0 : TW * KP);
 
     // Mask values of the staged tile, loaded with its K / V (raw element type; converted
     // when the tile is computed, so the loads stay in flight meanwhile).
@@ -338,9 +341,9 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     u32x4 kst[KD ? 1 : KIT];
     u32x4 vreg[KIT];
     auto load_k = [&](int t, KRegs& kr) {
-        const int key0 = t * WN;
+        const int key0 = t * TW;
         const T* ksrc = kq + static_cast<int64_t>(key0) * ks2;
-        const bool full = key0 + WN <= lk;  // uniform: the common case loads unconditionally
+        const bool full = key0 + TW <= lk;  // uniform: the common case loads unconditionally
         if constexpr (KD) {
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
@@ -371,9 +374,9 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     };
     // V rows and mask values of tile t.
     auto load_v = [&](int t) {
-        const int key0 = t * WN;
+        const int key0 = t * TW;
         const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
-        if (key0 + WN <= lk) {
+        if (key0 + TW <= lk) {
 #pragma unroll
             for (int i = 0; i < KIT; ++i) vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
         } else {
@@ -495,7 +498,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                     for (int j = 0; j < EPV; ++j) {
                         if (mask_logit_of<MK>(e[j]) > kMaskedLogit) {
                             keeps = true;
-                            const int tile = (v * EPV + j) / WN;
+                            const int tile = (v * EPV + j) / TW;
                             if (tile >= t_begin && tile < t_end) tflag[tile - t_begin] = 1;
                         }
                     }
@@ -514,8 +517,8 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // Softmax and PV of tile t from its S^T accumulators (and mask values).
     typedef MRaw MCur[MASKED ? NQB : 1][KB][4];
     auto consume = [&](const int t, const f32x4 (&s)[KB][NQB], const MCur& mcur) {
-        const int key0 = t * WN;
-        const bool edge = key0 + WN > lim_min;
+        const int key0 = t * TW;
+        const bool edge = key0 + TW > lim_min;
         // x: logits in base-2 units times 1 / xs.  Mask-free rows keep the raw accumulators
         // (the scale is folded into the exponent's FMA below), -inf where not visible.
         float x[NQB][KB][4];
@@ -582,8 +585,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         // it pays for the row reduction, the move and the O / l rescale.
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            const float lmax = fmaxf(fmaxf(fmaxf(x[b][0][0], x[b][0][1]), fmaxf(x[b][0][2], x[b][0][3])),
-                                     fmaxf(fmaxf(x[b][1][0], x[b][1][1]), fmaxf(x[b][1][2], x[b][1][3])));
+            float lmax = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                lmax = fmaxf(lmax, fmaxf(fmaxf(x[b][kb][0], x[b][kb][1]), fmaxf(x[b][kb][2], x[b][kb][3])));
             if (__builtin_amdgcn_ballot_w64(lmax * xs > m_thr[b])) {
                 const float mt = row_max4(lmax) * xs;
                 const bool move = mt > m_thr[b];
@@ -608,35 +613,37 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         // O^T += V^T P^T, and l += P 1 (the row sums of the bf16 weights, as MFMA columns).
         // The V fragments are requested first; the MFMAs of row block b then interleave
         // with the exponentials of row block b + 1 (scheduling groups below).
-        v8 vf[DB];
-        {
-            const T* vsrc = vl + (4 * g4 + (l16 >> 2)) * VP + 4 * (l16 & 3);
+        v8 vf[KH][DB];
+#pragma unroll
+        for (int h = 0; h < KH; ++h) {
+            const T* vsrc = vl + (32 * h + 4 * g4 + (l16 >> 2)) * VP + 4 * (l16 & 3);
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
-                const u32x2 lo = lds_read_tr(vsrc + 16 * d);            // keys 4 g + s
-                const u32x2 hi = lds_read_tr(vsrc + 16 * VP + 16 * d);  // keys 16 + 4 g + s
-                vf[d] = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                const u32x2 lo = lds_read_tr(vsrc + 16 * d);            // keys 32 h + 4 g + s
+                const u32x2 hi = lds_read_tr(vsrc + 16 * VP + 16 * d);  // keys 32 h + 16 + 4 g + s
+                vf[h][d] = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
             }
         }
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            v8 pf;
             float ls = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][0][i], xs, neg_m[b]));
-                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][1][i], xs, neg_m[b]));
-                if constexpr (!LMFMA) ls += e0 + e1;
-                pf[i] = static_cast<T>(e0);
-                pf[4 + i] = static_cast<T>(e1);
-            }
-            if constexpr (LMFMA) {
-                lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
-            } else {
-                lsum[b] += ls;
-            }
+            for (int h = 0; h < KH; ++h) {
+                // The 32 keys of chunk h: S accumulator blocks 2 h and 2 h + 1.
+                v8 pf;
 #pragma unroll
-            for (int d = 0; d < DB; ++d) o[d][b] = Mfma<T>::run(vf[d], pf, o[d][b]);
+                for (int i = 0; i < 4; ++i) {
+                    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * h][i], xs, neg_m[b]));
+                    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * h + 1][i], xs, neg_m[b]));
+                    if constexpr (!LMFMA) ls += e0 + e1;
+                    pf[i] = static_cast<T>(e0);
+                    pf[4 + i] = static_cast<T>(e1);
+                }
+                if constexpr (LMFMA) lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
+#pragma unroll
+                for (int d = 0; d < DB; ++d) o[d][b] = Mfma<T>::run(vf[h][d], pf, o[d][b]);
+            }
+            if constexpr (!LMFMA) lsum[b] += ls;
         }
         __builtin_amdgcn_iglp_opt(2);
     };
@@ -918,7 +925,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 // 2 npair shortest causal query tiles of each unit run two to a workgroup (shortest with
 // longest of that set, so no pair outlasts the heaviest tile), which keeps the grid within
 // one round of resident workgroups.
-template <typename T, int D, int NQB, int MK, bool RS>
+template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
 __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
     int lin = blockIdx.x;
     const int split = lin % p.splits;
@@ -927,18 +934,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int bh = lin % units;
     const int xi = lin / units;
     if (!p.causal) {
-        attn_block<T, D, NQB, MK, RS>(p, split, bh, xi);
+        attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, xi);
         return;
     }
     const int singles = p.nx - 2 * p.npair;
     if (xi < singles) {
-        attn_block<T, D, NQB, MK, RS>(p, split, bh, p.nx - 1 - xi);
+        attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, p.nx - 1 - xi);
         return;
     }
     const int j = xi - singles;
-    attn_block<T, D, NQB, MK, RS>(p, split, bh, 2 * p.npair - 1 - j);
+    attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, 2 * p.npair - 1 - j);
     __syncthreads();  // the second tile reuses the LDS
-    attn_block<T, D, NQB, MK, RS>(p, split, bh, j);
+    attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, j);
 }
 
 // Decode: at most 16 "virtual rows" (Sq x G) per (sequence, K/V head).  The key tiles of a
@@ -1591,13 +1598,13 @@ int cu_count() {
     return n;
 }
 
-template <typename T, int D, int NQB, int MK, bool RS = false>
+template <typename T, int D, int NQB, int MK, bool RS = false, int TWIDTH = WN>
 hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     static int per_cu = 0;  // resident workgroups per CU
-    const size_t lds = Shape<D, NQB>::template lds_bytes<T>();
-    const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK, RS>);
+    const size_t lds = Shape<D, NQB, TWIDTH>::template lds_bytes<T>();
+    const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH>);
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (attr_err == hipSuccess &&
@@ -1616,7 +1623,7 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
         p.npair = static_cast<int>(std::min<int64_t>(ceil_div(extra, units), p.nx / 2));
         grid -= static_cast<int64_t>(p.npair) * units;
     }
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK, RS>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds,
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds,
                        stream, p);
     return hipGetLastError();
 }
