@@ -322,11 +322,22 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // (g4, l16) holds key 16 kb + l16, dims 32 c + 8 g4 .. + 7 of S^T = K Q^T.  Otherwise
     // K rows are staged through the wavefront's LDS tile like V (key row `krow` + RPP
     // per pass); V always is, for the transposed reads.
+    //
+    // Tiles load through a buffer resource per tile, based at its first key and ending at
+    // the unit's last key (at most one tile of rows): rows past the end read as zeros, with
+    // no tail branches.  Row strides are at most 2^24 elements (checked on the host), so the
+    // in-tile byte offsets fit 32 bits.
     const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
-    const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
-    const T* kq = KD ? static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + l16) * ks2 + 8 * g4
-                     : static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + krow) * ks2 + 8 * dg;
-    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + krow) * vs2 + 8 * dg;
+    const int64_t kstride = p.ks[2] * static_cast<int64_t>(sizeof(T)), vstride = p.vs[2] * static_cast<int64_t>(sizeof(T));
+    const char* kunit = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] +
+                                                      static_cast<int64_t>(k0) * p.ks[2]);
+    const char* vunit = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] +
+                                                      static_cast<int64_t>(k0) * p.vs[2]);
+    const uint32_t k_lane = KD ? static_cast<uint32_t>(l16 * kstride + 16 * g4) : static_cast<uint32_t>(krow * kstride + 16 * dg);
+    const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dg);
+    // Bytes per key of a resource's range (a zero row stride repeats one row).
+    const uint32_t kspan = static_cast<uint32_t>(kstride > 0 ? kstride : D * static_cast<int64_t>(sizeof(T)));
+    const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : D * static_cast<int64_t>(sizeof(T)));
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
     T* vl = kl + (KD ? 0 : TW * KP);
 
@@ -340,52 +351,33 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     KRegs kreg, kreg2;  // KD: two sets, each loaded two of this wavefront's tiles ahead
     u32x4 kst[KD ? 1 : KIT];
     u32x4 vreg[KIT];
+    // The row shifts of a tile's passes are uniform; the compiler barrier on them keeps the
+    // per-lane offsets from being precomputed into registers held across the loop.
     auto load_k = [&](int t, KRegs& kr) {
         const int key0 = t * TW;
-        const T* ksrc = kq + static_cast<int64_t>(key0) * ks2;
-        const bool full = key0 + TW <= lk;  // uniform: the common case loads unconditionally
+        const auto rs = buffer_rsrc(kunit + key0 * kstride, static_cast<uint32_t>(min(lk - key0, TW)) * kspan);
+        uint32_t step = static_cast<uint32_t>(kstride);
+        __asm__ volatile("" : "+s"(step));
         if constexpr (KD) {
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-                for (int c = 0; c < DC; ++c) {
-                    if (full) {
-                        kr[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
-                    } else if (key0 + 16 * kb + l16 < lk) {
-                        kr[kb][c] = *reinterpret_cast<const v8*>(ksrc + (16 * kb) * ks2 + 32 * c);
-                    } else {
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) kr[kb][c][j] = static_cast<T>(0.f);
-                    }
-                }
+                for (int c = 0; c < DC; ++c)
+                    kr[kb][c] = __builtin_bit_cast(v8, buffer_load16(rs, k_lane + 16 * kb * step + 64 * c));
             }
         } else {
-            if (full) {
 #pragma unroll
-                for (int i = 0; i < KIT; ++i) kst[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
-            } else {
-#pragma unroll
-                for (int i = 0; i < KIT; ++i) {
-                    kst[i] = u32x4{0u, 0u, 0u, 0u};
-                    if (key0 + krow + i * RPP < lk) kst[i] = *reinterpret_cast<const u32x4*>(ksrc + (i * RPP) * ks2);
-                }
-            }
+            for (int i = 0; i < KIT; ++i) kst[i] = buffer_load16(rs, k_lane + i * RPP * step);
         }
     };
     // V rows and mask values of tile t.
     auto load_v = [&](int t) {
         const int key0 = t * TW;
-        const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
-        if (key0 + TW <= lk) {
+        const auto rs = buffer_rsrc(vunit + key0 * vstride, static_cast<uint32_t>(min(lk - key0, TW)) * vspan);
+        uint32_t step = static_cast<uint32_t>(vstride);
+        __asm__ volatile("" : "+s"(step));
 #pragma unroll
-            for (int i = 0; i < KIT; ++i) vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
-        } else {
-#pragma unroll
-            for (int i = 0; i < KIT; ++i) {
-                vreg[i] = u32x4{0u, 0u, 0u, 0u};
-                if (key0 + krow + i * RPP < lk) vreg[i] = *reinterpret_cast<const u32x4*>(vsrc + (i * RPP) * vs2);
-            }
-        }
+        for (int i = 0; i < KIT; ++i) vreg[i] = buffer_load16(rs, v_lane + i * RPP * step);
         if constexpr (MASKED) {
             const MRaw* mp = static_cast<const MRaw*>(mptr);
 #pragma unroll
@@ -1092,11 +1084,19 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     };
 
     // K fragments of a tile come straight from memory: lane (g4, l16) holds key
-    // 16 kb + l16, dims 32 c + 8 g4 .. + 7 -- the A operand of S^T = K Q^T.
-    const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
-    const T* kq = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0 + l16) * ks2 + 8 * g4;
+    // 16 kb + l16, dims 32 c + 8 g4 .. + 7 -- the A operand of S^T = K Q^T.  Both K and V
+    // load through one buffer resource per tile that ends at the unit's last key (rows past
+    // it read as zeros).
+    const int64_t kstride = p.ks[2] * static_cast<int64_t>(sizeof(T)), vstride = p.vs[2] * static_cast<int64_t>(sizeof(T));
+    const char* kunit = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] +
+                                                      static_cast<int64_t>(k0) * p.ks[2]);
+    const char* vunit = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] +
+                                                      static_cast<int64_t>(k0) * p.vs[2]);
     const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
-    const T* vbase = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0 + krow) * vs2 + 8 * dg;
+    const uint32_t k_lane = static_cast<uint32_t>(l16 * kstride + 16 * g4);
+    const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dg);
+    const uint32_t kspan = static_cast<uint32_t>(kstride > 0 ? kstride : D * static_cast<int64_t>(sizeof(T)));
+    const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : D * static_cast<int64_t>(sizeof(T)));
     T* vl = reinterpret_cast<T*>(smem) + wave * WN * VP;
 
     v8 kreg[KB][DC];
@@ -1104,26 +1104,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     MRaw mpre[MASKED ? KB : 1][4];
     auto load_tile = [&](int i) {
         const int key0 = (slot + i * nslots) * WN;
-        const bool full = key0 + WN <= lk;
+        const uint32_t rows = static_cast<uint32_t>(min(lk - key0, WN));
+        const auto rk = buffer_rsrc(kunit + key0 * kstride, rows * kspan);
+        const auto rv = buffer_rsrc(vunit + key0 * vstride, rows * vspan);
+        uint32_t kst = static_cast<uint32_t>(kstride), vst = static_cast<uint32_t>(vstride);
+        __asm__ volatile("" : "+s"(kst), "+s"(vst));
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-            const bool ok = full || key0 + 16 * kb + l16 < lk;
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                if (ok) {
-                    kreg[kb][c] = *reinterpret_cast<const v8*>(kq + static_cast<int64_t>(key0 + 16 * kb) * ks2 + 32 * c);
-                } else {
+            for (int c = 0; c < DC; ++c)
+                kreg[kb][c] = __builtin_bit_cast(v8, buffer_load16(rk, k_lane + 16 * kb * kst + 64 * c));
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) kreg[kb][c][j] = static_cast<T>(0.f);
-                }
-            }
-        }
-        const T* vsrc = vbase + static_cast<int64_t>(key0) * vs2;
-#pragma unroll
-        for (int i2 = 0; i2 < KIT; ++i2) {
-            vreg[i2] = u32x4{0u, 0u, 0u, 0u};
-            if (full || key0 + krow + i2 * RPP < lk) vreg[i2] = *reinterpret_cast<const u32x4*>(vsrc + (i2 * RPP) * vs2);
-        }
+        for (int i2 = 0; i2 < KIT; ++i2) vreg[i2] = buffer_load16(rv, v_lane + i2 * RPP * vst);
         if constexpr (MASKED) {
             const MRaw* mp = static_cast<const MRaw*>(p.mask);
 #pragma unroll
@@ -1476,6 +1468,8 @@ const char* check_args(const kmi_attn_args* a) {
             return "q, k and v strides must be multiples of 8 elements";
         if (a->o_stride[i] % 4) return "out strides must be multiples of 4 elements";
     }
+    if (a->k_stride[2] < 0 || a->k_stride[2] > (1 << 24) || a->v_stride[2] < 0 || a->v_stride[2] > (1 << 24))
+        return "k and v row strides must be within [0, 2^24] elements";
     if (a->seq_q > (1 << 30) / 64 || a->seq_k > (1 << 30) || a->heads_q > 65536)
         return "sizes too large";
     const bool varlen = a->cu_seqlens_q != nullptr;

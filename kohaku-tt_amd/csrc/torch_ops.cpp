@@ -114,9 +114,10 @@ std::string sdpa_refusal_impl(const Tensor& q, const Tensor& k, const Tensor& v,
 }
 
 // q/k/v as the kernels read them: last-dim stride 1, 16-byte aligned, strides multiples
-// of 8 elements; anything else is copied once.
-Tensor kernel_operand(const Tensor& t) {
-    bool ok = t.stride(-1) == 1 && reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0;
+// of 8 elements, the sequence (row) stride within [0, 2^24]; anything else is copied once.
+Tensor kernel_operand(const Tensor& t, int64_t row_dim) {
+    bool ok = t.stride(-1) == 1 && reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0 && t.stride(row_dim) >= 0 &&
+              t.stride(row_dim) <= (1 << 24);
     for (int64_t i = 0; ok && i + 1 < t.dim(); ++i) ok = t.stride(i) % 8 == 0;
     return ok ? t : t.contiguous();
 }
@@ -150,9 +151,9 @@ AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in
         k = k.to(at::kBFloat16);
         v = v.to(at::kBFloat16);
     }
-    q = kernel_operand(q);
-    k = kernel_operand(k);
-    v = kernel_operand(v);
+    q = kernel_operand(q, 2);
+    k = kernel_operand(k, 2);
+    v = kernel_operand(v, 2);
     const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3);
     const int64_t Hk = k.size(1), Sk = k.size(2);
     Tensor out = at::empty({B, H, Sq, D}, q.options());
@@ -320,9 +321,9 @@ std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, c
     TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type() &&
                     (q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf),
                 "kohakutt_amd: sdpa_varlen takes bf16 / fp16 (or fp32, cast to bf16)");
-    q = kernel_operand(q);
-    k = kernel_operand(k);
-    v = kernel_operand(v);
+    q = kernel_operand(q, 0);
+    k = kernel_operand(k, 0);
+    v = kernel_operand(v, 0);
     const int64_t nseq = cu_q_in.numel() - 1;
     TORCH_CHECK(nseq >= 1 && cu_k_in.numel() == cu_q_in.numel(),
                 "kohakutt_amd: sdpa_varlen needs cumulative offsets [0, ..., total] of equal count for queries and keys");

@@ -76,6 +76,8 @@ def _args(**kw):
         (dict(mask_mode=capi.KMI_MASK_STRIDED), "mask_mode set without a mask"),
         (dict(mask_mode=capi.KMI_MASK_PACKED, mask=0x2000, mask_dtype=capi.KMI_BOOL), "varlen only"),
         (dict(cu_seqlens_q=0x3000), "go together"),
+        (dict(k_stride=(ctypes.c_int64 * 3)(4 * 8 * 64, 8 * 64, (1 << 24) + 8)), "row strides"),
+        (dict(v_stride=(ctypes.c_int64 * 3)(4 * 8 * 64, 8 * 64, -64)), "row strides"),
     ],
 )
 def test_attention_rejects_malformed_calls(kw, msg):

@@ -366,3 +366,38 @@ def test_causal_paired_query_tiles(native, dev, b, hq, hk, s):
     again = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev), is_causal=True,
                                            enable_gqa=hq != hk).cpu()
     assert torch.equal(again, out)
+
+
+@pytest.mark.parametrize("sk,d,causal", [(77, 64, False), (301, 128, False), (130, 64, True)])
+def test_broadcast_key_rows_and_partial_tiles(native, dev, sk, d, causal):
+    """K and V given with a zero sequence stride (one row repeated over every key: an
+    expanded view) and key counts that end inside a tile: the tile loads read the repeated
+    row and stop at the last key.  The result equals the oracle on the materialised K/V
+    (for non-causal rows: exactly V's row, since every key scores the same)."""
+    from kohakutt_amd import capi
+
+    b, hq, hk, sq = 2, 8, 2, 96
+    g = C.gen(700 + sk)
+    q = C.randn(g, b, hq, sq, d)
+    k1, v1 = C.randn(g, b, hk, 1, d), C.randn(g, b, hk, 1, d)
+    k, v = k1.expand(b, hk, sk, d), v1.expand(b, hk, sk, d)
+    qd, kd, vd = q.to(dev), k1.to(dev).expand(b, hk, sk, d), v1.to(dev).expand(b, hk, sk, d)
+    assert kd.stride(2) == 0 and vd.stride(2) == 0
+    out = torch.empty_like(qd)
+    a = capi.AttnArgs(
+        q=qd.data_ptr(), k=kd.data_ptr(), v=vd.data_ptr(), out=out.data_ptr(), lse=0,
+        dtype=capi.KMI_BF16, causal=int(causal), batch=b, heads_q=hq, heads_kv=hk, seq_q=sq, seq_k=sk,
+        head_dim=d, scale=d**-0.5,
+    )
+    a.q_stride[:] = qd.stride()[:3]
+    a.k_stride[:] = kd.stride()[:3]
+    a.v_stride[:] = vd.stride()[:3]
+    a.o_stride[:] = out.stride()[:3]
+    n = capi.workspace_bytes(a)
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=dev)
+    capi.attn_fwd(a, ws.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k.contiguous()), C.f64(v.contiguous()), is_causal=causal)
+    err = np.abs(out.cpu().double().numpy() - ref)
+    # Every visible key holds the same V row: the output is that row, rounded to bf16.
+    assert err.max() < 1e-2, err.max()
