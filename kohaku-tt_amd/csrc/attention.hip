@@ -203,6 +203,19 @@ __device__ __forceinline__ bool row_any4(bool pred, int l16) {
     return (m & 0x0001000100010001ull) != 0;
 }
 
+// Mask value of key `key` of the mask row at `mrow` (zero when the key is out of range),
+// read from a clamped, always-valid index: every lane loads, and a group of such loads
+// shares one round trip (a per-lane branch around each load can make each wait in turn).
+// Used where the loads are few (the decode skip scan); needs lk >= 1 and m_end >= 1.
+template <typename MRaw>
+__device__ __forceinline__ MRaw mask_load(const MRaw* mp, int64_t mrow, int key, int lk, int64_t m_key, int64_t m_end) {
+    const int kc = min(max(key, 0), lk - 1);
+    const int64_t mi = min(mrow + static_cast<int64_t>(kc) * m_key, m_end - 1);
+    const bool ok = key >= 0 && key < lk && mrow + static_cast<int64_t>(key) * m_key < m_end;
+    const MRaw v = mp[mi];
+    return ok ? v : MRaw{};
+}
+
 // RS (row split, short key ranges): each wavefront owns its own 16 NQB rows and runs every
 // key tile itself -- no key split, no merge, no barrier; the workgroup holds 4 row blocks.
 template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
@@ -290,15 +303,9 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         const int head = kvh * G + (rr - pos * G);
         lim[b] = p.causal ? min(lk, pos + coff + 1) : lk;  // keys [0, lim) are visible
         const T* src = qp + qb_off + head * p.qs[1] + static_cast<int64_t>(q0 + pos) * p.qs[2];
+        // Rows past the end read row r_begin (in range) and are never written.
 #pragma unroll
-        for (int c = 0; c < DC; ++c) {
-            if (valid) {
-                qf[b][c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qf[b][c][j] = static_cast<T>(0.f);
-            }
-        }
+        for (int c = 0; c < DC; ++c) qf[b][c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
         if constexpr (MASKED) {
             if (p.mask_mode == KMI_MASK_PACKED) {
                 int64_t m_seq = 0;
@@ -1010,15 +1017,9 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     v8 qf[DC];
     {
         const T* src = static_cast<const T*>(p.q) + qb_off + head * p.qs[1] + static_cast<int64_t>(q0 + pos) * p.qs[2];
+        // Lanes past the last row read row 0 (in range) and are never written.
 #pragma unroll
-        for (int c = 0; c < DC; ++c) {
-            if (valid) {
-                qf[c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qf[c][j] = static_cast<T>(0.f);
-            }
-        }
+        for (int c = 0; c < DC; ++c) qf[c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
     }
     int64_t mrow = 0, m_key = 0, m_end = 0;
     bool shared_row = false;
@@ -1047,20 +1048,19 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
 
     // Tiles this wavefront runs: bit i of `live` stands for tile slot + i * nslots.
     uint32_t live = 0xffffffffu;
-    const bool use_bits = MASKED && shared_row && n_t <= 2 * SCAN;
+    const bool use_bits = MASKED && shared_row && n_t > 0 && n_t <= 2 * SCAN;
     if constexpr (MASKED) {
         if (use_bits) {
             const MRaw* mp = static_cast<const MRaw*>(p.mask);
             const int lim0 = p.causal ? min(lk, coff + 1) : lk;
             const int pk = lane;
-            const MRaw first = (pk < lim0 && mrow + pk * m_key < m_end) ? mp[mrow + pk * m_key] : MRaw{};
+            const MRaw first = mask_load(mp, mrow, pk < lim0 ? pk : -1, lk, m_key, m_end);
             MRaw sv[SCAN];
 #pragma unroll
             for (int j = 0; j < SCAN; ++j) {
                 const int i = 2 * j + (lane >> 5);
                 const int key = (slot + i * nslots) * WN + (lane & 31);
-                const int64_t mi = mrow + static_cast<int64_t>(key) * m_key;
-                sv[j] = (i < n_t && key < lk && mi < m_end) ? mp[mi] : MRaw{};
+                sv[j] = mask_load(mp, mrow, i < n_t ? key : -1, lk, m_key, m_end);
             }
             const bool proof = __builtin_amdgcn_ballot_w64(pk < lim0 && mask_logit_of<MK>(first) > kMaskedLogit) != 0;
             if (proof) {
@@ -1354,12 +1354,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     bool any_masked = false;  // some split met a kept key: raw-score partials drop out
     if (p.splits <= 32) {
         // Every split's statistics (lane s) and O values in one round of loads.
-        float lse = -INFINITY, flag = 1.f;
-        if (lane < p.splits) {
-            const float* e = p.part_lse + 2 * (lane * stride + item);
-            lse = e[0];
-            flag = e[1];
-        }
+        // Lanes past the last split read the last split's record (one round of loads, no
+        // per-lane branch) and drop it.
+        const float* e = p.part_lse + 2 * (min(lane, p.splits - 1) * stride + item);
+        const float e0 = e[0], e1 = e[1];
+        float lse = lane < p.splits ? e0 : -INFINITY;
+        const float flag = lane < p.splits ? e1 : 1.f;
         float v[32][PER];
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
