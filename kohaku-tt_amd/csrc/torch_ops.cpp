@@ -47,6 +47,8 @@ bool env_on(const char* name) {
 // switches them at run time.
 std::atomic<bool> g_attention{env_on("KMI_ATTENTION")};
 std::atomic<bool> g_norms{env_on("KMI_NORMS")};
+// KMI_PITCHED_OUT=0 (read at load) keeps the attention output dense for head-view inputs.
+const bool g_pitched_out = env_on("KMI_PITCHED_OUT");
 // Calls the kernels took, per family (ktt::counters).
 std::atomic<int64_t> g_attn_calls{0}, g_norm_calls{0}, g_attn_declined{0};
 
@@ -139,6 +141,27 @@ struct AttnOut {
     Tensor out, lse;
 };
 
+// `t` [B, H, S, D] as a head view of a [B, S, C] row-major projection (a fused qkv or a
+// separate one): heads adjacent within a row of pitch C (the reference's head_view,
+// core/torch/views.cpp:808-830, without its 32-element tile alignment).
+bool head_view(const Tensor& t) {
+    if (t.dim() != 4 || t.numel() == 0 || t.stride(3) != 1) return false;
+    const int64_t b = t.size(0), h = t.size(1), s = t.size(2), d = t.size(3), c = t.stride(2);
+    return (h == 1 || t.stride(1) == d) && c >= h * d && (b == 1 || t.stride(0) == s * c);
+}
+
+// The pitched route's output (aten_attention.cpp:605-628): with q, k and v head views of
+// [B, S, C] projections, no mask and no gradients, the output is a [B, H, S, D] view of a
+// dense [B, S, H D] tensor, so that transposing it back to the projection layout is free.
+Tensor attention_output(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, bool masked, const Tensor& q) {
+    const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3);
+    const bool pitched = g_pitched_out && !masked && q_in.scalar_type() == at::kBFloat16 && !q_in.requires_grad() &&
+                         !k_in.requires_grad() && !v_in.requires_grad() && head_view(q_in) && head_view(k_in) &&
+                         head_view(v_in);
+    if (!pitched) return at::empty({B, H, Sq, D}, q.options());
+    return at::empty({B, Sq, H * D}, q.options()).as_strided({B, H, Sq, D}, {Sq * H * D, D, H * D, 1});
+}
+
 AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, const optional<Tensor>& mask,
                       bool is_causal, optional<double> scale) {
     c10::DeviceGuard guard(q_in.device());
@@ -156,7 +179,7 @@ AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in
     v = kernel_operand(v, 2);
     const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3);
     const int64_t Hk = k.size(1), Sk = k.size(2);
-    Tensor out = at::empty({B, H, Sq, D}, q.options());
+    Tensor out = attention_output(q_in, k_in, v_in, mask_given(mask), q);
     Tensor lse = at::empty({B, H, Sq}, q.options().dtype(at::kFloat));
     kmi_attn_args a{};
     a.q = q.data_ptr();

@@ -401,3 +401,42 @@ def test_broadcast_key_rows_and_partial_tiles(native, dev, sk, d, causal):
     err = np.abs(out.cpu().double().numpy() - ref)
     # Every visible key holds the same V row: the output is that row, rounded to bf16.
     assert err.max() < 1e-2, err.max()
+
+
+@pytest.mark.parametrize("b,s,h,hk,d,causal", [(2, 197, 12, 12, 64, False), (1, 300, 8, 2, 128, True)])
+def test_head_view_inputs_give_a_projection_layout_output(native, dev, b, s, h, hk, d, causal):
+    """q, k, v as head views of [B, S, C] projections (a fused qkv for MHA, separate q and
+    kv projections for GQA) are read in place, and the output comes back as a [B, H, S, D]
+    view of a dense [B, S, H D] tensor (the reference's pitched route,
+    aten_attention.cpp:605-628): transposing it back to the projection layout is free.
+    With gradients required the output stays dense [B, H, S, D]."""
+    g = C.gen(800 + s)
+    if h == hk:
+        qkv = C.randn(g, b, s, 3 * h * d)
+        q, k, v = (qkv[..., i * h * d:(i + 1) * h * d].view(b, s, h, d).transpose(1, 2) for i in range(3))
+        dev_views = lambda: (lambda x: [x[..., i * h * d:(i + 1) * h * d].view(b, s, h, d).transpose(1, 2)
+                                        for i in range(3)])(qkv.to(dev))
+    else:
+        qp, kvp = C.randn(g, b, s, h * d), C.randn(g, b, s, 2 * hk * d)
+        q = qp.view(b, s, h, d).transpose(1, 2)
+        k, v = (kvp[..., i * hk * d:(i + 1) * hk * d].view(b, s, hk, d).transpose(1, 2) for i in range(2))
+        def dev_views():
+            qx, kvx = qp.to(dev), kvp.to(dev)
+            return [qx.view(b, s, h, d).transpose(1, 2)] + [
+                kvx[..., i * hk * d:(i + 1) * hk * d].view(b, s, hk, d).transpose(1, 2) for i in range(2)]
+    qd, kd, vd = dev_views()
+    assert qd.stride(1) == d and kd.stride(1) == d  # head views, not contiguous copies
+    native.reset_counters()
+    out = F.scaled_dot_product_attention(qd, kd, vd, is_causal=causal, enable_gqa=h != hk)
+    torch.cuda.synchronize()
+    _ran(native)
+    assert out.shape == (b, h, s, d)
+    assert out.stride() == (s * h * d, d, h * d, 1), out.stride()
+    assert out.transpose(1, 2).is_contiguous()
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), None, causal)
+    _check(out.cpu(), C.torch_cpu_sdpa(q.contiguous(), k.contiguous(), v.contiguous(), None, causal), ref,
+           f"head views {b}x{s}x{h}/{hk}x{d}")
+    qg = qd.detach().clone().requires_grad_(True)
+    out_g = F.scaled_dot_product_attention(qg, kd, vd, is_causal=causal, enable_gqa=h != hk)
+    assert out_g.is_contiguous()
+    assert torch.equal(out_g.detach().cpu(), out.cpu())
