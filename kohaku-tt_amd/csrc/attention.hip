@@ -65,6 +65,9 @@ struct AttnParams {
     const int32_t* cu_q;
     const int32_t* cu_k;
     int mask_dtype, mask_mode;
+    // Strided mask whose rows are read four keys per load: key stride 1, other strides and
+    // the base aligned to four elements (varlen units also need their first key aligned).
+    int mask_vec4;
     int batch, hq, hkv, group, seq_q, seq_k;
     int causal;
     float scale_log2;
@@ -203,6 +206,21 @@ __device__ __forceinline__ bool row_any4(bool pred, int l16) {
     return (m & 0x0001000100010001ull) != 0;
 }
 
+// Four consecutive mask values (one load of 4, 8 or 16 bytes).
+template <typename MRaw>
+struct Mask4 {
+    typedef typename std::conditional<sizeof(MRaw) == 1, uint32_t,
+            typename std::conditional<sizeof(MRaw) == 2, u32x2, u32x4>::type>::type V;
+    struct E {
+        MRaw e[4];
+    };
+    static __device__ __forceinline__ void load(const MRaw* at, MRaw (&out)[4]) {
+        const E x = __builtin_bit_cast(E, *reinterpret_cast<const V*>(at));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i] = x.e[i];
+    }
+};
+
 // Mask value of key `key` of the mask row at `mrow` (zero when the key is out of range),
 // read from a clamped, always-valid index: every lane loads, and a group of such loads
 // shares one round trip (a per-lane branch around each load can make each wait in turn).
@@ -289,10 +307,12 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     int64_t mrow[NQB];
     int64_t m_key = 0, m_end = 0;
     const void* mptr = p.mask;
+    bool mvec = false;  // uniform: full tiles read their mask values four keys per load
     if constexpr (MASKED) {
         // Packed masks are bounded by their element count; strided ones by their shape.
         m_end = p.mask_mode == KMI_MASK_PACKED ? p.mask_numel : INT64_MAX;
         m_key = p.mask_mode == KMI_MASK_PACKED ? 1 : p.ms[3];
+        mvec = p.mask_vec4 && (k0 & 3) == 0;
     }
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
@@ -387,15 +407,23 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         for (int i = 0; i < KIT; ++i) vreg[i] = buffer_load16(rs, v_lane + i * RPP * step);
         if constexpr (MASKED) {
             const MRaw* mp = static_cast<const MRaw*>(mptr);
+            if (mvec && key0 + TW <= lk) {
+                // Whole tile in range: four keys per load.
 #pragma unroll
-            for (int b = 0; b < NQB; ++b) {
+                for (int b = 0; b < NQB; ++b)
 #pragma unroll
-                for (int kb = 0; kb < KB; ++kb) {
+                    for (int kb = 0; kb < KB; ++kb) Mask4<MRaw>::load(mp + mrow[b] + key0 + 16 * kb + 4 * g4, mpre[b][kb]);
+            } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int kk = key0 + 16 * kb + 4 * g4 + i;
-                        const int64_t mi = mrow[b] + kk * m_key;
-                        mpre[b][kb][i] = (kk < lk && mi < m_end) ? mp[mi] : MRaw{};
+                for (int b = 0; b < NQB; ++b) {
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int kk = key0 + 16 * kb + 4 * g4 + i;
+                            const int64_t mi = mrow[b] + kk * m_key;
+                            mpre[b][kb][i] = (kk < lk && mi < m_end) ? mp[mi] : MRaw{};
+                        }
                     }
                 }
             }
@@ -1023,6 +1051,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     }
     int64_t mrow = 0, m_key = 0, m_end = 0;
     bool shared_row = false;
+    const bool mvec = MASKED && p.mask_vec4 && (k0 & 3) == 0;  // see attn_block
     if constexpr (MASKED) {
         const bool packed = p.mask_mode == KMI_MASK_PACKED;
         m_end = packed ? p.mask_numel : INT64_MAX;
@@ -1118,13 +1147,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
         for (int i2 = 0; i2 < KIT; ++i2) vreg[i2] = buffer_load16(rv, v_lane + i2 * RPP * vst);
         if constexpr (MASKED) {
             const MRaw* mp = static_cast<const MRaw*>(p.mask);
+            if (mvec && key0 + WN <= lk) {
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
+                for (int kb = 0; kb < KB; ++kb) Mask4<MRaw>::load(mp + mrow + key0 + 16 * kb + 4 * g4, mpre[kb]);
+            } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int kk = key0 + 16 * kb + 4 * g4 + j;
-                    const int64_t mi = mrow + kk * m_key;
-                    mpre[kb][j] = (kk < lk && mi < m_end) ? mp[mi] : MRaw{};
+                for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int kk = key0 + 16 * kb + 4 * g4 + j;
+                        const int64_t mi = mrow + kk * m_key;
+                        mpre[kb][j] = (kk < lk && mi < m_end) ? mp[mi] : MRaw{};
+                    }
                 }
             }
         }
@@ -1721,6 +1755,12 @@ extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t work
     p.mask_dtype = a->mask_dtype;
     for (int i = 0; i < 4; ++i) p.ms[i] = a->mask_stride[i];
     p.mask_numel = a->mask_numel;
+    {
+        const size_t esz = a->mask_dtype == KMI_BOOL ? 1 : (a->mask_dtype == KMI_F32 ? 4 : 2);
+        p.mask_vec4 = a->mask_mode == KMI_MASK_STRIDED && a->mask_stride[3] == 1 && a->mask_stride[0] % 4 == 0 &&
+                      a->mask_stride[1] % 4 == 0 && a->mask_stride[2] % 4 == 0 &&
+                      reinterpret_cast<uintptr_t>(a->mask) % (4 * esz) == 0;
+    }
     p.cu_q = a->cu_seqlens_q;
     p.cu_k = a->cu_seqlens_k;
     p.batch = static_cast<int>(a->batch);

@@ -97,10 +97,14 @@ def test_fp32_inputs_cast_like_reference(native, dev):
     _check(out, cpu, ref, "fp32 cast to bf16")
 
 
+@pytest.mark.parametrize("s", [96, 100, 99])
 @pytest.mark.parametrize("mask_kind", ["bool_key", "bool_full", "add_bf16", "add_f32_bcast_heads"])
-def test_masks(native, dev, mask_kind):
+def test_masks(native, dev, mask_kind, s):
+    """Mask kinds and dtypes.  S = 96 and 100 read whole tiles' mask values four keys per
+    load (100 ends in a partial tile, read key by key); S = 99 gives strides that are not
+    multiples of four, read key by key throughout."""
     g = C.gen(11)
-    b, h, s, d = 2, 4, 96, 64
+    b, h, d = 2, 4, 64
     q = C.randn(g, b, h, s, d)
     k = C.randn(g, b, 2, s, d)
     v = C.randn(g, b, 2, s, d)
@@ -116,7 +120,7 @@ def test_masks(native, dev, mask_kind):
         mask = torch.randn(b, 1, s, s, generator=g).masked_fill(torch.rand(b, 1, s, s, generator=g) < 0.2, float("-inf"))
         mask[..., 0] = 0.0
     out, cpu, ref = _dense_case(native, dev, q, k, v, mask=mask)
-    _check(out, cpu, ref, f"mask {mask_kind}")
+    _check(out, cpu, ref, f"mask {mask_kind} s={s}")
 
 
 def test_fully_masked_row_is_softmax_of_raw_scores(native, dev):
@@ -440,3 +444,22 @@ def test_head_view_inputs_give_a_projection_layout_output(native, dev, b, s, h, 
     out_g = F.scaled_dot_product_attention(qg, kd, vd, is_causal=causal, enable_gqa=h != hk)
     assert out_g.is_contiguous()
     assert torch.equal(out_g.detach().cpu(), out.cpu())
+
+
+def test_mask_with_unaligned_base_reads_key_by_key(native, dev):
+    """A mask view starting one element into its storage (base not aligned to four
+    elements) takes the key-by-key loads; results match the oracle."""
+    g = C.gen(13)
+    b, h, s, d = 2, 4, 128, 64
+    q, k, v = C.randn(g, b, h, s, d), C.randn(g, b, h, s, d), C.randn(g, b, h, s, d)
+    big = torch.randn(b * h * s * s + 1, generator=g)
+    mask = big[1:].view(b, h, s, s).masked_fill(torch.rand(b, h, s, s, generator=g) < 0.2, float("-inf"))
+    mask[..., 0] = 0.0
+    native.reset_counters()
+    md = torch.randn(b * h * s * s + 1, device=dev)[1:].view(b, h, s, s)
+    md.copy_(mask.to(dev))
+    assert md.storage_offset() == 1
+    out = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev), attn_mask=md).cpu()
+    _ran(native)
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), C.f64(mask))
+    _check(out, C.torch_cpu_sdpa(q, k, v, mask), ref, "unaligned mask base")
