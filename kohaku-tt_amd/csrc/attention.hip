@@ -65,8 +65,8 @@ struct AttnParams {
     const int32_t* cu_q;
     const int32_t* cu_k;
     int mask_dtype, mask_mode;
-    // Strided mask whose rows are read four keys per load: key stride 1, other strides and
-    // the base aligned to four elements (varlen units also need their first key aligned).
+    // Mask rows with unit key stride (every packed mask; strided masks with key stride 1):
+    // whole tiles read their mask values four keys per load (element-aligned vector loads).
     int mask_vec4;
     int batch, hq, hkv, group, seq_q, seq_k;
     int causal;
@@ -206,16 +206,16 @@ __device__ __forceinline__ bool row_any4(bool pred, int l16) {
     return (m & 0x0001000100010001ull) != 0;
 }
 
-// Four consecutive mask values (one load of 4, 8 or 16 bytes).
+// Four consecutive mask values: one 4-, 8- or 16-byte load at element alignment (gfx950
+// global loads take unaligned addresses; the copy tells the compiler the alignment).
 template <typename MRaw>
 struct Mask4 {
-    typedef typename std::conditional<sizeof(MRaw) == 1, uint32_t,
-            typename std::conditional<sizeof(MRaw) == 2, u32x2, u32x4>::type>::type V;
     struct E {
         MRaw e[4];
     };
     static __device__ __forceinline__ void load(const MRaw* at, MRaw (&out)[4]) {
-        const E x = __builtin_bit_cast(E, *reinterpret_cast<const V*>(at));
+        E x;
+        __builtin_memcpy(&x, at, sizeof(E));
 #pragma unroll
         for (int i = 0; i < 4; ++i) out[i] = x.e[i];
     }
@@ -308,11 +308,22 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     int64_t m_key = 0, m_end = 0;
     const void* mptr = p.mask;
     bool mvec = false;  // uniform: full tiles read their mask values four keys per load
+    int64_t m_seq_packed = 0;  // packed masks: the first value of this sequence's block
     if constexpr (MASKED) {
         // Packed masks are bounded by their element count; strided ones by their shape.
         m_end = p.mask_mode == KMI_MASK_PACKED ? p.mask_numel : INT64_MAX;
         m_key = p.mask_mode == KMI_MASK_PACKED ? 1 : p.ms[3];
-        mvec = p.mask_vec4 && (k0 & 3) == 0;
+        if (p.mask_mode == KMI_MASK_PACKED) {
+            for (int s = 0; s < seq; ++s) {
+                const int a0 = min(max(p.cu_q[s], 0), p.total_q);
+                const int a1 = min(max(p.cu_q[s + 1], a0), p.total_q);
+                const int b0 = min(max(p.cu_k[s], 0), p.total_k);
+                const int b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
+                m_seq_packed += static_cast<int64_t>(a1 - a0) * (b1 - b0);
+            }
+        }
+        // A packed block must lie within the mask for the unchecked vector loads.
+        mvec = p.mask_vec4 && (p.mask_mode != KMI_MASK_PACKED || m_seq_packed + static_cast<int64_t>(lq) * lk <= m_end);
     }
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
@@ -328,15 +339,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         for (int c = 0; c < DC; ++c) qf[b][c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
         if constexpr (MASKED) {
             if (p.mask_mode == KMI_MASK_PACKED) {
-                int64_t m_seq = 0;
-                for (int s = 0; s < seq; ++s) {
-                    const int a0 = min(max(p.cu_q[s], 0), p.total_q);
-                    const int a1 = min(max(p.cu_q[s + 1], a0), p.total_q);
-                    const int b0 = min(max(p.cu_k[s], 0), p.total_k);
-                    const int b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
-                    m_seq += static_cast<int64_t>(a1 - a0) * (b1 - b0);
-                }
-                mrow[b] = m_seq + static_cast<int64_t>(pos) * lk;
+                mrow[b] = m_seq_packed + static_cast<int64_t>(pos) * lk;
             } else {
                 const int64_t m_seq = p.cu_q ? (static_cast<int64_t>(q0) * p.ms[2] + static_cast<int64_t>(k0) * p.ms[3])
                                              : seq * p.ms[0];
@@ -1051,7 +1054,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     }
     int64_t mrow = 0, m_key = 0, m_end = 0;
     bool shared_row = false;
-    const bool mvec = MASKED && p.mask_vec4 && (k0 & 3) == 0;  // see attn_block
+    bool mvec = false;  // see attn_block
     if constexpr (MASKED) {
         const bool packed = p.mask_mode == KMI_MASK_PACKED;
         m_end = packed ? p.mask_numel : INT64_MAX;
@@ -1066,10 +1069,12 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
                 m_seq += static_cast<int64_t>(a1 - a0) * (b1 - b0);
             }
             mrow = m_seq + static_cast<int64_t>(pos) * lk;
+            mvec = p.mask_vec4 && m_seq + static_cast<int64_t>(lq) * lk <= m_end;
         } else {
             const int64_t m_seq = p.cu_q ? (static_cast<int64_t>(q0) * p.ms[2] + static_cast<int64_t>(k0) * p.ms[3])
                                          : seq * p.ms[0];
             mrow = m_seq + head * p.ms[1] + static_cast<int64_t>(pos) * p.ms[2];
+            mvec = p.mask_vec4;
         }
         // Every row of the wavefront reads the same mask row.
         shared_row = (lq == 1 || (!packed && p.ms[2] == 0)) && (G == 1 || packed || p.ms[1] == 0);
@@ -1756,10 +1761,7 @@ extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t work
     for (int i = 0; i < 4; ++i) p.ms[i] = a->mask_stride[i];
     p.mask_numel = a->mask_numel;
     {
-        const size_t esz = a->mask_dtype == KMI_BOOL ? 1 : (a->mask_dtype == KMI_F32 ? 4 : 2);
-        p.mask_vec4 = a->mask_mode == KMI_MASK_STRIDED && a->mask_stride[3] == 1 && a->mask_stride[0] % 4 == 0 &&
-                      a->mask_stride[1] % 4 == 0 && a->mask_stride[2] % 4 == 0 &&
-                      reinterpret_cast<uintptr_t>(a->mask) % (4 * esz) == 0;
+        p.mask_vec4 = a->mask_mode == KMI_MASK_PACKED || (a->mask_mode == KMI_MASK_STRIDED && a->mask_stride[3] == 1);
     }
     p.cu_q = a->cu_seqlens_q;
     p.cu_k = a->cu_seqlens_k;
