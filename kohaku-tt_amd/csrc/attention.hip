@@ -961,8 +961,13 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     const int split = lin % p.splits;
     lin /= p.splits;
     const int units = p.batch * p.hkv;
-    const int bh = lin % units;
     const int xi = lin / units;
+    // Varlen: the units of a query tile row are rotated by 9 per row.  Workgroups are dealt
+    // to XCDs and then shader engines in fixed rotation, so without it the units that have
+    // work at a given row (the long sequences of the batch) land on the same engines row
+    // after row, fill them, and stall the in-order dispatch while the rest of the chip
+    // idles.  Equal-length batches keep each XCD on few units (their K/V stay in its L2).
+    const int bh = (lin - xi * units + (p.cu_q ? xi * 9 : 0)) % units;
     if (!p.causal) {
         attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, xi);
         return;
@@ -1013,7 +1018,10 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     const int bh = blockIdx.x / wg_per_unit;
     const int split = blockIdx.x - bh * wg_per_unit;
     const int nslots = wg_per_unit * NWAVES;
-    const int slot = split * NWAVES + wave;
+    // Wavefront-major slots: workgroup `split` takes tiles split, split + wg_per_unit, ...
+    // across the whole key range, so every workgroup meets the live keys of a padded row
+    // (no workgroup of only masked tiles) and the work spreads evenly.
+    const int slot = wave * wg_per_unit + split;
     const int seq = bh / p.hkv;
     const int kvh = bh - seq * p.hkv;
     const int G = p.group;
