@@ -449,11 +449,9 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // (every element of lacc[b] holds lane l16's row sum), the reference point m (base-2
     // logit units), m + 8 (the lazy-rescale threshold) and -m for the exponent.
     f32x4 o[DB][NQB];
-    // Row sums as MFMA columns where the 64-row tiles leave registers to spare; otherwise
-    // per-lane fp32 partial sums reduced across the row's four lanes at the end.
-    constexpr bool LMFMA = NQB == 4;
-    f32x4 lacc[LMFMA ? NQB : 1];
-    float lsum[LMFMA ? 1 : NQB];
+    // Row sums as MFMA columns (P times a column of ones: one MFMA per 32 keys and row
+    // block, where fp32 adds would take eight VALU instructions).
+    f32x4 lacc[NQB];
     float m_run[NQB], m_thr[NQB], neg_m[NQB];
     bool raw[NQB];
 #pragma unroll
@@ -462,11 +460,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         m_run[b] = -INFINITY;
         m_thr[b] = -INFINITY;
         neg_m[b] = 0.f;
-        if constexpr (LMFMA) {
-            lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-        } else {
-            lsum[b] = 0.f;
-        }
+        lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int d = 0; d < DB; ++d) o[d][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -615,10 +609,13 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         // it pays for the row reduction, the move and the O / l rescale.
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            float lmax = -INFINITY;
+            // A chain of three-way maxima (v_max3): 4 instructions per 8 scores.
+            float lmax = fmaxf(x[b][0][0], x[b][0][1]);
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-                lmax = fmaxf(lmax, fmaxf(fmaxf(x[b][kb][0], x[b][kb][1]), fmaxf(x[b][kb][2], x[b][kb][3])));
+            for (int j = 2; j < 4 * KB; j += 2) {
+                const float a0 = x[b][j / 4][j % 4], a1 = x[b][(j + 1) / 4][(j + 1) % 4];
+                lmax = fmaxf(fmaxf(lmax, a0), a1);
+            }
             if (__builtin_amdgcn_ballot_w64(lmax * xs > m_thr[b])) {
                 const float mt = row_max4(lmax) * xs;
                 const bool move = mt > m_thr[b];
@@ -630,11 +627,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                     neg_m[b] = -mt;
                 }
                 if (__builtin_amdgcn_ballot_w64(move)) {
-                    if constexpr (LMFMA) {
-                        lacc[b] *= alpha;
-                    } else {
-                        lsum[b] *= alpha;
-                    }
+                    lacc[b] *= alpha;
 #pragma unroll
                     for (int d = 0; d < DB; ++d) o[d][b] *= alpha;
                 }
@@ -656,7 +649,6 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         }
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            float ls = 0.f;
 #pragma unroll
             for (int h = 0; h < KH; ++h) {
                 // The 32 keys of chunk h: S accumulator blocks 2 h and 2 h + 1.
@@ -665,15 +657,13 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                 for (int i = 0; i < 4; ++i) {
                     const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * h][i], xs, neg_m[b]));
                     const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * h + 1][i], xs, neg_m[b]));
-                    if constexpr (!LMFMA) ls += e0 + e1;
                     pf[i] = static_cast<T>(e0);
                     pf[4 + i] = static_cast<T>(e1);
                 }
-                if constexpr (LMFMA) lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
+                lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
 #pragma unroll
                 for (int d = 0; d < DB; ++d) o[d][b] = Mfma<T>::run(vf[h][d], pf, o[d][b]);
             }
-            if constexpr (!LMFMA) lsum[b] += ls;
         }
         __builtin_amdgcn_iglp_opt(2);
     };
@@ -771,7 +761,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
             const int r = r_begin + 16 * b + l16;
-            const float l = LMFMA ? lacc[b][0] : row_sum4(lsum[b]);
+            const float l = lacc[b][0];
             if (r >= r_end) continue;
             const int pos = r / G;
             const int head = kvh * G + (r - pos * G);
@@ -800,11 +790,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     float l_run[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
-        if constexpr (LMFMA) {
-            l_run[b] = lacc[b][0];
-        } else {
-            l_run[b] = row_sum4(lsum[b]);
-        }
+        l_run[b] = lacc[b][0];
     }
     auto combine = [&](const f32x4 (&sw)[NWAVES], float (&wt)[NWAVES], float& m, float& lt, bool& any_masked) {
         any_masked = false;
