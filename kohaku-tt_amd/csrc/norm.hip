@@ -25,19 +25,21 @@ struct alignas(E * sizeof(T)) Pack {
 };
 
 template <typename T, int E>
-__device__ __forceinline__ void load_pack(const T* p, float* out) {
-    const Pack<T, E> v = *reinterpret_cast<const Pack<T, E>*>(p);
-#pragma unroll
-    for (int j = 0; j < E; ++j) out[j] = to_f32(v.e[j]);
-}
-
-template <typename T, int E>
 __device__ __forceinline__ void store_pack(T* p, const float* in) {
     Pack<T, E> v;
 #pragma unroll
     for (int j = 0; j < E; ++j) v.e[j] = from_f32<T>(in[j]);
     *reinterpret_cast<Pack<T, E>*>(p) = v;
 }
+
+// Weight or bias values for one vector of E elements of x, loaded raw (so that every load
+// of a row is issued before the first one is waited for) and widened when used.
+template <typename W, int E>
+struct Param {
+    Pack<W, E> v;
+    __device__ __forceinline__ void load(const W* p, int vi) { v = *reinterpret_cast<const Pack<W, E>*>(p + vi * E); }
+    __device__ __forceinline__ float at(int j) const { return to_f32(v.e[j]); }
+};
 
 // The E = 16 / sizeof(T) elements of one 16-byte vector as fp32 (bf16: the high half of
 // an fp32; f16: converted; f32: as is).
@@ -61,26 +63,42 @@ __device__ __forceinline__ void unpack(const u32x4& raw, float* out) {
     }
 }
 
-// One wavefront per row, 4 rows per 256-thread block.  T: x / y; W: weight and bias.  The
+// One wavefront per row, blockDim / 64 rows per block.  T: x / y; W: weight and bias.  The
 // row stays in registers as loaded (packed) and is widened to fp32 in each pass, which
-// keeps the register count, and so the wavefronts in flight per SIMD, up.
-template <typename T, typename W, int VPL, bool LAYER>
-__global__ __launch_bounds__(256) void norm_rows_wave(
-    const T* __restrict__ x, const W* __restrict__ weight, const W* __restrict__ bias,
+// keeps the register count, and so the wavefronts in flight per SIMD, up.  Every load of
+// the row (x, weight, bias) is issued at once from clamped in-range indices: per-lane
+// branches around them made each wait for the previous one (five round trips for a
+// LayerNorm row instead of one).
+template <typename T, typename W, int VPL, bool LAYER, int PRM>
+__global__ __launch_bounds__(1024) void norm_rows_wave(
+    const T* x, const W* weight, const W* bias,
     T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
     int64_t rows, int width, float eps) {
     constexpr int E = 16 / sizeof(T);
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int nvec = width / E;
     const T* xr = x + row * width;
+    // PRM bit 0: a weight, bit 1: a bias (compile-time, so that the loads form one
+    // straight-line group).
+    constexpr bool HW = PRM & 1, HB = PRM & 2;
     u32x4 raw[VPL];
+    Param<W, E> g[VPL], bb[VPL];
+    // Weight and bias first, then the row: the row's values are used first, and the
+    // compiler waits for them where they are used (after every load is issued).
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-        const int vi = lane + kWave * i;
-        raw[i] = vi < nvec ? *reinterpret_cast<const u32x4*>(xr + vi * E) : u32x4{0u, 0u, 0u, 0u};
+        const int vc = min(lane + kWave * i, nvec - 1);
+        if constexpr (HW) g[i].load(weight, vc);
+        if constexpr (HB) bb[i].load(bias, vc);
     }
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) raw[i] = *reinterpret_cast<const u32x4*>(xr + min(lane + kWave * i, nvec - 1) * E);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+        if (lane + kWave * i >= nvec) raw[i] = u32x4{0u, 0u, 0u, 0u};
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -118,22 +136,14 @@ __global__ __launch_bounds__(256) void norm_rows_wave(
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + kWave * i;
         if (vi < nvec) {
-            float v[E], o[E], g[E], b[E];
+            float v[E], o[E];
             unpack<T>(raw[i], v);
-            if (weight) {
-                load_pack<W, E>(weight + vi * E, g);
-            } else {
 #pragma unroll
-                for (int j = 0; j < E; ++j) g[j] = 1.f;
+            for (int j = 0; j < E; ++j) {
+                o[j] = (v[j] - mean) * rstd;
+                if constexpr (HW) o[j] *= g[i].at(j);
+                if constexpr (HB) o[j] += bb[i].at(j);
             }
-            if (bias) {
-                load_pack<W, E>(bias + vi * E, b);
-            } else {
-#pragma unroll
-                for (int j = 0; j < E; ++j) b[j] = 0.f;
-            }
-#pragma unroll
-            for (int j = 0; j < E; ++j) o[j] = (v[j] - mean) * rstd * g[j] + b[j];
             store_pack<T, E>(yr + vi * E, o);
         }
     }
@@ -145,9 +155,9 @@ __global__ __launch_bounds__(256) void norm_rows_wave(
 
 // Wide rows: one 256-thread block per row, each thread holding VPT vectors; the four
 // wavefronts' partial sums meet in LDS in a fixed order.
-template <typename T, typename W, int VPT, bool LAYER>
+template <typename T, typename W, int VPT, bool LAYER, int PRM>
 __global__ __launch_bounds__(256) void norm_rows_block(
-    const T* __restrict__ x, const W* __restrict__ weight, const W* __restrict__ bias,
+    const T* x, const W* weight, const W* bias,
     T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
     int width, float eps) {
     constexpr int E = 16 / sizeof(T);
@@ -158,12 +168,23 @@ __global__ __launch_bounds__(256) void norm_rows_block(
     const int64_t row = blockIdx.x;
     const int nvec = width / E;
     const T* xr = x + row * width;
+    constexpr bool HW = PRM & 1, HB = PRM & 2;  // weight, bias (see norm_rows_wave)
     u32x4 raw[VPT];
+    Param<W, E> g[VPT], bb[VPT];
+    // Weight and bias first, then the row: the row's values are used first, and the
+    // compiler waits for them where they are used (after every load is issued).
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-        const int vi = tid + 256 * i;
-        raw[i] = vi < nvec ? *reinterpret_cast<const u32x4*>(xr + vi * E) : u32x4{0u, 0u, 0u, 0u};
+        const int vc = min(tid + 256 * i, nvec - 1);
+        if constexpr (HW) g[i].load(weight, vc);
+        if constexpr (HB) bb[i].load(bias, vc);
     }
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) raw[i] = *reinterpret_cast<const u32x4*>(xr + min(tid + 256 * i, nvec - 1) * E);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+        if (tid + 256 * i >= nvec) raw[i] = u32x4{0u, 0u, 0u, 0u};
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -206,22 +227,14 @@ __global__ __launch_bounds__(256) void norm_rows_block(
     for (int i = 0; i < VPT; ++i) {
         const int vi = tid + 256 * i;
         if (vi < nvec) {
-            float v[E], o[E], g[E], b[E];
+            float v[E], o[E];
             unpack<T>(raw[i], v);
-            if (weight) {
-                load_pack<W, E>(weight + vi * E, g);
-            } else {
 #pragma unroll
-                for (int j = 0; j < E; ++j) g[j] = 1.f;
+            for (int j = 0; j < E; ++j) {
+                o[j] = (v[j] - mean) * rstd;
+                if constexpr (HW) o[j] *= g[i].at(j);
+                if constexpr (HB) o[j] += bb[i].at(j);
             }
-            if (bias) {
-                load_pack<W, E>(bias + vi * E, b);
-            } else {
-#pragma unroll
-                for (int j = 0; j < E; ++j) b[j] = 0.f;
-            }
-#pragma unroll
-            for (int j = 0; j < E; ++j) o[j] = (v[j] - mean) * rstd * g[j] + b[j];
             store_pack<T, E>(yr + vi * E, o);
         }
     }
@@ -302,15 +315,27 @@ template <typename T, typename W, bool LAYER>
 hipError_t launch_wave(const void* x, const void* w, const void* b, void* y, float* mean,
                        float* rstd, int64_t rows, int width, float eps, int vpl,
                        hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(ceil_div(rows, 4))), block(256);
+    // 16 rows per block once there are enough rows to fill the chip that way (fewer
+    // workgroups to dispatch), 4 rows per block otherwise.
+    const int rpb = rows >= 16 * 512 ? 16 : 4;
+    const dim3 grid(static_cast<unsigned>(ceil_div(rows, rpb))), block(kWave * rpb);
     auto* xp = static_cast<const T*>(x);
     auto* wp = static_cast<const W*>(w);
     auto* bp = static_cast<const W*>(b);
     auto* yp = static_cast<T*>(y);
-#define KMI_NORM_CASE(N)                                                                  \
-    case N:                                                                               \
-        hipLaunchKernelGGL((norm_rows_wave<T, W, N, LAYER>), grid, block, 0, stream, xp,  \
-                           wp, bp, yp, mean, rstd, rows, width, eps);                     \
+    const int prm = (w ? 1 : 0) | (b ? 2 : 0);
+#define KMI_NORM_CASE(N)                                                                           \
+    case N:                                                                                        \
+        switch (prm) {                                                                             \
+            case 0: hipLaunchKernelGGL((norm_rows_wave<T, W, N, LAYER, 0>), grid, block, 0, stream, \
+                                       xp, wp, bp, yp, mean, rstd, rows, width, eps); break;       \
+            case 1: hipLaunchKernelGGL((norm_rows_wave<T, W, N, LAYER, 1>), grid, block, 0, stream, \
+                                       xp, wp, bp, yp, mean, rstd, rows, width, eps); break;       \
+            case 2: hipLaunchKernelGGL((norm_rows_wave<T, W, N, LAYER, 2>), grid, block, 0, stream, \
+                                       xp, wp, bp, yp, mean, rstd, rows, width, eps); break;       \
+            default: hipLaunchKernelGGL((norm_rows_wave<T, W, N, LAYER, 3>), grid, block, 0, stream, \
+                                        xp, wp, bp, yp, mean, rstd, rows, width, eps);             \
+        }                                                                                          \
         break;
     switch (vpl) {
         KMI_NORM_CASE(1)
@@ -331,10 +356,19 @@ hipError_t launch_block(const void* x, const void* w, const void* b, void* y, fl
     auto* wp = static_cast<const W*>(w);
     auto* bp = static_cast<const W*>(b);
     auto* yp = static_cast<T*>(y);
-#define KMI_NORM_CASE(N)                                                                   \
-    case N:                                                                                \
-        hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER>), grid, block, 0, stream, xp,  \
-                           wp, bp, yp, mean, rstd, width, eps);                            \
+    const int prm = (w ? 1 : 0) | (b ? 2 : 0);
+#define KMI_NORM_CASE(N)                                                                            \
+    case N:                                                                                         \
+        switch (prm) {                                                                              \
+            case 0: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 0>), grid, block, 0, stream, \
+                                       xp, wp, bp, yp, mean, rstd, width, eps); break;              \
+            case 1: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 1>), grid, block, 0, stream, \
+                                       xp, wp, bp, yp, mean, rstd, width, eps); break;              \
+            case 2: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 2>), grid, block, 0, stream, \
+                                       xp, wp, bp, yp, mean, rstd, width, eps); break;              \
+            default: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 3>), grid, block, 0, stream, \
+                                        xp, wp, bp, yp, mean, rstd, width, eps);                    \
+        }                                                                                           \
         break;
     switch (vpt) {
         KMI_NORM_CASE(1)
