@@ -469,6 +469,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     for (int j = 0; j < 8; ++j) ones[j] = static_cast<T>(1.f);
     // A negative scale flips the sign of Q (exact) so that the exponent's multiplier is
     // positive and a larger score is a larger logit.
+    // Each wavefront's first tile is requested before anything else waits on memory (its
+    // loads share one round trip with the Q fragments and the mask-row scan below).
+    const int t_spec = t_begin + (RS ? 0 : wave);
+    if (t_spec < t_end) load_tile(t_spec);
     float c2 = p.scale_log2;
     if (c2 < 0.f) {
         c2 = -c2;
@@ -478,11 +482,6 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             for (int c = 0; c < DC; ++c)
                 qf[b][c] = __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, qf[b][c]) ^ 0x80008000u);
     }
-
-    // Each wavefront's first tile is requested before anything else waits on memory (its
-    // loads share one round trip with the Q fragments and the mask-row scan below).
-    const int t_spec = t_begin + (RS ? 0 : wave);
-    if (t_spec < t_end) load_tile(t_spec);
 
     // Key-mask tile skipping: with a mask that depends only on the key (a padding mask),
     // tiles whose every key is masked contribute exactly nothing once the row is known to
