@@ -1167,10 +1167,17 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     for (int d = 0; d < DB; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
     bool raw = MASKED;
-    const float c2 = p.scale_log2;
 
     int i = use_bits ? (live ? __builtin_ctz(live) : n_t) : 0;
     if (i < n_t) load_tile(i);
+    // A negative scale flips the sign of Q (exact) so that the exponent's multiplier is
+    // positive and the row maximum of the raw scores is the maximum logit.
+    float c2 = p.scale_log2;
+    if (c2 < 0.f) {
+        c2 = -c2;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) qf[c] = __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, qf[c]) ^ 0x80008000u);
+    }
     while (i < n_t) {
         // LDS keeps one wavefront's accesses in order (the previous tile's reads, these
         // writes, this tile's reads): only the compiler must keep it.

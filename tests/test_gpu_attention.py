@@ -463,3 +463,26 @@ def test_mask_with_unaligned_base_reads_key_by_key(native, dev):
     _ran(native)
     ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), C.f64(mask))
     _check(out, C.torch_cpu_sdpa(q, k, v, mask), ref, "unaligned mask base")
+
+
+@pytest.mark.parametrize(
+    "b,hq,hk,sq,sk,d,causal,masked",
+    [
+        (2, 4, 2, 90, 90, 64, True, False),  # prefill, 16/32-row tiles
+        (2, 8, 8, 70, 300, 128, False, True),  # prefill, masked
+        (4, 16, 2, 1, 700, 128, False, False),  # decode, split-KV
+        (4, 16, 2, 1, 700, 128, False, True),  # decode with a padding mask
+        (32, 12, 12, 197, 197, 64, False, False),  # row-split mode
+    ],
+)
+def test_negative_scale(native, dev, b, hq, hk, sq, sk, d, causal, masked):
+    """A negative softmax scale (legal in SDPA) flips which key has the largest logit:
+    every kernel takes it exactly (Q's sign is flipped) and matches the oracle."""
+    g = C.gen(900 + sk)
+    q, k, v = C.randn(g, b, hq, sq, d), C.randn(g, b, hk, sk, d), C.randn(g, b, hk, sk, d)
+    mask = None
+    if masked:
+        lengths = torch.randint(1, sk + 1, (b,), generator=g)
+        mask = (torch.arange(sk)[None, :] < lengths[:, None]).reshape(b, 1, 1, sk)
+    out, cpu, ref = _dense_case(native, dev, q, k, v, mask=mask, causal=causal, scale=-0.2)
+    _check(out, cpu, ref, f"negative scale {b}x{hq}/{hk}x{sq}x{sk}x{d}")
