@@ -486,3 +486,13 @@ def test_negative_scale(native, dev, b, hq, hk, sq, sk, d, causal, masked):
         mask = (torch.arange(sk)[None, :] < lengths[:, None]).reshape(b, 1, 1, sk)
     out, cpu, ref = _dense_case(native, dev, q, k, v, mask=mask, causal=causal, scale=-0.2)
     _check(out, cpu, ref, f"negative scale {b}x{hq}/{hk}x{sq}x{sk}x{d}")
+
+
+@pytest.mark.parametrize("b,hq,hk,sq,sk,d", [(1, 4, 4, 100, 1, 64), (2, 8, 2, 1, 1, 128), (3, 6, 3, 33, 2, 64)])
+def test_one_or_two_keys(native, dev, b, hq, hk, sq, sk, d):
+    """Key ranges of one or two keys (a single partial tile, every other row of it past
+    the end): each output row is the softmax-weighted V rows, matching the oracle."""
+    g = C.gen(950 + sq)
+    q, k, v = C.randn(g, b, hq, sq, d), C.randn(g, b, hk, sk, d), C.randn(g, b, hk, sk, d)
+    out, cpu, ref = _dense_case(native, dev, q, k, v)
+    _check(out, cpu, ref, f"few keys {b}x{hq}/{hk}x{sq}x{sk}x{d}")
