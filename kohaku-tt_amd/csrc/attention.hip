@@ -68,6 +68,9 @@ struct AttnParams {
     // Mask rows with unit key stride (every packed mask; strided masks with key stride 1):
     // whole tiles read their mask values four keys per load (element-aligned vector loads).
     int mask_vec4;
+    // Row split with the unit's whole key range staged once in the workgroup's LDS
+    // (rs_shared: the dynamic LDS holds every key tile, K then V).
+    int rs_shared;
     int batch, hq, hkv, group, seq_q, seq_k;
     int causal;
     float scale_log2;
@@ -283,7 +286,41 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     }
     const int vrows = lq * G;
     const int r_begin = RS ? (xt * NWAVES + wave) * BM : xt * BM;
-    if (r_begin >= vrows || lk <= 0) return;
+    if (lk <= 0) return;
+    if constexpr (RS) {
+        if (p.rs_shared) {
+            // Shared row split: the workgroup stages every key tile of the unit (K rows at
+            // pitch KP, then V rows at pitch VP) in one round of loads, then each wavefront
+            // runs its own rows over them with no memory traffic in the loop.  Rows past the
+            // last key repeat it (finite; their scores are masked).  Every wavefront takes
+            // part in the staging and the barrier, rows or not.
+            const int nt = (lk + S::TW - 1) / S::TW;
+            T* kls = reinterpret_cast<T*>(smem);
+            T* vls = kls + nt * S::TW * S::KP;
+            const T* kg = static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] + static_cast<int64_t>(k0) * p.ks[2];
+            const T* vg = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0) * p.vs[2];
+            constexpr int VPR_ = D / 8;
+            const int nvec = nt * S::TW * VPR_;
+            constexpr int MAXV = 4 * 32 * VPR_ / NTHREADS;  // up to four tiles (host bound)
+            u32x4 kv[MAXV], vv[MAXV];
+#pragma unroll
+            for (int j = 0; j < MAXV; ++j) {
+                const int v = min(tid + NTHREADS * j, nvec - 1);
+                const int row = min(v / VPR_, lk - 1), ch = v % VPR_;
+                kv[j] = *reinterpret_cast<const u32x4*>(kg + static_cast<int64_t>(row) * p.ks[2] + 8 * ch);
+                vv[j] = *reinterpret_cast<const u32x4*>(vg + static_cast<int64_t>(row) * p.vs[2] + 8 * ch);
+            }
+#pragma unroll
+            for (int j = 0; j < MAXV; ++j) {
+                const int v = min(tid + NTHREADS * j, nvec - 1);
+                const int row = v / VPR_, ch = v % VPR_;
+                *reinterpret_cast<u32x4*>(kls + row * S::KP + 8 * ch) = kv[j];
+                *reinterpret_cast<u32x4*>(vls + row * S::VP + 8 * ch) = vv[j];
+            }
+            __syncthreads();
+        }
+    }
+    if (r_begin >= vrows) return;
     constexpr int TS = RS ? 1 : NWAVES;  // tile stride of one wavefront
     const int r_end = min(vrows, r_begin + BM);
     const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys <= i + coff
@@ -472,7 +509,8 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // Each wavefront's first tile is requested before anything else waits on memory (its
     // loads share one round trip with the Q fragments and the mask-row scan below).
     const int t_spec = t_begin + (RS ? 0 : wave);
-    if (t_spec < t_end) load_tile(t_spec);
+    const bool rs_shared = RS && p.rs_shared;
+    if (t_spec < t_end && !rs_shared) load_tile(t_spec);
     float c2 = p.scale_log2;
     if (c2 < 0.f) {
         c2 = -c2;
@@ -678,8 +716,35 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     };
 
     int t = next_tile(t_spec);
-    if (t != t_spec && t < t_end) load_tile(t);
-    if constexpr (KD) {
+    if (t != t_spec && t < t_end && !rs_shared) load_tile(t);
+    if (rs_shared) {
+        // Every key tile is in LDS: S, softmax and PV per tile, nothing else.
+        T* const kls = reinterpret_cast<T*>(smem);
+        T* const vls = kls + ((lk + TW - 1) / TW) * TW * KP;
+        for (; t < t_end; ++t) {
+            kl = kls + t * TW * KP;
+            vl = vls + t * TW * VP;
+            v8 kf[KB][DC];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int c = 0; c < DC; ++c)
+                    kf[kb][c] = *reinterpret_cast<const v8*>(kl + (16 * kb + l16) * KP + 32 * c + 8 * g4);
+            }
+            f32x4 s[KB][NQB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int b = 0; b < NQB; ++b) {
+                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
+                }
+            }
+            const MCur mnone{};
+            consume(t, s, mnone);
+        }
+    } else if constexpr (KD) {
         // K fragments in registers.  32-row workgroups keep two sets: tile t's in one while
         // the tile after next loads into the other (a full iteration of cover).  64-row
         // workgroups have no registers to spare: the next tile's K loads into the set the
@@ -1486,6 +1551,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
 struct Plan {
     bool decode;  // attn_decode_kernel: per-wavefront key ranges, fp32 partials + merge
     bool rs;      // row split: short key ranges, one row block per wavefront
+    bool rs_shared;  // row split with the unit's key tiles (at most four) staged in LDS once
     int nqb, nx, splits, tiles_per_split;
     int64_t rows_total;
     size_t ws_bytes;
@@ -1606,6 +1672,7 @@ Plan make_plan(const kmi_attn_args* a) {
         const int64_t nx_rs = ceil_div(vrows, NWAVES * 16 * q);
         if (nx_rs * units >= 256) {
             pl.rs = true;
+            pl.rs_shared = nk <= 4;
             pl.nqb = q;
             pl.nx = static_cast<int>(nx_rs);
         }
@@ -1639,12 +1706,19 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     static int per_cu = 0;  // resident workgroups per CU
-    const size_t lds = Shape<D, NQB, TWIDTH>::template lds_bytes<T>();
+    typedef Shape<D, NQB, TWIDTH> S;
+    // Shared row split: every key tile of a unit (at most four) in LDS, K then V.
+    constexpr size_t rs_max = RS ? 4 * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T) : 0;
+    const size_t lds_tiles = S::template lds_bytes<T>();
+    const size_t lds = RS && p_in.rs_shared
+                           ? ceil_div(p_in.seq_k, TWIDTH) * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T)
+                           : lds_tiles;
     const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH>);
     std::call_once(once, [&] {
-        attr_err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        attr_err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(std::max(lds_tiles, rs_max)));
         if (attr_err == hipSuccess &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NTHREADS, lds) != hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NTHREADS, lds_tiles) != hipSuccess)
             per_cu = 0;
     });
     if (attr_err != hipSuccess) return attr_err;
@@ -1780,6 +1854,7 @@ extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t work
     p.tiles_per_split = pl.tiles_per_split;
     p.nx = pl.nx;
     p.rows_total = pl.rows_total;
+    p.rs_shared = pl.rs && pl.rs_shared ? 1 : 0;
     p.total_q = static_cast<int>(a->total_q);
     p.total_k = static_cast<int>(a->total_k);
     if (pl.splits > 1) {

@@ -328,11 +328,13 @@ def test_varlen_cross_lengths_bottom_right(native, dev):
         (16, 16, 4, 300, 200, 128),  # GQA, 7 key tiles: one row block per wavefront
         (8, 8, 8, 512, 100, 64),
         (32, 8, 2, 128, 256, 64),  # exactly 8 key tiles
+        (4, 16, 16, 1024, 77, 128),  # three tiles staged once in LDS, partial last tile
     ],
 )
 def test_short_key_ranges_output_and_lse(native, dev, b, hq, hk, sq, sk, d):
-    """Short unmasked key ranges run one row block per wavefront (no key split, no merge);
-    output and natural-log LSE match the oracle through the C ABI."""
+    """Short unmasked key ranges run one row block per wavefront (no key split, no merge;
+    up to four key tiles are staged once per workgroup in LDS); output and natural-log LSE
+    match the oracle through the C ABI."""
     from kohakutt_amd import capi
 
     g = C.gen(500 + sq)
