@@ -157,6 +157,9 @@ __device__ __forceinline__ u32x2 lds_read_tr(const T* p) {
 
 // Keys per wavefront tile.
 constexpr int WN = 32;
+// Row split stages a unit's whole key range in LDS up to this many tiles (eight measured
+// slower: fewer workgroups fit per CU).
+constexpr int kRsTiles = 4;
 
 template <int D, int NQB, int TWIDTH = WN>
 struct Shape {
@@ -301,7 +304,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             const T* vg = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0) * p.vs[2];
             constexpr int VPR_ = D / 8;
             const int nvec = nt * S::TW * VPR_;
-            constexpr int MAXV = 4 * 32 * VPR_ / NTHREADS;  // up to four tiles (host bound)
+            constexpr int MAXV = kRsTiles * 32 * VPR_ / NTHREADS;  // up to kRsTiles tiles (host bound)
             u32x4 kv[MAXV], vv[MAXV];
 #pragma unroll
             for (int j = 0; j < MAXV; ++j) {
@@ -1672,7 +1675,7 @@ Plan make_plan(const kmi_attn_args* a) {
         const int64_t nx_rs = ceil_div(vrows, NWAVES * 16 * q);
         if (nx_rs * units >= 256) {
             pl.rs = true;
-            pl.rs_shared = nk <= 4;
+            pl.rs_shared = nk <= kRsTiles;
             pl.nqb = q;
             pl.nx = static_cast<int>(nx_rs);
         }
@@ -1708,7 +1711,7 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
     static int per_cu = 0;  // resident workgroups per CU
     typedef Shape<D, NQB, TWIDTH> S;
     // Shared row split: every key tile of a unit (at most four) in LDS, K then V.
-    constexpr size_t rs_max = RS ? 4 * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T) : 0;
+    constexpr size_t rs_max = RS ? kRsTiles * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T) : 0;
     const size_t lds_tiles = S::template lds_bytes<T>();
     const size_t lds = RS && p_in.rs_shared
                            ? ceil_div(p_in.seq_k, TWIDTH) * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T)
