@@ -418,7 +418,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     MRaw mpre[MASKED ? NQB : 1][KB][4];
 
     typedef v8 KRegs[KD ? KB : 1][KD ? DC : 1];
-    KRegs kreg, kreg2;  // KD: two sets, each loaded two of this wavefront's tiles ahead
+    KRegs kreg;  // KD: the next tile's K, loaded as soon as the S MFMAs consumed this tile's
     u32x4 kst[KD ? 1 : KIT];
     u32x4 vreg[KIT];
     // The row shifts of a tile's passes are uniform; the compiler barrier on them keeps the
@@ -748,13 +748,9 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             consume(t, s, mnone);
         }
     } else if constexpr (KD) {
-        // K fragments in registers.  32-row workgroups keep two sets: tile t's in one while
-        // the tile after next loads into the other (a full iteration of cover).  64-row
-        // workgroups have no registers to spare: the next tile's K loads into the set the
-        // S MFMAs just consumed.  V is one tile ahead either way.
-        constexpr bool K2 = NQB == 2;
+        // K fragments in registers (64-row workgroups): the next tile's K loads into the set
+        // the S MFMAs just consumed; V is one tile ahead through LDS.
         int t1 = next_tile(t + TS);
-        if (K2 && t < t_end && t1 < t_end) load_k(t1, kreg2);
         auto step = [&](KRegs& kc) {
             // LDS keeps one wavefront's accesses in order (the previous tile's reads,
             // these writes, this tile's reads): only the compiler must keep it.
@@ -775,20 +771,12 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                 }
             }
             const int t_nn = t_next < t_end ? next_tile(t_next + TS) : t_end;
-            if constexpr (K2) {
-                if (t_nn < t_end) load_k(t_nn, kc);
-            } else {
-                if (t_next < t_end) load_k(t_next, kc);
-            }
+            if (t_next < t_end) load_k(t_next, kc);
             consume(t, s, mcur);
             t = t_next;
             t1 = t_nn;
         };
-        while (t < t_end) {
-            step(kreg);
-            if (!K2 || t >= t_end) continue;
-            step(kreg2);
-        }
+        while (t < t_end) step(kreg);
     } else {
         while (t < t_end) {
             // LDS keeps one wavefront's accesses in order (the previous tile's reads,
