@@ -153,6 +153,14 @@ def build_rows():
              pairs=int(lens.sum()) * 1)
     rows["c3_decode"].bytes = dec_bytes
     rows["c3_decode"].flops = C.attn_flops(d3, 16, int(lens.sum()))
+    def lengths_make(dev, n):
+        sets = _rotate(dev, [c3["q"], c3["k"], c3["v"], lens.to(torch.int32)], n)
+        return [(lambda s=s: torch.ops.ktt._sdpa_lengths(s[0], s[1], s[2], s[3], False, None, False)) for s in sets]
+
+    rows["c3_decode_lengths"] = Row(
+        "c3_decode_lengths", "extra: C3 decode through key lengths (ktt::_sdpa_lengths, no mask)", "hbm",
+        C.attn_flops(d3, 16, int(lens.sum())), dec_bytes - 8 * 4096 + 8 * 4,
+        (lengths_make, rows["c3_decode"].make[1]), "attn_decode_kernel")
     norm_row("c3_rms", "C3 rms_norm [8,1,2048]", c3["x"], c3["w"], None, 1e-6, "rms")
 
     c4 = C.config4()

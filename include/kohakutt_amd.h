@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KMI_ABI_VERSION 1
+#define KMI_ABI_VERSION 2
 
 /* Element types of operands. */
 enum kmi_dtype {
@@ -110,6 +110,13 @@ typedef struct kmi_attn_args {
      * 1: no split; n > 1: at most n key splits. */
     int32_t num_splits;
     int32_t reserved;
+    /* Dense calls only (ABI 2; NULL: every key).  Device int32 [batch]: sequence b's
+     * queries see keys [0, L_b), L_b = key_lengths[b] clamped to [1, seq_k]; no mask is
+     * built or read and key tiles past L_b are not loaded.  Query rows past L_b still see
+     * the first L_b keys.  Composes with causal (top-left) and with a mask.  Replaces the
+     * reference's bridge::sdpa_lengths behind ktt::_sdpa_lengths (aten_lengths.cpp:69-101,
+     * 175-197; docs/reference/kernels/flash.md, Key lengths). */
+    const int32_t* key_lengths;
 } kmi_attn_args;
 
 /* Bytes of workspace kmi_attn_fwd needs for `args` (0 when it does not split). */

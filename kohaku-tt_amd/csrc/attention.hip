@@ -64,6 +64,8 @@ struct AttnParams {
     int64_t mask_numel;
     const int32_t* cu_q;
     const int32_t* cu_k;
+    // Dense key lengths [batch] (or null): sequence b sees keys [0, clamp(klen[b], 1, seq_k)).
+    const int32_t* klen;
     int mask_dtype, mask_mode;
     // Mask rows with unit key stride (every packed mask; strided masks with key stride 1):
     // whole tiles read their mask values four keys per load (element-aligned vector loads).
@@ -287,6 +289,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         qb_off = kb_off = vb_off = ob_off = lb_off = 0;
         row_base = q0;
     }
+    if (p.klen) lk = min(max(p.klen[seq], 1), p.seq_k);
     const int vrows = lq * G;
     const int r_begin = RS ? (xt * NWAVES + wave) * BM : xt * BM;
     if (lk <= 0) return;
@@ -1082,6 +1085,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
         qb_off = kb_off = vb_off = 0;
         row_base = q0;
     }
+    if (p.klen) lk = min(max(p.klen[seq], 1), p.seq_k);
     // Uniform over the workgroup: an empty sequence leaves before any barrier.
     const int vrows = min(lq * G, 16);
     if (vrows <= 0) return;
@@ -1558,6 +1562,7 @@ const char* check_args(const kmi_attn_args* a) {
     if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seq_q < 0 || a->seq_k <= 0)
         return "sizes must be positive (seq_q may be 0)";
     if (a->heads_q % a->heads_kv != 0) return "heads_kv must divide heads_q";
+    if (a->key_lengths && a->cu_seqlens_q) return "key_lengths are for dense calls (varlen has cu_seqlens_k)";
     if (!a->q || !a->k || !a->v || !a->out) return "null q, k, v or out";
     for (const void* ptr : {a->q, a->k, a->v})
         if (reinterpret_cast<uintptr_t>(ptr) % 16) return "q, k and v must be 16-byte aligned";
@@ -1836,6 +1841,7 @@ extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t work
     }
     p.cu_q = a->cu_seqlens_q;
     p.cu_k = a->cu_seqlens_k;
+    p.klen = a->key_lengths;
     p.batch = static_cast<int>(a->batch);
     p.hq = static_cast<int>(a->heads_q);
     p.hkv = static_cast<int>(a->heads_kv);

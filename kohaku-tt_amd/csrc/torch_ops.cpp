@@ -163,7 +163,7 @@ Tensor attention_output(const Tensor& q_in, const Tensor& k_in, const Tensor& v_
 }
 
 AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, const optional<Tensor>& mask,
-                      bool is_causal, optional<double> scale) {
+                      bool is_causal, optional<double> scale, const Tensor* key_lengths = nullptr) {
     c10::DeviceGuard guard(q_in.device());
     Tensor q = q_in, k = k_in, v = v_in;
     const bool fp32 = q.scalar_type() == at::kFloat;
@@ -211,6 +211,7 @@ AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in
         a.mask_mode = KMI_MASK_STRIDED;
         for (int i = 0; i < 4; ++i) a.mask_stride[i] = m.stride(i);
     }
+    if (key_lengths) a.key_lengths = key_lengths->data_ptr<int32_t>();
     size_t ws = 0;
     check(kmi_attn_workspace_bytes(&a, &ws), "kmi_attn_workspace_bytes");
     Tensor work;
@@ -320,6 +321,58 @@ std::string sdpa_refusal_op(const Tensor& q, const Tensor& k, const Tensor& v, c
 // aten_varlen.cpp:165-231 / bridge::sdpa_varlen).  key_mask: [Tk] bool keep-mask or
 // additive; attn_mask: every sequence's [Lq_i, Lk_i] block, concatenated (additive or
 // bool), shared by the heads.  Returns (out [Tq, H, D], lse [H, Tq] fp32).
+// ---------------------------------------------------------------- key lengths
+
+// ktt::_sdpa_lengths and its companions (the reference's aten_lengths.cpp:28-67 checks,
+// 69-101 forward, 103-152 backward, 154-172 supported, 175-197 schemas): batch b's queries
+// see keys [0, lengths[b]) with lengths an int32 [B] GPU tensor clamped in-kernel to
+// [1, Sk].  No mask is built; the kernels stop at each sequence's length.
+void lengths_check(const char* op, const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& lengths) {
+    for (const Tensor* t : {&q, &k, &v})
+        TORCH_CHECK(t->dim() == 4 && t->numel() > 0 && t->is_cuda() &&
+                        (t->scalar_type() == at::kBFloat16 || t->scalar_type() == at::kHalf),
+                    "kohakutt_amd: ", op, " needs non-empty bf16 / fp16 [batch, heads, sequence, head dim] GPU tensors");
+    TORCH_CHECK(k.size(0) == q.size(0) && v.size(0) == q.size(0) && k.size(1) == v.size(1) &&
+                    q.size(1) % k.size(1) == 0 && k.size(2) == v.size(2) && k.size(3) == q.size(3),
+                "kohakutt_amd: ", op, " q / k / v shapes do not match");
+    TORCH_CHECK(lengths.dim() == 1 && lengths.size(0) == q.size(0) && lengths.scalar_type() == at::kInt &&
+                    lengths.device() == q.device(),
+                "kohakutt_amd: ", op, " key_lengths must be int32 [batch] on q's device");
+}
+
+Tensor sdpa_lengths(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& lengths, bool is_causal,
+                    optional<double> scale, bool stats) {
+    (void)stats;  // the backward recomputes in fp32; it needs no saved statistics
+    lengths_check("_sdpa_lengths", q, k, v, lengths);
+    const std::string why = sdpa_refusal_impl(q, k, v, std::nullopt, 0.0, is_causal);
+    TORCH_CHECK(why.empty(), "kohakutt_amd: _sdpa_lengths: ", why);
+    const Tensor len = lengths.contiguous();
+    return run_attention(q, k, v, std::nullopt, is_causal, scale, &len).out;
+}
+
+bool sdpa_lengths_supported(const Tensor& q, const Tensor& k, const Tensor& v, bool is_causal, bool stats) {
+    if (!sdpa_refusal_impl(q, k, v, std::nullopt, 0.0, is_causal).empty()) return false;
+    // The backward takes causal with Sq == Sk only (aten_lengths.cpp:115-118).
+    return !(stats && is_causal && q.size(2) != k.size(2));
+}
+
+std::tuple<Tensor, Tensor, Tensor> sdpa_lengths_backward(const Tensor& grad, const Tensor& out, const Tensor& q,
+                                                         const Tensor& k, const Tensor& v, const Tensor& lengths,
+                                                         bool is_causal, optional<double> scale) {
+    lengths_check("_sdpa_lengths_backward", q, k, v, lengths);
+    TORCH_CHECK(!is_causal || q.size(2) == k.size(2), "kohakutt_amd: _sdpa_lengths_backward causal needs Sq == Sk");
+    TORCH_CHECK(grad.sizes() == out.sizes() && grad.scalar_type() == q.scalar_type(),
+                "kohakutt_amd: _sdpa_lengths_backward grad must be shaped and typed as the output");
+    c10::DeviceGuard guard(q.device());
+    const int64_t B = q.size(0), Sk = k.size(2);
+    const Tensor len = lengths.clamp(1, Sk).view({B, 1, 1, 1});
+    const Tensor keep = at::arange(Sk, lengths.options()).view({1, 1, 1, Sk}) < len;
+    auto g = sdpa_overrideable_backward(grad, q, k, v, keep, {true, true, true, false}, out, Tensor(), Tensor(),
+                                        Tensor(), c10::SymInt(q.size(2)), c10::SymInt(Sk), 0.0, is_causal, Tensor(),
+                                        Tensor(), scale);
+    return {std::get<0>(g), std::get<1>(g), std::get<2>(g)};
+}
+
 std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in,
                                        const Tensor& cu_q_in, const Tensor& cu_k_in, int64_t max_q, int64_t max_k,
                                        bool is_causal, optional<double> scale, const optional<Tensor>& key_mask,
@@ -629,12 +682,20 @@ TORCH_LIBRARY(ktt, m) {
           TORCH_FN(kta::sdpa_refusal_op));
     m.def("_set_enabled(bool attention, bool norms) -> ()", TORCH_FN(kta::set_enabled));
     m.def("counters() -> int[]", TORCH_FN(kta::counters));
+    m.def("_sdpa_lengths_supported(Tensor q, Tensor k, Tensor v, bool is_causal, bool stats) -> bool");
+    m.def("_sdpa_lengths(Tensor q, Tensor k, Tensor v, Tensor lengths, bool is_causal, float? scale, bool stats) "
+          "-> Tensor");
+    m.def("_sdpa_lengths_backward(Tensor grad, Tensor out, Tensor q, Tensor k, Tensor v, Tensor lengths, "
+          "bool is_causal, float? scale) -> (Tensor, Tensor, Tensor)");
     m.def("reset_counters() -> ()", TORCH_FN(kta::reset_counters));
 }
 
 TORCH_LIBRARY_IMPL(ktt, CUDA, m) {
     m.impl("rms_norm", TORCH_FN(kta::ktt_rms_norm_cuda));
     m.impl("_sdpa_varlen", TORCH_FN(kta::sdpa_varlen));
+    m.impl("_sdpa_lengths", TORCH_FN(kta::sdpa_lengths));
+    m.impl("_sdpa_lengths_supported", TORCH_FN(kta::sdpa_lengths_supported));
+    m.impl("_sdpa_lengths_backward", TORCH_FN(kta::sdpa_lengths_backward));
 }
 
 TORCH_LIBRARY_IMPL(ktt, CompositeExplicitAutograd, m) {

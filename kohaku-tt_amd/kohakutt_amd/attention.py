@@ -15,22 +15,89 @@ _MASKED_LOGIT = -5e5
 def sdpa(q, k, v, key_lengths=None, is_causal=False, scale=None):
     """``F.scaled_dot_product_attention`` of q [B, H, Sq, D], k / v [B, Hk, Sk, D] with
     the key mask ``key < key_lengths[b]`` (B ints in [1, Sk]: a list, CPU or GPU tensor),
-    as the reference's ``kohakutt.sdpa`` (``attention.py:10-23``).  The lengths become a
-    [B, 1, 1, Sk] bool padding mask (with causal, a [B, 1, Sq, Sk] mask that also holds
-    the top-left causal rule)."""
+    as the reference's ``kohakutt.sdpa`` (``attention.py:10-23``).  On the kernels
+    (``ktt::_sdpa_lengths``) the lengths go to the kernel as a per-batch key count: no
+    mask is built, key tiles past a length are not read.  Calls the kernels do not take
+    run SDPA with a bool mask built on the device (``lengths.py:79-89``)."""
     gqa = q.size(1) != k.size(1)
     if key_lengths is None:
         return F.scaled_dot_product_attention(
             q, k, v, is_causal=is_causal, scale=scale, enable_gqa=gqa
         )
+    lengths = device_lengths(key_lengths, q.size(0), k.size(-2), q.device)
+    if kernel_takes(q, k, v, is_causal):
+        return _lengths_kernel(q, k, v, lengths, is_causal, scale)
+    return _lengths_masked(q, k, v, lengths, is_causal, scale)
+
+
+def device_lengths(key_lengths, batch, keys, device):
+    """``key_lengths`` as an int32 [batch] tensor on ``device`` (``lengths.py:10-29``): a
+    list or a CPU tensor is checked to lie in [1, keys]; a GPU tensor is taken as it is
+    (the kernels clamp it to [1, keys], so it is never downloaded)."""
+    if isinstance(key_lengths, torch.Tensor) and key_lengths.device.type != "cpu":
+        lengths = key_lengths.to(device=device, dtype=torch.int32)
+    else:
+        lengths = torch.as_tensor(key_lengths, dtype=torch.int32)
+        if lengths.numel() and (int(lengths.min()) < 1 or int(lengths.max()) > keys):
+            raise ValueError(
+                f"kohakutt_amd.sdpa: key_lengths must lie in [1, {keys}], got {lengths.tolist()}"
+            )
+        lengths = lengths.to(device)
+    if lengths.dim() != 1 or lengths.size(0) != batch:
+        raise ValueError(
+            f"kohakutt_amd.sdpa: key_lengths must hold one length per batch ({batch}), "
+            f"got shape {tuple(lengths.shape)}"
+        )
+    return lengths.contiguous()
+
+
+def kernel_takes(q, k, v, is_causal):
+    """True when ``ktt::_sdpa_lengths`` takes q, k, v (``lengths.py:36-50``): GPU tensors
+    the attention kernels cover; with gradients, causal needs Sq == Sk."""
+    tensors = (q, k, v)
+    grads = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+    return all(t.is_cuda and t.dim() == 4 for t in tensors) and bool(
+        torch.ops.ktt._sdpa_lengths_supported(q, k, v, bool(is_causal), grads)
+    )
+
+
+class _Lengths(torch.autograd.Function):
+    """The kernel route with autograd (``lengths.py:53-69``): dq, dk, dv from
+    ``ktt::_sdpa_lengths_backward``; the lengths get no gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, lengths, causal, scale):
+        out = torch.ops.ktt._sdpa_lengths(q, k, v, lengths, causal, scale, True)
+        ctx.save_for_backward(q, k, v, lengths, out)
+        ctx.args = (causal, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        q, k, v, lengths, out = ctx.saved_tensors
+        causal, scale = ctx.args
+        dq, dk, dv = torch.ops.ktt._sdpa_lengths_backward(
+            grad.contiguous(), out, q, k, v, lengths, causal, scale
+        )
+        return dq, dk, dv, None, None, None
+
+
+def _lengths_kernel(q, k, v, lengths, is_causal, scale):
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _Lengths.apply(q, k, v, lengths, bool(is_causal), scale)
+    return torch.ops.ktt._sdpa_lengths(q, k, v, lengths, bool(is_causal), scale, False)
+
+
+def _lengths_masked(q, k, v, lengths, is_causal, scale):
+    """The explicit-mask route: a bool [B, 1, Sq, Sk] mask built on the device."""
     b, sq, sk = q.size(0), q.size(2), k.size(2)
-    lengths = torch.as_tensor(key_lengths, device=q.device).reshape(b, 1, 1, 1)
-    mask = torch.arange(sk, device=q.device).reshape(1, 1, 1, sk) < lengths
+    keys = torch.arange(sk, device=q.device, dtype=torch.int32)
+    keep = (keys[None, :] < lengths.reshape(b, 1))[:, None, None, :]
     if is_causal:
-        rows = torch.arange(sq, device=q.device).reshape(1, 1, sq, 1)
-        mask = mask & (torch.arange(sk, device=q.device).reshape(1, 1, 1, sk) <= rows)
+        rows = torch.arange(sq, device=q.device, dtype=torch.int32)
+        keep = keep & (keys[None, :] <= rows[:, None])[None, None]
     return F.scaled_dot_product_attention(
-        q, k, v, attn_mask=mask, scale=scale, enable_gqa=gqa
+        q, k, v, attn_mask=keep, scale=scale, enable_gqa=q.size(1) != k.size(1)
     )
 
 

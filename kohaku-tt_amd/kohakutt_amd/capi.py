@@ -64,6 +64,7 @@ class AttnArgs(ctypes.Structure):
         ("total_k", ctypes.c_int64),
         ("num_splits", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("key_lengths", ctypes.c_void_p),
     ]
 
 

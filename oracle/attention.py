@@ -99,6 +99,23 @@ def sdpa(q, k, v, attn_mask=None, is_causal=False, scale=None):
     return out, lse
 
 
+def sdpa_lengths(q, k, v, key_lengths, is_causal=False, scale=None):
+    """Attention with per-batch key lengths (the reference's ``kohakutt.sdpa(key_lengths=)``,
+    ``src/kohakutt/attention.py:10-23``): batch b's queries see keys [0, L_b), L_b =
+    key_lengths[b] clamped to [1, Sk] (device lengths are clamped,
+    ``docs/reference/kernels/flash.md`` "Key lengths"); with causal, also keys <= the
+    query's position (top-left).  Restated as the reference's explicit-mask route
+    (``torch_backend/lengths.py:79-89``).  Returns (out, lse) in float64."""
+    q = _f64(q)
+    b, sq, sk = q.shape[0], q.shape[2], np.asarray(k).shape[2]
+    lengths = np.clip(np.asarray(key_lengths, dtype=np.int64).reshape(b), 1, sk)
+    keys = np.arange(sk)
+    keep = (keys[None, :] < lengths[:, None])[:, None, None, :]
+    if is_causal:
+        keep = keep & (keys[None, :] <= np.arange(sq)[:, None])[None, None]
+    return sdpa(q, k, v, keep, False, scale)
+
+
 def offsets(cu) -> list[int]:
     """Cumulative offsets as a list of ints."""
     return [int(x) for x in np.asarray(cu).reshape(-1).tolist()]

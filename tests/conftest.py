@@ -19,9 +19,15 @@ def pytest_configure(config):
     # Test modules import the package at collection; build it here when it is missing
     # (on the GPU box the libraries come prebuilt with the tree).
     if not _built():
-        from kohakutt_amd import _build
+        # Loaded by path: the package's __init__ refuses to import before the libraries exist.
+        import importlib.util
 
-        _build.build_all()
+        spec = importlib.util.spec_from_file_location(
+            "_kohakutt_amd_build", REPO / "kohaku-tt_amd" / "kohakutt_amd" / "_build.py"
+        )
+        build = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(build)
+        build.build_all()
 
 
 @pytest.fixture(scope="session")

@@ -70,3 +70,18 @@ def test_set_enabled_round_trip():
 
 def test_varlen_kernel_registered_for_gpu():
     assert katt.install_varlen_kernel()
+
+
+def test_key_lengths_validation_follows_the_reference():
+    """Host key lengths must lie in [1, Sk] with one per batch (``lengths.py:10-29``); a
+    GPU tensor is not checked on the host (the kernels clamp it)."""
+    from kohakutt_amd.attention import device_lengths
+
+    assert device_lengths([1, 5], 2, 5, "cpu").tolist() == [1, 5]
+    assert device_lengths(torch.tensor([3, 4]), 2, 5, "cpu").dtype == torch.int32
+    with pytest.raises(ValueError, match="must lie in"):
+        device_lengths([0, 5], 2, 5, "cpu")
+    with pytest.raises(ValueError, match="must lie in"):
+        device_lengths([1, 6], 2, 5, "cpu")
+    with pytest.raises(ValueError, match="one length per batch"):
+        device_lengths([1, 2, 3], 2, 5, "cpu")

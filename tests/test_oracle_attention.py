@@ -204,3 +204,34 @@ def test_varlen_key_mask_and_packed_mask():
 def test_varlen_offset_errors(cu_q, cu_k, causal, msg):
     with pytest.raises(ValueError, match=msg):
         A.intervals(cu_q, cu_k, causal)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_lengths_is_attention_over_each_batch_prefix(causal):
+    """Key lengths pinned by slicing: batch b's output equals torch CPU float64 SDPA over
+    its first L_b keys only (causal top-left over the prefix, query rows past L_b seeing
+    the prefix), and lengths outside [1, Sk] clamp."""
+    b, hq, hk, sq, sk, d = 4, 6, 2, 9, 37, 16
+    q, k, v = _t64(b, hq, sq, d, seed=71), _t64(b, hk, sk, d, seed=72), _t64(b, hk, sk, d, seed=73)
+    lengths = [5, 37, 1, 20]
+    out, _ = A.sdpa_lengths(q.numpy(), k.numpy(), v.numpy(), lengths, is_causal=causal)
+    for i, n in enumerate(lengths):
+        qi, ki, vi = q[i : i + 1], k[i : i + 1, :, :n], v[i : i + 1, :, :n]
+        if causal:
+            keep = torch.arange(n)[None, :] <= torch.arange(sq)[:, None]
+            ref = _torch_sdpa(qi, ki, vi, mask=keep)
+        else:
+            ref = _torch_sdpa(qi, ki, vi)
+        assert np.abs(out[i : i + 1] - ref.numpy()).max() < 1e-12, (i, n)
+    clamped, _ = A.sdpa_lengths(q.numpy(), k.numpy(), v.numpy(), [0, 99, -3, 20], is_causal=causal)
+    expect, _ = A.sdpa_lengths(q.numpy(), k.numpy(), v.numpy(), [1, 37, 1, 20], is_causal=causal)
+    assert np.array_equal(clamped, expect)
+
+
+def test_sdpa_lengths_catches_a_planted_off_by_one():
+    """A planted mistake (keys <= L_b kept instead of < L_b) moves the result."""
+    b, hq, sq, sk, d = 2, 2, 3, 10, 8
+    q, k, v = _t64(b, hq, sq, d, seed=81), _t64(b, hq, sk, d, seed=82), _t64(b, hq, sk, d, seed=83)
+    good, _ = A.sdpa_lengths(q.numpy(), k.numpy(), v.numpy(), [4, 7])
+    wrong, _ = A.sdpa_lengths(q.numpy(), k.numpy(), v.numpy(), [5, 8])
+    assert np.abs(good - wrong).max() > 1e-3
