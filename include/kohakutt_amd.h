@@ -113,7 +113,7 @@ typedef struct kmi_attn_args {
     /* Dense calls only (ABI 2; NULL: every key).  Device int32 [batch]: sequence b's
      * queries see keys [0, L_b), L_b = key_lengths[b] clamped to [1, seq_k]; no mask is
      * built or read and key tiles past L_b are not loaded.  Query rows past L_b still see
-     * the first L_b keys.  Composes with causal (top-left) and with a mask.  Replaces the
+     * the first L_b keys.  Composes with causal (top-left).  Replaces the
      * reference's bridge::sdpa_lengths behind ktt::_sdpa_lengths (aten_lengths.cpp:69-101,
      * 175-197; docs/reference/kernels/flash.md, Key lengths). */
     const int32_t* key_lengths;
