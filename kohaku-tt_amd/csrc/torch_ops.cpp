@@ -18,6 +18,7 @@
 #include <ATen/ops/_fused_sdp_choice_cuda_dispatch.h>
 #include <ATen/ops/native_layer_norm_cuda_dispatch.h>
 #include <ATen/ops/rms_norm_compositeimplicitautograd_dispatch.h>
+#include <ATen/ops/scaled_dot_product_attention_compositeimplicitautograd_dispatch.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/autograd.h>
@@ -310,17 +311,31 @@ int64_t fused_sdp_choice(const Tensor& q, const Tensor& k, const Tensor& v, cons
     return at::cuda::_fused_sdp_choice(q, k, v, mask, dropout_p, is_causal, scale, enable_gqa);
 }
 
+// aten::scaled_dot_product_attention on AutogradCUDA: a bool mask reaches the kernels as
+// it is (they read bool keep-masks natively), where torch's composite would first turn it
+// into an additive mask of the query dtype -- three device kernels per call, about 6 us of
+// a config 3 decode.  Everything else (gradients, float masks, no mask, calls the kernels
+// do not take, an sdpa_kernel scope without the overrideable backend) runs torch's
+// composite, which routes through _fused_sdp_choice as before.  Like the reference's
+// route, enable_gqa is not required: K/V heads dividing Q heads is enough.
+Tensor sdpa_entry(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask, double dropout_p,
+                  bool is_causal, optional<double> scale, bool enable_gqa) {
+    const bool grads = at::GradMode::is_enabled() && (q.requires_grad() || k.requires_grad() || v.requires_grad());
+    if (!grads && mask_given(mask) && mask->scalar_type() == at::kBool &&
+        at::globalContext().userEnabledOverrideableSDP() &&
+        sdpa_refusal_impl(q, k, v, mask, dropout_p, is_causal).empty()) {
+        at::AutoDispatchBelowADInplaceOrView below;
+        return run_attention(q, k, v, mask, is_causal, scale).out;
+    }
+    return at::compositeimplicitautograd::scaled_dot_product_attention(q, k, v, mask, dropout_p, is_causal, scale,
+                                                                       enable_gqa);
+}
+
 std::string sdpa_refusal_op(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask,
                             bool is_causal) {
     return sdpa_refusal_impl(q, k, v, mask, 0.0, is_causal);
 }
 
-// ---------------------------------------------------------------- varlen
-
-// ktt::_sdpa_varlen: packed attention over cu_seqlens (the reference's
-// aten_varlen.cpp:165-231 / bridge::sdpa_varlen).  key_mask: [Tk] bool keep-mask or
-// additive; attn_mask: every sequence's [Lq_i, Lk_i] block, concatenated (additive or
-// bool), shared by the heads.  Returns (out [Tq, H, D], lse [H, Tq] fp32).
 // ---------------------------------------------------------------- key lengths
 
 // ktt::_sdpa_lengths and its companions (the reference's aten_lengths.cpp:28-67 checks,
@@ -373,6 +388,12 @@ std::tuple<Tensor, Tensor, Tensor> sdpa_lengths_backward(const Tensor& grad, con
     return {std::get<0>(g), std::get<1>(g), std::get<2>(g)};
 }
 
+// ---------------------------------------------------------------- varlen
+
+// ktt::_sdpa_varlen: packed attention over cu_seqlens (the reference's
+// aten_varlen.cpp:165-231 / bridge::sdpa_varlen).  key_mask: [Tk] bool keep-mask or
+// additive; attn_mask: every sequence's [Lq_i, Lk_i] block, concatenated (additive or
+// bool), shared by the heads.  Returns (out [Tq, H, D], lse [H, Tq] fp32).
 std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in,
                                        const Tensor& cu_q_in, const Tensor& cu_k_in, int64_t max_q, int64_t max_k,
                                        bool is_causal, optional<double> scale, const optional<Tensor>& key_mask,
@@ -711,4 +732,5 @@ TORCH_LIBRARY_IMPL(aten, CUDA, m) {
 
 TORCH_LIBRARY_IMPL(aten, AutogradCUDA, m) {
     m.impl("rms_norm", TORCH_FN(kta::rms_norm));
+    m.impl("scaled_dot_product_attention", TORCH_FN(kta::sdpa_entry));
 }

@@ -498,3 +498,54 @@ def test_one_or_two_keys(native, dev, b, hq, hk, sq, sk, d):
     q, k, v = C.randn(g, b, hq, sq, d), C.randn(g, b, hk, sk, d), C.randn(g, b, hk, sk, d)
     out, cpu, ref = _dense_case(native, dev, q, k, v)
     _check(out, cpu, ref, f"few keys {b}x{hq}/{hk}x{sq}x{sk}x{d}")
+
+
+def test_bool_mask_reaches_the_kernels_unconverted(native, dev):
+    """F.scaled_dot_product_attention with a bool mask (no gradients) runs the kernels on
+    the bool mask itself; the output is bit-identical to the same mask given additively
+    (0 / -inf in bf16, what torch's composite would have made of it), including a
+    fully-masked row (softmax over its raw scores)."""
+    g = C.gen(21)
+    b, h, hk, s, sk, d = 2, 8, 2, 5, 700, 128
+    q, k, v = C.randn(g, b, h, s, d), C.randn(g, b, hk, sk, d), C.randn(g, b, hk, sk, d)
+    keep = torch.rand(b, 1, s, sk, generator=g) > 0.3
+    keep[1, 0, 2] = False
+    qd, kd, vd, md = q.to(dev), k.to(dev), v.to(dev), keep.to(dev)
+    add = torch.zeros(keep.shape, dtype=torch.bfloat16).masked_fill(~keep, float("-inf")).to(dev)
+    native.reset_counters()
+    out_b = F.scaled_dot_product_attention(qd, kd, vd, attn_mask=md, enable_gqa=True)
+    out_a = F.scaled_dot_product_attention(qd, kd, vd, attn_mask=add, enable_gqa=True)
+    torch.cuda.synchronize()
+    assert native.counters()["attention"] == 2
+    assert torch.equal(out_b, out_a)
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), keep.numpy())
+    assert np.abs(out_b.cpu().double().numpy() - ref).max() < 2e-2
+
+
+def test_bool_mask_with_gradients_and_scopes_keep_torch_routes(native, dev):
+    """With gradients a bool-mask call goes through torch's composite (overrideable op +
+    the fp32 recompute backward); under sdpa_kernel(MATH) the kernels are not used."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    g = C.gen(22)
+    b, h, s, d = 2, 4, 64, 64
+    q, k, v = C.randn(g, b, h, s, d), C.randn(g, b, h, s, d), C.randn(g, b, h, s, d)
+    keep = torch.rand(b, 1, s, s, generator=g) > 0.3
+    keep[..., 0] = True
+    qd = q.to(dev).requires_grad_()
+    kd, vd, md = k.to(dev), v.to(dev), keep.to(dev)
+    native.reset_counters()
+    out = F.scaled_dot_product_attention(qd, kd, vd, attn_mask=md)
+    out.float().sum().backward()
+    torch.cuda.synchronize()
+    assert native.counters()["attention"] == 1
+    q64 = q.double().requires_grad_()
+    ref = F.scaled_dot_product_attention(q64, k.double(), v.double(), attn_mask=keep)
+    ref.sum().backward()
+    assert (qd.grad.cpu().double() - q64.grad).abs().max().item() < 5e-2
+    native.reset_counters()
+    with sdpa_kernel([SDPBackend.MATH]):
+        out_m = F.scaled_dot_product_attention(qd.detach(), kd, vd, attn_mask=md)
+    torch.cuda.synchronize()
+    assert native.counters()["attention"] == 0
+    assert (out_m.float() - out.detach().float()).abs().max().item() < 3e-2
