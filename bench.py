@@ -137,6 +137,26 @@ def build_rows():
 
     c1 = C.config1()
     sdpa_row("c1_attn", "C1 causal GQA prefill 1x14/2x2048x64", "mfma", c1["q"], c1["k"], c1["v"], causal=True)
+
+    def bwd_make(dev, n):
+        sets = _rotate(dev, [c1["q"], c1["k"], c1["v"], c1["q"]], n)
+        calls = []
+        for s in sets:
+            q, k, v, go = s
+            out, lse = torch.ops.aten._scaled_dot_product_fused_attention_overrideable(q, k, v, None, 0.0, True)[:2]
+            calls.append(lambda q=q, k=k, v=v, go=go, out=out, lse=lse:
+                         torch.ops.ktt._sdpa_flash_backward(go, q, k, v, out, lse, True))
+        return calls
+
+    def bwd_cpu():
+        q, k, v = (t.detach().clone().requires_grad_() for t in (c1["q"], c1["k"], c1["v"]))
+        out = F.scaled_dot_product_attention(q, k.repeat_interleave(7, 1), v.repeat_interleave(7, 1), is_causal=True)
+        return lambda: torch.autograd.grad(out, (q, k, v), c1["q"], retain_graph=True)
+
+    # Backward FLOPs: S, dP, dV, dK, dQ = 2.5x the forward's two products.
+    rows["c1_attn_bwd"] = Row(
+        "c1_attn_bwd", "extra: C1 attention backward (flash dQ/dK/dV from the forward's lse)", "mfma",
+        2.5 * C.attn_flops(64, 14, C.causal_pairs(1, 2048)), None, (bwd_make, bwd_cpu), "attn_bwd_dkdv")
     norm_row("c1_rms", "C1 rms_norm [1,2048,896]", c1["x"], c1["w"], None, 1e-6, "rms")
 
     c2 = C.config2(1)

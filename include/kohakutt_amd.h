@@ -127,6 +127,51 @@ int kmi_attn_fwd(const kmi_attn_args* args, void* workspace, size_t workspace_by
                  void* stream);
 
 /*
+ * Attention backward of an unmasked dense call (causal top-left or not):
+ *   dq, dk, dv of out = softmax(scale * q k^T) v given grad_out and the forward's lse
+ *   (fp32 natural log, as kmi_attn_fwd writes it).  The probabilities are recomputed per
+ *   tile from lse; nothing of size Sq x Sk is stored.  GQA: dk / dv of a K/V head sum its
+ *   query heads.  Layouts as kmi_attn_fwd's dense ones (element strides of the batch, head
+ *   and sequence dims, head-dim stride 1); q, k, v, grad_out 16-byte aligned with strides
+ *   multiples of 8.  Workspace: kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row
+ *   dot products; with GQA also fp32 per-query-head dK / dV partials).
+ * Replaces the reference's flash backward behind tt_sdpa_overrideable_backward's stats
+ * route (aten_attention.cpp:716-812; bridge in device_attention.cpp:1208-1281;
+ * docs/reference/kernels/flash.md:151-206).  Supported: BF16 / F16, head_dim 64 or 128.
+ */
+typedef struct kmi_attn_bwd_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* out;
+    const void* grad_out;
+    const float* lse;
+    void* grad_q;
+    void* grad_k;
+    void* grad_v;
+    int32_t dtype;
+    int32_t causal;
+    int64_t batch, heads_q, heads_kv, seq_q, seq_k, head_dim;
+    int64_t q_stride[3];
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[3];
+    int64_t do_stride[3];
+    int64_t dq_stride[3];
+    int64_t dk_stride[3];
+    int64_t dv_stride[3];
+    int64_t lse_stride[3];
+    double scale;
+} kmi_attn_bwd_args;
+
+/* Bytes of workspace kmi_attn_bwd needs for `args`. */
+int kmi_attn_bwd_workspace_bytes(const kmi_attn_bwd_args* args, size_t* bytes);
+
+/* Enqueues the attention backward of `args` on `stream` (hipStream_t). */
+int kmi_attn_bwd(const kmi_attn_bwd_args* args, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
  * LayerNorm forward over rows of `width` contiguous elements:
  *   y = (x - mean) * rstd * weight + bias, rstd = 1 / sqrt(max(var, 0) + eps),
  * mean / rstd written as fp32 [rows] (either may be NULL).  weight / bias may be NULL;

@@ -1,0 +1,444 @@
+// Attention backward on gfx950 (flash-style: nothing of size Sq x Sk is stored).
+//
+// The reference's training route recomputes the probabilities from the forward's row
+// statistics and runs a dQ pass and a dK/dV pass (docs/reference/kernels/flash.md,
+// "Backward", flash.md:151-206; ktt_flash/bw_*.cpp; bridge in device_attention.cpp:
+// 1208-1281).  Here, for unmasked dense calls (causal top-left or not, GQA, head dim 64
+// or 128, bf16 / fp16):
+//
+//   attn_bwd_pre     Dr[row] = sum_d dO[row, d] * O[row, d]   (fp32)
+//   attn_bwd_dkdv    one workgroup per (sequence, query head, 32-key tile): for every
+//                    32-row query block that sees the tile, P = exp2(c S - lse2),
+//                    dP = dO V^T, dS = P (dP - Dr); dV += P^T dO, dK += dS^T Q (fp32
+//                    accumulators in registers).  Without GQA it writes dK / dV; with GQA
+//                    fp32 per-query-head partials that
+//   attn_bwd_group_sum sums over each K/V head's query heads in a fixed order (no atomics)
+//   attn_bwd_dq      one workgroup per (sequence, query head, 32-row block): over the key
+//                    tiles it sees, the same P / dS, dQ += dS K
+//
+// S = Q K^T, dP = dO V^T and the three gradient products run on
+// v_mfma_f32_16x16x32_{bf16,f16}.  Every operand is read from LDS along its contraction
+// index (16 contiguous bytes per lane): tiles needed with either index contiguous are
+// staged twice, row-major and transposed.  lse is the forward's natural-log row LSE.
+#include "common.hpp"
+
+namespace kmi {
+namespace {
+
+constexpr int BT = 32;          // keys per K/V tile and rows per query block
+constexpr int TP = BT + 8;      // pitch of transposed / [32][32] tiles (elements)
+constexpr int BWD_THREADS = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T>
+struct BwdMfma;
+template <>
+struct BwdMfma<bf16> {
+    typedef bf16x8 v8;
+    static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct BwdMfma<f16> {
+    typedef f16x8 v8;
+    static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+struct BwdParams {
+    const void *q, *k, *v, *o, *dout;
+    const float* lse;
+    void *dq, *dk, *dv;
+    float* dr;  // [batch][hq][seq_q] fp32 workspace
+    // GQA (group > 1): per-query-head dK / dV partials [batch][hq][seq_k][D] fp32, summed
+    // over each group by attn_bwd_group_sum; null when every K/V head has one query head.
+    float *pdk, *pdv;
+    int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3], ls[3];
+    int batch, hq, hkv, group, seq_q, seq_k, causal;
+    float scale, c2;  // c2 = scale * log2(e)
+};
+
+// One 16x16 output block, k = 32: A rows at a (pitch ap), B columns at b (pitch bp),
+// both contiguous along k.  Lane (g4, l16) reads A[l16][8 g4 ..] and B[l16][8 g4 ..].
+template <typename T>
+__device__ __forceinline__ f32x4 mma_lds(const T* a, int ap, const T* b, int bp, f32x4 acc) {
+    typedef typename BwdMfma<T>::v8 v8;
+    const int lane = threadIdx.x & 63;
+    const int g4 = lane >> 4, l16 = lane & 15;
+    const v8 av = *reinterpret_cast<const v8*>(a + l16 * ap + 8 * g4);
+    const v8 bv = *reinterpret_cast<const v8*>(b + l16 * bp + 8 * g4);
+    return BwdMfma<T>::run(av, bv, acc);
+}
+
+// Stages rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) into LDS: row-major
+// at dst (pitch D + 8) and, when dstT is set, transposed at dstT ([D][TP]).  Rows past the
+// end are zeros.
+template <typename T, int D>
+__device__ __forceinline__ void stage(const T* src, int64_t rs, int r0, int nrows, T* dst, T* dstT) {
+    constexpr int CH = D / 8;
+    for (int c = threadIdx.x; c < BT * CH; c += BWD_THREADS) {
+        const int r = c / CH, ch = c - r * CH;
+        u32x4 val = u32x4{0u, 0u, 0u, 0u};
+        if (r0 + r < nrows) val = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(r0 + r) * rs + 8 * ch);
+        *reinterpret_cast<u32x4*>(dst + r * (D + 8) + 8 * ch) = val;
+        if (dstT) {
+            const auto e = __builtin_bit_cast(typename BwdMfma<T>::v8, val);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dstT[(8 * ch + i) * TP + r] = e[i];
+        }
+    }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_pre(const BwdParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t rows = static_cast<int64_t>(p.batch) * p.hq * p.seq_q;
+    if (row >= rows) return;
+    const int i = static_cast<int>(row % p.seq_q);
+    const int h = static_cast<int>((row / p.seq_q) % p.hq);
+    const int b = static_cast<int>(row / (static_cast<int64_t>(p.seq_q) * p.hq));
+    const T* o = static_cast<const T*>(p.o) + b * p.os[0] + h * p.os[1] + i * p.os[2];
+    const T* d = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1] + i * p.dos[2];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) s += to_f32(o[lane + 64 * j]) * to_f32(d[lane + 64 * j]);
+    s = wave_sum(s);
+    if (lane == 0) p.dr[row] = s;
+}
+
+// P and dS of one 16x16 block held by the calling wavefront: S = Q K^T and dP = dO V^T
+// from the staged tiles, rows [rb 16, +16) of the query block at r0 and keys [kb 16, +16)
+// of the key tile at k0.  Lane (g4, l16) returns rows 4 g4 + j, key l16.
+template <typename T, int D>
+__device__ __forceinline__ void p_ds(const BwdParams& p, const T* qs, const T* dos, const T* ks, const T* vs,
+                                     const float* lse2, const float* drs, int rb, int kb, int r0, int k0,
+                                     float pv[4], float dsv[4]) {
+    const int lane = threadIdx.x & 63;
+    const int g4 = lane >> 4, l16 = lane & 15;
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f}, dp = s;
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+        s = mma_lds<T>(qs + rb * 16 * (D + 8) + 32 * c, D + 8, ks + kb * 16 * (D + 8) + 32 * c, D + 8, s);
+        dp = mma_lds<T>(dos + rb * 16 * (D + 8) + 32 * c, D + 8, vs + kb * 16 * (D + 8) + 32 * c, D + 8, dp);
+    }
+    const int key = k0 + kb * 16 + l16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int rl = rb * 16 + 4 * g4 + j;
+        const int pos = r0 + rl;
+        const bool keep = key < p.seq_k && (!p.causal || key <= pos);
+        // Rows past the end carry lse2 = +inf: their P is exactly 0.
+        const float e = keep ? __builtin_amdgcn_exp2f(s[j] * p.c2 - lse2[rl]) : 0.f;
+        pv[j] = e;
+        dsv[j] = e * (dp[j] - drs[rl]);
+    }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void stage_rows_stats(const BwdParams& p, int b, int h, int r0, float* lse2, float* drs) {
+    if (threadIdx.x < BT) {
+        const int i = r0 + threadIdx.x;
+        const bool ok = i < p.seq_q;
+        lse2[threadIdx.x] = ok ? p.lse[b * p.ls[0] + h * p.ls[1] + static_cast<int64_t>(i) * p.ls[2]] * kLog2e
+                               : INFINITY;
+        drs[threadIdx.x] = ok ? p.dr[(static_cast<int64_t>(b) * p.hq + h) * p.seq_q + i] : 0.f;
+    }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) {
+    constexpr int RP = D + 8;
+    __shared__ __align__(16) T ks[BT * RP];
+    __shared__ __align__(16) T vs[BT * RP];
+    __shared__ __align__(16) T qs[BT * RP];
+    __shared__ __align__(16) T dos[BT * RP];
+    __shared__ __align__(16) T qt[D * TP];
+    __shared__ __align__(16) T dot[D * TP];
+    __shared__ __align__(16) T pt[BT * TP];
+    __shared__ __align__(16) T dst[BT * TP];
+    __shared__ float lse2[BT], drs[BT];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g4 = lane >> 4, l16 = lane & 15;
+    const int ntk = (p.seq_k + BT - 1) / BT;
+    const int tile = blockIdx.x % ntk;
+    const int bh = blockIdx.x / ntk;  // (sequence, query head)
+    const int b = bh / p.hq, h = bh - b * p.hq;
+    const int kvh = h / p.group;
+    const int k0 = tile * BT;
+
+    stage<T, D>(static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1], p.ks[2], k0, p.seq_k, ks, nullptr);
+    stage<T, D>(static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1], p.vs[2], k0, p.seq_k, vs, nullptr);
+
+    // Wave w: P / dS block (rows rb, keys kb); dK / dV blocks keys kb2, dims db0 + i.
+    const int rb = wave >> 1, kb = wave & 1;
+    const int kb2 = wave & 1;
+    constexpr int NDB = D / 32;
+    const int db0 = (wave >> 1) * NDB;
+    f32x4 dk[NDB], dv[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) dk[i] = dv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Causal (top-left): a query block sees this tile only if its last position reaches k0.
+    const int rstart = p.causal ? (k0 / BT) * BT : 0;
+    {
+        for (int r0 = rstart; r0 < p.seq_q; r0 += BT) {
+            __syncthreads();  // the previous block's LDS reads are done
+            stage<T, D>(static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1], p.qs[2], r0, p.seq_q, qs, qt);
+            stage<T, D>(static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1], p.dos[2], r0, p.seq_q, dos, dot);
+            stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
+            __syncthreads();
+            float pv[4], dsv[4];
+            p_ds<T, D>(p, qs, dos, ks, vs, lse2, drs, rb, kb, r0, k0, pv, dsv);
+            // Transposed stores: key row kb 16 + l16, rows rb 16 + 4 g4 .. + 3.
+            T* pw = pt + (kb * 16 + l16) * TP + rb * 16 + 4 * g4;
+            T* dw = dst + (kb * 16 + l16) * TP + rb * 16 + 4 * g4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pw[j] = from_f32<T>(pv[j]);
+                dw[j] = from_f32<T>(dsv[j]);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < NDB; ++i) {
+                const int db = db0 + i;
+                dv[i] = mma_lds<T>(pt + kb2 * 16 * TP, TP, dot + db * 16 * TP, TP, dv[i]);
+                dk[i] = mma_lds<T>(dst + kb2 * 16 * TP, TP, qt + db * 16 * TP, TP, dk[i]);
+            }
+        }
+    }
+    // Lane (g4, l16) of block (kb2, db) holds keys kb2 16 + 4 g4 + j, dim db 16 + l16.
+    if (p.pdk) {
+        const int64_t base = (static_cast<int64_t>(b) * p.hq + h) * p.seq_k;
+#pragma unroll
+        for (int i = 0; i < NDB; ++i) {
+            const int d = (db0 + i) * 16 + l16;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int key = k0 + kb2 * 16 + 4 * g4 + j;
+                if (key < p.seq_k) {
+                    p.pdk[(base + key) * D + d] = dk[i][j] * p.scale;
+                    p.pdv[(base + key) * D + d] = dv[i][j];
+                }
+            }
+        }
+        return;
+    }
+    T* dkp = static_cast<T*>(p.dk) + b * p.dks[0] + kvh * p.dks[1];
+    T* dvp = static_cast<T*>(p.dv) + b * p.dvs[0] + kvh * p.dvs[1];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) {
+        const int d = (db0 + i) * 16 + l16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int key = k0 + kb2 * 16 + 4 * g4 + j;
+            if (key < p.seq_k) {
+                dkp[static_cast<int64_t>(key) * p.dks[2] + d] = from_f32<T>(dk[i][j] * p.scale);
+                dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[i][j]);
+            }
+        }
+    }
+}
+
+// dK / dV of a K/V head: the sum of its query heads' fp32 partials, in head order.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_group_sum(const BwdParams p) {
+    constexpr int Q = D / 4;  // float4 items per key row
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t items = static_cast<int64_t>(p.batch) * p.hkv * p.seq_k * Q;
+    if (item >= items) return;
+    const int c = static_cast<int>(item % Q);
+    const int key = static_cast<int>((item / Q) % p.seq_k);
+    const int64_t bk = item / (static_cast<int64_t>(Q) * p.seq_k);  // b * hkv + kvh
+    const int b = static_cast<int>(bk / p.hkv), kvh = static_cast<int>(bk % p.hkv);
+    f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = sk;
+    for (int g = 0; g < p.group; ++g) {
+        const int64_t row = (static_cast<int64_t>(b) * p.hq + kvh * p.group + g) * p.seq_k + key;
+        sk += *reinterpret_cast<const f32x4*>(p.pdk + row * D + 4 * c);
+        sv += *reinterpret_cast<const f32x4*>(p.pdv + row * D + 4 * c);
+    }
+    T* dkp = static_cast<T*>(p.dk) + b * p.dks[0] + kvh * p.dks[1] + static_cast<int64_t>(key) * p.dks[2] + 4 * c;
+    T* dvp = static_cast<T*>(p.dv) + b * p.dvs[0] + kvh * p.dvs[1] + static_cast<int64_t>(key) * p.dvs[2] + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        dkp[e] = from_f32<T>(sk[e]);
+        dvp[e] = from_f32<T>(sv[e]);
+    }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
+    constexpr int RP = D + 8;
+    __shared__ __align__(16) T qs[BT * RP];
+    __shared__ __align__(16) T dos[BT * RP];
+    __shared__ __align__(16) T ks[BT * RP];
+    __shared__ __align__(16) T vs[BT * RP];
+    __shared__ __align__(16) T kt[D * TP];
+    __shared__ __align__(16) T dss[BT * TP];
+    __shared__ float lse2[BT], drs[BT];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g4 = lane >> 4, l16 = lane & 15;
+    const int nqb = (p.seq_q + BT - 1) / BT;
+    const int qb = blockIdx.x % nqb;
+    const int bh = blockIdx.x / nqb;
+    const int b = bh / p.hq, h = bh - b * p.hq;
+    const int kvh = h / p.group;
+    const int r0 = qb * BT;
+
+    stage<T, D>(static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1], p.qs[2], r0, p.seq_q, qs, nullptr);
+    stage<T, D>(static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1], p.dos[2], r0, p.seq_q, dos, nullptr);
+    stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
+
+    const int rb = wave >> 1, kb = wave & 1;
+    const int rb2 = wave & 1;
+    constexpr int NDB = D / 32;
+    const int db0 = (wave >> 1) * NDB;
+    f32x4 dq[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) dq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int kend = p.causal ? min(p.seq_k, r0 + BT) : p.seq_k;
+    const T* kbase = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
+    const T* vbase = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
+    for (int k0 = 0; k0 < kend; k0 += BT) {
+        __syncthreads();
+        stage<T, D>(kbase, p.ks[2], k0, p.seq_k, ks, kt);
+        stage<T, D>(vbase, p.vs[2], k0, p.seq_k, vs, nullptr);
+        __syncthreads();
+        float pv[4], dsv[4];
+        p_ds<T, D>(p, qs, dos, ks, vs, lse2, drs, rb, kb, r0, k0, pv, dsv);
+        (void)pv;
+        // dS row-major: rows rb 16 + 4 g4 + j, key kb 16 + l16.
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dss[(rb * 16 + 4 * g4 + j) * TP + kb * 16 + l16] = from_f32<T>(dsv[j]);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NDB; ++i) dq[i] = mma_lds<T>(dss + rb2 * 16 * TP, TP, kt + (db0 + i) * 16 * TP, TP, dq[i]);
+    }
+    T* dqp = static_cast<T*>(p.dq) + b * p.dqs[0] + h * p.dqs[1];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) {
+        const int d = (db0 + i) * 16 + l16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = r0 + rb2 * 16 + 4 * g4 + j;
+            if (row < p.seq_q) dqp[static_cast<int64_t>(row) * p.dqs[2] + d] = from_f32<T>(dq[i][j] * p.scale);
+        }
+    }
+}
+
+const char* check_bwd(const kmi_attn_bwd_args* a) {
+    if (!a) return "null args";
+    if (a->dtype != KMI_BF16 && a->dtype != KMI_F16) return "dtype must be BF16 or F16";
+    if (a->head_dim != 64 && a->head_dim != 128) return "head_dim must be 64 or 128";
+    if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seq_q <= 0 || a->seq_k <= 0)
+        return "sizes must be positive";
+    if (a->heads_q % a->heads_kv != 0) return "heads_kv must divide heads_q";
+    if (a->batch * a->heads_q * a->seq_q > (int64_t{1} << 31) || a->seq_q > (1 << 30) || a->seq_k > (1 << 30))
+        return "sizes too large";
+    const void* ptrs[] = {a->q, a->k, a->v, a->out, a->grad_out, a->lse, a->grad_q, a->grad_k, a->grad_v};
+    for (const void* ptr : ptrs)
+        if (!ptr) return "null tensor pointer";
+    const void* vec[] = {a->q, a->k, a->v, a->grad_out};
+    for (const void* ptr : vec)
+        if (reinterpret_cast<uintptr_t>(ptr) % 16) return "q, k, v and grad_out must be 16-byte aligned";
+    const int64_t* strides[] = {a->q_stride, a->k_stride, a->v_stride, a->do_stride};
+    for (const int64_t* s : strides)
+        for (int i = 0; i < 3; ++i)
+            if (s[i] < 0 || s[i] % 8) return "q, k, v and grad_out strides must be non-negative multiples of 8";
+    return nullptr;
+}
+
+// Row dot products (padded to 16 bytes), then with GQA the dK / dV partials.
+size_t bwd_ws_bytes(const kmi_attn_bwd_args* a) {
+    size_t floats = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
+    if (a->heads_q != a->heads_kv) floats += 2 * static_cast<size_t>(a->batch * a->heads_q * a->seq_k * a->head_dim);
+    return floats * sizeof(float);
+}
+
+template <typename T, int D>
+hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
+    const int64_t rows = static_cast<int64_t>(p.batch) * p.hq * p.seq_q;
+    hipLaunchKernelGGL((attn_bwd_pre<T, D>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, s, p);
+    const int64_t ntk = ceil_div(p.seq_k, BT), nqb = ceil_div(p.seq_q, BT);
+    hipLaunchKernelGGL((attn_bwd_dkdv<T, D>), dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk)),
+                       dim3(BWD_THREADS), 0, s, p);
+    if (p.pdk) {
+        const int64_t items = static_cast<int64_t>(p.batch) * p.hkv * p.seq_k * (D / 4);
+        hipLaunchKernelGGL((attn_bwd_group_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0,
+                           s, p);
+    }
+    hipLaunchKernelGGL((attn_bwd_dq<T, D>), dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb)),
+                       dim3(BWD_THREADS), 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace kmi
+
+extern "C" int kmi_attn_bwd_workspace_bytes(const kmi_attn_bwd_args* a, size_t* bytes) {
+    using namespace kmi;
+    if (!bytes) return fail(KMI_EINVAL, "kmi_attn_bwd_workspace_bytes: null bytes");
+    if (const char* why = check_bwd(a)) return fail(KMI_EINVAL, std::string("kmi_attn_bwd_workspace_bytes: ") + why);
+    *bytes = bwd_ws_bytes(a);
+    return KMI_OK;
+}
+
+extern "C" int kmi_attn_bwd(const kmi_attn_bwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+    using namespace kmi;
+    if (const char* why = check_bwd(a)) return fail(KMI_EINVAL, std::string("kmi_attn_bwd: ") + why);
+    const size_t need = bwd_ws_bytes(a);
+    if (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16)
+        return fail(KMI_EWORKSPACE, "kmi_attn_bwd: workspace missing or smaller than kmi_attn_bwd_workspace_bytes");
+    BwdParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->out;
+    p.dout = a->grad_out;
+    p.lse = a->lse;
+    p.dq = a->grad_q;
+    p.dk = a->grad_k;
+    p.dv = a->grad_v;
+    p.dr = static_cast<float*>(workspace);
+    if (a->heads_q != a->heads_kv) {
+        // Partials start 16-byte aligned after the row dot products.
+        const size_t dr_floats = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
+        const size_t part = static_cast<size_t>(a->batch * a->heads_q * a->seq_k * a->head_dim);
+        p.pdk = p.dr + dr_floats;
+        p.pdv = p.pdk + part;
+    }
+    for (int i = 0; i < 3; ++i) {
+        p.qs[i] = a->q_stride[i];
+        p.ks[i] = a->k_stride[i];
+        p.vs[i] = a->v_stride[i];
+        p.os[i] = a->o_stride[i];
+        p.dos[i] = a->do_stride[i];
+        p.dqs[i] = a->dq_stride[i];
+        p.dks[i] = a->dk_stride[i];
+        p.dvs[i] = a->dv_stride[i];
+        p.ls[i] = a->lse_stride[i];
+    }
+    p.batch = static_cast<int>(a->batch);
+    p.hq = static_cast<int>(a->heads_q);
+    p.hkv = static_cast<int>(a->heads_kv);
+    p.group = p.hq / p.hkv;
+    p.seq_q = static_cast<int>(a->seq_q);
+    p.seq_k = static_cast<int>(a->seq_k);
+    p.causal = a->causal ? 1 : 0;
+    p.scale = static_cast<float>(a->scale);
+    p.c2 = static_cast<float>(a->scale * 1.4426950408889634);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t err;
+    if (a->dtype == KMI_BF16)
+        err = a->head_dim == 64 ? launch_bwd<bf16, 64>(p, s) : launch_bwd<bf16, 128>(p, s);
+    else
+        err = a->head_dim == 64 ? launch_bwd<f16, 64>(p, s) : launch_bwd<f16, 128>(p, s);
+    return hip_status(err, "kmi_attn_bwd");
+}

@@ -51,7 +51,7 @@ std::atomic<bool> g_norms{env_on("KMI_NORMS")};
 // KMI_PITCHED_OUT=0 (read at load) keeps the attention output dense for head-view inputs.
 const bool g_pitched_out = env_on("KMI_PITCHED_OUT");
 // Calls the kernels took, per family (ktt::counters).
-std::atomic<int64_t> g_attn_calls{0}, g_norm_calls{0}, g_attn_declined{0};
+std::atomic<int64_t> g_attn_calls{0}, g_norm_calls{0}, g_attn_declined{0}, g_attn_bwd_calls{0};
 
 void check(int status, const char* what) {
     TORCH_CHECK(status == KMI_OK, "kohakutt_amd: ", what, " failed (", status, "): ", kmi_last_error());
@@ -242,11 +242,91 @@ SdpaResult sdpa_overrideable(const Tensor& q, const Tensor& k, const Tensor& v, 
         g_attn_declined.fetch_add(1);
         out = std::get<0>(at::_scaled_dot_product_attention_math(q, k, v, attn_bias, dropout_p, is_causal,
                                                                   std::nullopt, scale, q.size(1) != k.size(1)));
-        lse = at::empty({q.size(0), q.size(1), sq}, q.options().dtype(at::kFloat));
+        // No statistics off the kernels: a broadcast (stride 0) placeholder of the right
+        // shape, which the backward recognises (kernel-written lse is contiguous).
+        lse = at::empty({1}, q.options().dtype(at::kFloat)).expand({q.size(0), q.size(1), sq});
     }
     auto seed = at::empty({}, at::dtype(at::kLong));
     auto offset = at::empty({}, at::dtype(at::kLong));
     return {out, lse, Tensor(), Tensor(), c10::SymInt(sq), c10::SymInt(sk), seed, offset, Tensor()};
+}
+
+// The flash backward (kmi_attn_bwd) takes unmasked calls whose forward ran the kernels:
+// their lse is a contiguous fp32 [B, H, Sq] (a declined forward leaves a stride-0 one).
+bool flash_backward_takes(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& attn_bias,
+                          const Tensor& out, const Tensor& lse, const Tensor& grad_out) {
+    if (!g_attention.load() || attn_bias.defined() || !lse.defined()) return false;
+    const auto st = q.scalar_type();
+    if (!(st == at::kBFloat16 || st == at::kHalf) || k.scalar_type() != st || v.scalar_type() != st ||
+        grad_out.scalar_type() != st || out.scalar_type() != st)
+        return false;
+    if (q.dim() != 4 || k.dim() != 4 || v.dim() != 4 || !q.is_cuda()) return false;
+    const int64_t d = q.size(3);
+    if ((d != 64 && d != 128) || k.size(3) != d || v.size(3) != d || q.size(1) % k.size(1) != 0) return false;
+    return lse.scalar_type() == at::kFloat && lse.dim() == 3 && lse.size(0) == q.size(0) &&
+           lse.size(1) == q.size(1) && lse.size(2) == q.size(2) && lse.stride(2) == 1 && lse.stride(1) >= q.size(2);
+}
+
+std::tuple<Tensor, Tensor, Tensor> flash_backward(const Tensor& grad_out_in, const Tensor& q_in, const Tensor& k_in,
+                                                  const Tensor& v_in, const Tensor& out_in, const Tensor& lse,
+                                                  bool is_causal, optional<double> scale) {
+    const Tensor q = kernel_operand(q_in, 2), k = kernel_operand(k_in, 2), v = kernel_operand(v_in, 2);
+    const Tensor go = kernel_operand(grad_out_in, 2);
+    const Tensor o = out_in.stride(3) == 1 ? out_in : out_in.contiguous();
+    const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3), Hk = k.size(1), Sk = k.size(2);
+    Tensor dq = at::empty({B, H, Sq, D}, q.options());
+    Tensor dk = at::empty({B, Hk, Sk, D}, k.options());
+    Tensor dv = at::empty({B, Hk, Sk, D}, v.options());
+    kmi_attn_bwd_args a{};
+    a.q = q.data_ptr();
+    a.k = k.data_ptr();
+    a.v = v.data_ptr();
+    a.out = o.data_ptr();
+    a.grad_out = go.data_ptr();
+    a.lse = lse.data_ptr<float>();
+    a.grad_q = dq.data_ptr();
+    a.grad_k = dk.data_ptr();
+    a.grad_v = dv.data_ptr();
+    a.dtype = code_of(q.scalar_type());
+    a.causal = is_causal ? 1 : 0;
+    a.batch = B;
+    a.heads_q = H;
+    a.heads_kv = Hk;
+    a.seq_q = Sq;
+    a.seq_k = Sk;
+    a.head_dim = D;
+    for (int i = 0; i < 3; ++i) {
+        a.q_stride[i] = q.stride(i);
+        a.k_stride[i] = k.stride(i);
+        a.v_stride[i] = v.stride(i);
+        a.o_stride[i] = o.stride(i);
+        a.do_stride[i] = go.stride(i);
+        a.dq_stride[i] = dq.stride(i);
+        a.dk_stride[i] = dk.stride(i);
+        a.dv_stride[i] = dv.stride(i);
+        a.lse_stride[i] = lse.stride(i);
+    }
+    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
+    size_t ws = 0;
+    check(kmi_attn_bwd_workspace_bytes(&a, &ws), "kmi_attn_bwd_workspace_bytes");
+    Tensor work = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
+    check(kmi_attn_bwd(&a, work.data_ptr(), ws, stream_of(q)), "kmi_attn_bwd");
+    g_attn_bwd_calls.fetch_add(1);
+    return {dq, dk, dv};
+}
+
+// ktt::_sdpa_flash_backward(grad, q, k, v, out, lse, is_causal, scale): the flash
+// backward called directly (what the overrideable backward runs for unmasked calls).
+std::tuple<Tensor, Tensor, Tensor> sdpa_flash_backward_op(const Tensor& grad, const Tensor& q, const Tensor& k,
+                                                          const Tensor& v, const Tensor& out, const Tensor& lse,
+                                                          bool is_causal, optional<double> scale) {
+    TORCH_CHECK(flash_backward_takes(q, k, v, Tensor(), out, lse, grad),
+                "kohakutt_amd: _sdpa_flash_backward needs bf16 / fp16 [B, H, S, D] GPU tensors of one dtype, "
+                "head dim 64 or 128, K/V heads dividing Q heads and the forward's contiguous fp32 lse [B, H, Sq]");
+    TORCH_CHECK(grad.sizes() == q.sizes() && out.sizes() == q.sizes(),
+                "kohakutt_amd: _sdpa_flash_backward grad and out must be shaped as q");
+    c10::DeviceGuard guard(q.device());
+    return flash_backward(grad, q, k, v, out, lse, is_causal, scale);
 }
 
 // The math backward of the overrideable op, in fp32 (the reference's
@@ -257,10 +337,15 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> sdpa_overrideable_backward(
     std::array<bool, 4> grad_input_mask, const Tensor& out, const Tensor& logsumexp, const Tensor& cum_seq_q,
     const Tensor& cum_seq_k, c10::SymInt max_q, c10::SymInt max_k, double dropout_p, bool is_causal,
     const Tensor& philox_seed, const Tensor& philox_offset, optional<double> scale) {
-    (void)out, (void)logsumexp, (void)cum_seq_q, (void)cum_seq_k, (void)max_q, (void)max_k;
+    (void)cum_seq_q, (void)cum_seq_k, (void)max_q, (void)max_k;
     (void)philox_seed, (void)philox_offset;
     TORCH_CHECK(dropout_p == 0.0, "kohakutt_amd: attention backward takes no dropout");
     c10::DeviceGuard guard(q.device());
+    if (flash_backward_takes(q, k, v, attn_bias, out, logsumexp, grad_out)) {
+        auto g = flash_backward(grad_out, q, k, v, out, logsumexp, is_causal, scale);
+        return {grad_input_mask[0] ? std::get<0>(g) : Tensor(), grad_input_mask[1] ? std::get<1>(g) : Tensor(),
+                grad_input_mask[2] ? std::get<2>(g) : Tensor(), Tensor()};
+    }
     const int64_t H = q.size(1), Hk = k.size(1), Sq = q.size(2), Sk = k.size(2), D = q.size(3);
     const int64_t G = H / Hk;
     const double s = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
@@ -677,10 +762,11 @@ void set_enabled(bool attention, bool norms) {
 
 std::vector<int64_t> counters() {
     return {g_attn_calls.load(), g_attn_declined.load(), g_norm_calls.load(),
-            g_attention.load() ? 1 : 0, g_norms.load() ? 1 : 0};
+            g_attention.load() ? 1 : 0, g_norms.load() ? 1 : 0, g_attn_bwd_calls.load()};
 }
 
 void reset_counters() {
+    g_attn_bwd_calls.store(0);
     g_attn_calls.store(0);
     g_attn_declined.store(0);
     g_norm_calls.store(0);
@@ -703,6 +789,8 @@ TORCH_LIBRARY(ktt, m) {
           TORCH_FN(kta::sdpa_refusal_op));
     m.def("_set_enabled(bool attention, bool norms) -> ()", TORCH_FN(kta::set_enabled));
     m.def("counters() -> int[]", TORCH_FN(kta::counters));
+    m.def("_sdpa_flash_backward(Tensor grad, Tensor q, Tensor k, Tensor v, Tensor out, Tensor lse, "
+          "bool is_causal, float? scale=None) -> (Tensor, Tensor, Tensor)");
     m.def("_sdpa_lengths_supported(Tensor q, Tensor k, Tensor v, bool is_causal, bool stats) -> bool");
     m.def("_sdpa_lengths(Tensor q, Tensor k, Tensor v, Tensor lengths, bool is_causal, float? scale, bool stats) "
           "-> Tensor");
@@ -714,6 +802,7 @@ TORCH_LIBRARY(ktt, m) {
 TORCH_LIBRARY_IMPL(ktt, CUDA, m) {
     m.impl("rms_norm", TORCH_FN(kta::ktt_rms_norm_cuda));
     m.impl("_sdpa_varlen", TORCH_FN(kta::sdpa_varlen));
+    m.impl("_sdpa_flash_backward", TORCH_FN(kta::sdpa_flash_backward_op));
     m.impl("_sdpa_lengths", TORCH_FN(kta::sdpa_lengths));
     m.impl("_sdpa_lengths_supported", TORCH_FN(kta::sdpa_lengths_supported));
     m.impl("_sdpa_lengths_backward", TORCH_FN(kta::sdpa_lengths_backward));

@@ -71,6 +71,7 @@ def counters() -> dict:
         "norms": c[2],
         "attention_enabled": bool(c[3]),
         "norms_enabled": bool(c[4]),
+        "attention_backward": c[5],
     }
 
 

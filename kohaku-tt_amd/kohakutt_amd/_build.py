@@ -30,7 +30,7 @@ ARCH = "gfx950"
 CAPI_LIB = PKG / "libkohakutt_amd.so"
 OPS_LIB = PKG / "_torch_ops.so"
 
-HIP_SOURCES = ["capi.hip", "norm.hip", "attention.hip"]
+HIP_SOURCES = ["capi.hip", "norm.hip", "attention.hip", "attention_bwd.hip"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

@@ -20,6 +20,8 @@ KMI_MASK_NONE, KMI_MASK_STRIDED, KMI_MASK_PACKED = 0, 1, 2
 EXPORTS = (
     "kmi_attn_workspace_bytes",
     "kmi_attn_fwd",
+    "kmi_attn_bwd_workspace_bytes",
+    "kmi_attn_bwd",
     "kmi_layer_norm_fwd",
     "kmi_rms_norm_fwd",
     "kmi_last_error",
@@ -68,6 +70,40 @@ class AttnArgs(ctypes.Structure):
     ]
 
 
+class AttnBwdArgs(ctypes.Structure):
+    """``kmi_attn_bwd_args``, field for field."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("grad_out", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("grad_q", ctypes.c_void_p),
+        ("grad_k", ctypes.c_void_p),
+        ("grad_v", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("heads_q", ctypes.c_int64),
+        ("heads_kv", ctypes.c_int64),
+        ("seq_q", ctypes.c_int64),
+        ("seq_k", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("q_stride", _I64x3),
+        ("k_stride", _I64x3),
+        ("v_stride", _I64x3),
+        ("o_stride", _I64x3),
+        ("do_stride", _I64x3),
+        ("dq_stride", _I64x3),
+        ("dk_stride", _I64x3),
+        ("dv_stride", _I64x3),
+        ("lse_stride", _I64x3),
+        ("scale", ctypes.c_double),
+    ]
+
+
 class KmiError(RuntimeError):
     def __init__(self, status, message):
         super().__init__(f"kmi status {status}: {message}")
@@ -87,6 +123,8 @@ def lib():
         vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
         h.kmi_attn_workspace_bytes.argtypes = [ctypes.POINTER(AttnArgs), ctypes.POINTER(ctypes.c_size_t)]
         h.kmi_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), vp, ctypes.c_size_t, vp]
+        h.kmi_attn_bwd_workspace_bytes.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.POINTER(ctypes.c_size_t)]
+        h.kmi_attn_bwd.argtypes = [ctypes.POINTER(AttnBwdArgs), vp, ctypes.c_size_t, vp]
         h.kmi_layer_norm_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, ctypes.c_double, vp]
         h.kmi_rms_norm_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, ctypes.c_double, vp]
         h.kmi_last_error.restype = ctypes.c_char_p

@@ -37,10 +37,11 @@ def test_abi_version_matches_header():
     assert capi.lib().kmi_abi_version() == int(m.group(1))
 
 
-def test_struct_layout_matches_header_field_order():
+@pytest.mark.parametrize("struct,cls", [("kmi_attn_args", "AttnArgs"), ("kmi_attn_bwd_args", "AttnBwdArgs")])
+def test_struct_layout_matches_header_field_order(struct, cls):
     text = HEADER.read_text()
-    start = text.index("{", text.index("typedef struct kmi_attn_args")) + 1
-    body = text[start : text.index("} kmi_attn_args;")]
+    start = text.index("{", text.index("typedef struct " + struct)) + 1
+    body = text[start : text.index("} " + struct + ";")]
     body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
     names = []
     for decl in body.split(";"):
@@ -48,7 +49,7 @@ def test_struct_layout_matches_header_field_order():
             idents = re.findall(r"[A-Za-z_]\w*", re.sub(r"\[.*?\]", "", part))
             if idents:
                 names.append(idents[-1])
-    assert names == [f[0] for f in capi.AttnArgs._fields_]
+    assert names == [f[0] for f in getattr(capi, cls)._fields_]
 
 
 def _args(**kw):
@@ -122,3 +123,19 @@ def test_norms_reject_malformed_calls():
                                   None) == capi.KMI_EINVAL
     # zero rows: nothing to do, nothing launched
     assert lib.kmi_rms_norm_fwd(None, None, None, None, None, 0, 64, capi.KMI_BF16, 0, 0, 1e-6, None) == capi.KMI_OK
+
+
+def test_backward_rejects_malformed_calls_before_launch():
+    a = capi.AttnBwdArgs()
+    assert capi.lib().kmi_attn_bwd(ctypes.byref(a), None, 0, None) == capi.KMI_EINVAL
+    a.q = a.k = a.v = a.out = a.grad_out = a.lse = a.grad_q = a.grad_k = a.grad_v = 0x1000
+    a.dtype = capi.KMI_BF16
+    a.batch, a.heads_q, a.heads_kv, a.seq_q, a.seq_k, a.head_dim = 1, 4, 3, 8, 8, 64
+    assert capi.lib().kmi_attn_bwd(ctypes.byref(a), None, 0, None) == capi.KMI_EINVAL
+    assert "heads_kv must divide" in capi.lib().kmi_last_error().decode()
+    a.heads_kv = 2
+    n = ctypes.c_size_t()
+    assert capi.lib().kmi_attn_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == capi.KMI_OK
+    # fp32 row dot products, then (GQA) the dK / dV partials of every query head.
+    assert n.value == (4 * 8 + 2 * 4 * 8 * 64) * 4
+    assert capi.lib().kmi_attn_bwd(ctypes.byref(a), None, 0, None) == capi.KMI_EWORKSPACE
