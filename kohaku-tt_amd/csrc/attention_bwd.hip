@@ -91,6 +91,42 @@ __device__ __forceinline__ void stage(const T* src, int64_t rs, int r0, int nrow
     }
 }
 
+// The same staging split in two: loads of rows [r0, r0 + 32) into registers (D / 64
+// 16-byte chunks per thread, zeros past the end), issued a tile ahead, and their LDS stores.
+template <int D>
+struct TileRegs {
+    u32x4 v[D / 64];
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int nrows, TileRegs<D>& t) {
+    constexpr int CH = D / 8;
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) {
+        const int c = threadIdx.x + BWD_THREADS * j;
+        const int r = c / CH, ch = c - r * CH;
+        const int row = min(r0 + r, nrows - 1);  // in range; rows past the end are dropped below
+        const u32x4 val = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(row) * rs + 8 * ch);
+        t.v[j] = r0 + r < nrows ? val : u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void store_regs(const TileRegs<D>& t, T* dst, T* dstT) {
+    constexpr int CH = D / 8;
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) {
+        const int c = threadIdx.x + BWD_THREADS * j;
+        const int r = c / CH, ch = c - r * CH;
+        *reinterpret_cast<u32x4*>(dst + r * (D + 8) + 8 * ch) = t.v[j];
+        if (dstT) {
+            const auto e = __builtin_bit_cast(typename BwdMfma<T>::v8, t.v[j]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dstT[(8 * ch + i) * TP + r] = e[i];
+        }
+    }
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_pre(const BwdParams p) {
     const int lane = threadIdx.x & 63;
@@ -185,13 +221,24 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
 
     // Causal (top-left): a query block sees this tile only if its last position reaches k0.
     const int rstart = p.causal ? (k0 / BT) * BT : 0;
+    const T* qbase = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1];
+    const T* dobase = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1];
+    TileRegs<D> qr, dor;
+    if (rstart < p.seq_q) {
+        load_regs<T, D>(qbase, p.qs[2], rstart, p.seq_q, qr);
+        load_regs<T, D>(dobase, p.dos[2], rstart, p.seq_q, dor);
+    }
     {
         for (int r0 = rstart; r0 < p.seq_q; r0 += BT) {
             __syncthreads();  // the previous block's LDS reads are done
-            stage<T, D>(static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1], p.qs[2], r0, p.seq_q, qs, qt);
-            stage<T, D>(static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1], p.dos[2], r0, p.seq_q, dos, dot);
+            store_regs<T, D>(qr, qs, qt);
+            store_regs<T, D>(dor, dos, dot);
             stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
             __syncthreads();
+            if (r0 + BT < p.seq_q) {  // the next block's loads overlap this block's products
+                load_regs<T, D>(qbase, p.qs[2], r0 + BT, p.seq_q, qr);
+                load_regs<T, D>(dobase, p.dos[2], r0 + BT, p.seq_q, dor);
+            }
             float pv[4], dsv[4];
             p_ds<T, D>(p, qs, dos, ks, vs, lse2, drs, rb, kb, r0, k0, pv, dsv);
             // Transposed stores: key row kb 16 + l16, rows rb 16 + 4 g4 .. + 3.
@@ -306,11 +353,18 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int kend = p.causal ? min(p.seq_k, r0 + BT) : p.seq_k;
     const T* kbase = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
     const T* vbase = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
+    TileRegs<D> kr, vr;
+    load_regs<T, D>(kbase, p.ks[2], 0, p.seq_k, kr);
+    load_regs<T, D>(vbase, p.vs[2], 0, p.seq_k, vr);
     for (int k0 = 0; k0 < kend; k0 += BT) {
         __syncthreads();
-        stage<T, D>(kbase, p.ks[2], k0, p.seq_k, ks, kt);
-        stage<T, D>(vbase, p.vs[2], k0, p.seq_k, vs, nullptr);
+        store_regs<T, D>(kr, ks, kt);
+        store_regs<T, D>(vr, vs, nullptr);
         __syncthreads();
+        if (k0 + BT < kend) {  // the next tile's loads overlap this tile's products
+            load_regs<T, D>(kbase, p.ks[2], k0 + BT, p.seq_k, kr);
+            load_regs<T, D>(vbase, p.vs[2], k0 + BT, p.seq_k, vr);
+        }
         float pv[4], dsv[4];
         p_ds<T, D>(p, qs, dos, ks, vs, lse2, drs, rb, kb, r0, k0, pv, dsv);
         (void)pv;
