@@ -7,7 +7,7 @@
 // or 128, bf16 / fp16):
 //
 //   attn_bwd_pre     Dr[row] = sum_d dO[row, d] * O[row, d]   (fp32)
-//   attn_bwd_dkdv    one workgroup per (sequence, query head, 32-key tile): for every
+//   attn_bwd_dkdv    one workgroup per (sequence, query head, 64-key tile): for every
 //                    32-row query block that sees the tile, P = exp2(c S - lse2),
 //                    dP = dO V^T, dS = P (dP - Dr); dV += P^T dO, dK += dS^T Q (fp32
 //                    accumulators in registers).  Without GQA it writes dK / dV; with GQA
@@ -184,40 +184,58 @@ __device__ __forceinline__ void stage_rows_stats(const BwdParams& p, int b, int 
     }
 }
 
+// dK / dV: a workgroup takes KW keys, wavefront w owns keys [k0 + 16 w, + 16) with its K
+// and V fragments in registers (the A operands of S^T = K Q^T and dP^T = V dO^T).  Per
+// 32-row query block the workgroup stages Q and dO (row-major and transposed) once; each
+// wavefront then forms P^T and dS^T of its keys, passes them through its own LDS rows (one
+// wavefront's LDS accesses stay in order: no barrier) and accumulates dV += P^T dO and
+// dK += dS^T Q.  Two barriers per query block.
+constexpr int KW = 64;
+
 template <typename T, int D>
 __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) {
+    typedef typename BwdMfma<T>::v8 v8;
     constexpr int RP = D + 8;
-    __shared__ __align__(16) T ks[BT * RP];
-    __shared__ __align__(16) T vs[BT * RP];
+    constexpr int DC = D / 32, DB = D / 16;
     __shared__ __align__(16) T qs[BT * RP];
     __shared__ __align__(16) T dos[BT * RP];
     __shared__ __align__(16) T qt[D * TP];
     __shared__ __align__(16) T dot[D * TP];
-    __shared__ __align__(16) T pt[BT * TP];
-    __shared__ __align__(16) T dst[BT * TP];
+    __shared__ __align__(16) T pt[4 * 16 * TP];   // per wavefront: P^T [16 keys][32 rows]
+    __shared__ __align__(16) T dst[4 * 16 * TP];  // per wavefront: dS^T
     __shared__ float lse2[BT], drs[BT];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4, l16 = lane & 15;
-    const int ntk = (p.seq_k + BT - 1) / BT;
+    const int ntk = (p.seq_k + KW - 1) / KW;
     const int tile = blockIdx.x % ntk;
     const int bh = blockIdx.x / ntk;  // (sequence, query head)
     const int b = bh / p.hq, h = bh - b * p.hq;
     const int kvh = h / p.group;
-    const int k0 = tile * BT;
+    const int k0 = tile * KW;
+    const int kw0 = k0 + 16 * wave;  // this wavefront's first key
 
-    stage<T, D>(static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1], p.ks[2], k0, p.seq_k, ks, nullptr);
-    stage<T, D>(static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1], p.vs[2], k0, p.seq_k, vs, nullptr);
-
-    // Wave w: P / dS block (rows rb, keys kb); dK / dV blocks keys kb2, dims db0 + i.
-    const int rb = wave >> 1, kb = wave & 1;
-    const int kb2 = wave & 1;
-    constexpr int NDB = D / 32;
-    const int db0 = (wave >> 1) * NDB;
-    f32x4 dk[NDB], dv[NDB];
+    // K / V fragments: lane (g4, l16) holds key kw0 + l16, dims 32 c + 8 g4 .. + 7.
+    v8 kf[DC], vf[DC];
+    {
+        const int key = kw0 + l16;
+        const int kc = min(key, p.seq_k - 1);
+        const T* kp = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1] + static_cast<int64_t>(kc) * p.ks[2];
+        const T* vp = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1] + static_cast<int64_t>(kc) * p.vs[2];
 #pragma unroll
-    for (int i = 0; i < NDB; ++i) dk[i] = dv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < DC; ++c) {
+            const u32x4 kx = *reinterpret_cast<const u32x4*>(kp + 32 * c + 8 * g4);
+            const u32x4 vx = *reinterpret_cast<const u32x4*>(vp + 32 * c + 8 * g4);
+            kf[c] = __builtin_bit_cast(v8, key < p.seq_k ? kx : u32x4{0u, 0u, 0u, 0u});
+            vf[c] = __builtin_bit_cast(v8, key < p.seq_k ? vx : u32x4{0u, 0u, 0u, 0u});
+        }
+    }
+    f32x4 dk[DB], dv[DB];
+#pragma unroll
+    for (int i = 0; i < DB; ++i) dk[i] = dv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    T* ptw = pt + wave * 16 * TP;
+    T* dsw = dst + wave * 16 * TP;
 
     // Causal (top-left): a query block sees this tile only if its last position reaches k0.
     const int rstart = p.causal ? (k0 / BT) * BT : 0;
@@ -228,48 +246,66 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         load_regs<T, D>(qbase, p.qs[2], rstart, p.seq_q, qr);
         load_regs<T, D>(dobase, p.dos[2], rstart, p.seq_q, dor);
     }
-    {
-        for (int r0 = rstart; r0 < p.seq_q; r0 += BT) {
-            __syncthreads();  // the previous block's LDS reads are done
-            store_regs<T, D>(qr, qs, qt);
-            store_regs<T, D>(dor, dos, dot);
-            stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
-            __syncthreads();
-            if (r0 + BT < p.seq_q) {  // the next block's loads overlap this block's products
-                load_regs<T, D>(qbase, p.qs[2], r0 + BT, p.seq_q, qr);
-                load_regs<T, D>(dobase, p.dos[2], r0 + BT, p.seq_q, dor);
+    for (int r0 = rstart; r0 < p.seq_q; r0 += BT) {
+        __syncthreads();  // the previous block's LDS reads are done
+        store_regs<T, D>(qr, qs, qt);
+        store_regs<T, D>(dor, dos, dot);
+        stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
+        __syncthreads();
+        if (r0 + BT < p.seq_q) {  // the next block's loads overlap this block's products
+            load_regs<T, D>(qbase, p.qs[2], r0 + BT, p.seq_q, qr);
+            load_regs<T, D>(dobase, p.dos[2], r0 + BT, p.seq_q, dor);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            // S^T and dP^T of this wavefront's 16 keys x rows rb 16 .. + 15: lane (g4, l16)
+            // gets keys 4 g4 + j, row l16.
+            f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f}, dpt = st;
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                const v8 qb = *reinterpret_cast<const v8*>(qs + (rb * 16 + l16) * RP + 32 * c + 8 * g4);
+                const v8 ob = *reinterpret_cast<const v8*>(dos + (rb * 16 + l16) * RP + 32 * c + 8 * g4);
+                st = BwdMfma<T>::run(kf[c], qb, st);
+                dpt = BwdMfma<T>::run(vf[c], ob, dpt);
             }
-            float pv[4], dsv[4];
-            p_ds<T, D>(p, qs, dos, ks, vs, lse2, drs, rb, kb, r0, k0, pv, dsv);
-            // Transposed stores: key row kb 16 + l16, rows rb 16 + 4 g4 .. + 3.
-            T* pw = pt + (kb * 16 + l16) * TP + rb * 16 + 4 * g4;
-            T* dw = dst + (kb * 16 + l16) * TP + rb * 16 + 4 * g4;
+            const int rl = rb * 16 + l16;
+            const int pos = r0 + rl;
+            const float l2 = lse2[rl], dr = drs[rl];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                pw[j] = from_f32<T>(pv[j]);
-                dw[j] = from_f32<T>(dsv[j]);
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < NDB; ++i) {
-                const int db = db0 + i;
-                dv[i] = mma_lds<T>(pt + kb2 * 16 * TP, TP, dot + db * 16 * TP, TP, dv[i]);
-                dk[i] = mma_lds<T>(dst + kb2 * 16 * TP, TP, qt + db * 16 * TP, TP, dk[i]);
+                const int key = kw0 + 4 * g4 + j;
+                const bool keep = key < p.seq_k && (!p.causal || key <= pos);
+                // Rows past the end carry lse2 = +inf: their P is exactly 0.
+                const float e = keep ? __builtin_amdgcn_exp2f(st[j] * p.c2 - l2) : 0.f;
+                ptw[(4 * g4 + j) * TP + rl] = from_f32<T>(e);
+                dsw[(4 * g4 + j) * TP + rl] = from_f32<T>(e * (dpt[j] - dr));
             }
         }
+        // The compiler keeps these LDS reads after the stores above (same arrays); the
+        // hardware runs one wavefront's LDS accesses in order.
+        __asm__ volatile("" ::: "memory");
+        const v8 pa = *reinterpret_cast<const v8*>(ptw + l16 * TP + 8 * g4);
+        const v8 sa = *reinterpret_cast<const v8*>(dsw + l16 * TP + 8 * g4);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const v8 ob = *reinterpret_cast<const v8*>(dot + (db * 16 + l16) * TP + 8 * g4);
+            const v8 qb = *reinterpret_cast<const v8*>(qt + (db * 16 + l16) * TP + 8 * g4);
+            dv[db] = BwdMfma<T>::run(pa, ob, dv[db]);
+            dk[db] = BwdMfma<T>::run(sa, qb, dk[db]);
+        }
     }
-    // Lane (g4, l16) of block (kb2, db) holds keys kb2 16 + 4 g4 + j, dim db 16 + l16.
+    // Lane (g4, l16) of block db holds keys kw0 + 4 g4 + j, dim db 16 + l16.
     if (p.pdk) {
         const int64_t base = (static_cast<int64_t>(b) * p.hq + h) * p.seq_k;
 #pragma unroll
-        for (int i = 0; i < NDB; ++i) {
-            const int d = (db0 + i) * 16 + l16;
+        for (int db = 0; db < DB; ++db) {
+            const int d = db * 16 + l16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int key = k0 + kb2 * 16 + 4 * g4 + j;
+                const int key = kw0 + 4 * g4 + j;
                 if (key < p.seq_k) {
-                    p.pdk[(base + key) * D + d] = dk[i][j] * p.scale;
-                    p.pdv[(base + key) * D + d] = dv[i][j];
+                    p.pdk[(base + key) * D + d] = dk[db][j] * p.scale;
+                    p.pdv[(base + key) * D + d] = dv[db][j];
                 }
             }
         }
@@ -278,14 +314,14 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     T* dkp = static_cast<T*>(p.dk) + b * p.dks[0] + kvh * p.dks[1];
     T* dvp = static_cast<T*>(p.dv) + b * p.dvs[0] + kvh * p.dvs[1];
 #pragma unroll
-    for (int i = 0; i < NDB; ++i) {
-        const int d = (db0 + i) * 16 + l16;
+    for (int db = 0; db < DB; ++db) {
+        const int d = db * 16 + l16;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int key = k0 + kb2 * 16 + 4 * g4 + j;
+            const int key = kw0 + 4 * g4 + j;
             if (key < p.seq_k) {
-                dkp[static_cast<int64_t>(key) * p.dks[2] + d] = from_f32<T>(dk[i][j] * p.scale);
-                dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[i][j]);
+                dkp[static_cast<int64_t>(key) * p.dks[2] + d] = from_f32<T>(dk[db][j] * p.scale);
+                dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[db][j]);
             }
         }
     }
@@ -420,7 +456,7 @@ template <typename T, int D>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
     const int64_t rows = static_cast<int64_t>(p.batch) * p.hq * p.seq_q;
     hipLaunchKernelGGL((attn_bwd_pre<T, D>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, s, p);
-    const int64_t ntk = ceil_div(p.seq_k, BT), nqb = ceil_div(p.seq_q, BT);
+    const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, BT);
     hipLaunchKernelGGL((attn_bwd_dkdv<T, D>), dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk)),
                        dim3(BWD_THREADS), 0, s, p);
     if (p.pdk) {
