@@ -13,7 +13,7 @@
 //                    accumulators in registers).  Without GQA it writes dK / dV; with GQA
 //                    fp32 per-query-head partials that
 //   attn_bwd_group_sum sums over each K/V head's query heads in a fixed order (no atomics)
-//   attn_bwd_dq      one workgroup per (sequence, query head, 32-row block): over the key
+//   attn_bwd_dq      one workgroup per (sequence, query head, 64-row block): over the key
 //                    tiles it sees, the same P / dS, dQ += dS K
 //
 // S = Q K^T, dP = dO V^T and the three gradient products run on
@@ -60,39 +60,10 @@ struct BwdParams {
     float scale, c2;  // c2 = scale * log2(e)
 };
 
-// One 16x16 output block, k = 32: A rows at a (pitch ap), B columns at b (pitch bp),
-// both contiguous along k.  Lane (g4, l16) reads A[l16][8 g4 ..] and B[l16][8 g4 ..].
-template <typename T>
-__device__ __forceinline__ f32x4 mma_lds(const T* a, int ap, const T* b, int bp, f32x4 acc) {
-    typedef typename BwdMfma<T>::v8 v8;
-    const int lane = threadIdx.x & 63;
-    const int g4 = lane >> 4, l16 = lane & 15;
-    const v8 av = *reinterpret_cast<const v8*>(a + l16 * ap + 8 * g4);
-    const v8 bv = *reinterpret_cast<const v8*>(b + l16 * bp + 8 * g4);
-    return BwdMfma<T>::run(av, bv, acc);
-}
-
-// Stages rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) into LDS: row-major
-// at dst (pitch D + 8) and, when dstT is set, transposed at dstT ([D][TP]).  Rows past the
-// end are zeros.
-template <typename T, int D>
-__device__ __forceinline__ void stage(const T* src, int64_t rs, int r0, int nrows, T* dst, T* dstT) {
-    constexpr int CH = D / 8;
-    for (int c = threadIdx.x; c < BT * CH; c += BWD_THREADS) {
-        const int r = c / CH, ch = c - r * CH;
-        u32x4 val = u32x4{0u, 0u, 0u, 0u};
-        if (r0 + r < nrows) val = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(r0 + r) * rs + 8 * ch);
-        *reinterpret_cast<u32x4*>(dst + r * (D + 8) + 8 * ch) = val;
-        if (dstT) {
-            const auto e = __builtin_bit_cast(typename BwdMfma<T>::v8, val);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) dstT[(8 * ch + i) * TP + r] = e[i];
-        }
-    }
-}
-
-// The same staging split in two: loads of rows [r0, r0 + 32) into registers (D / 64
-// 16-byte chunks per thread, zeros past the end), issued a tile ahead, and their LDS stores.
+// Staging of rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) in two steps:
+// loads into registers (D / 64 16-byte chunks per thread, zeros past the end), issued a
+// tile ahead, and their LDS stores, row-major at pitch D + 8 and, when dstT is set,
+// transposed ([D][TP]).
 template <int D>
 struct TileRegs {
     u32x4 v[D / 64];
@@ -143,34 +114,6 @@ __global__ __launch_bounds__(256) void attn_bwd_pre(const BwdParams p) {
     for (int j = 0; j < D / 64; ++j) s += to_f32(o[lane + 64 * j]) * to_f32(d[lane + 64 * j]);
     s = wave_sum(s);
     if (lane == 0) p.dr[row] = s;
-}
-
-// P and dS of one 16x16 block held by the calling wavefront: S = Q K^T and dP = dO V^T
-// from the staged tiles, rows [rb 16, +16) of the query block at r0 and keys [kb 16, +16)
-// of the key tile at k0.  Lane (g4, l16) returns rows 4 g4 + j, key l16.
-template <typename T, int D>
-__device__ __forceinline__ void p_ds(const BwdParams& p, const T* qs, const T* dos, const T* ks, const T* vs,
-                                     const float* lse2, const float* drs, int rb, int kb, int r0, int k0,
-                                     float pv[4], float dsv[4]) {
-    const int lane = threadIdx.x & 63;
-    const int g4 = lane >> 4, l16 = lane & 15;
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f}, dp = s;
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-        s = mma_lds<T>(qs + rb * 16 * (D + 8) + 32 * c, D + 8, ks + kb * 16 * (D + 8) + 32 * c, D + 8, s);
-        dp = mma_lds<T>(dos + rb * 16 * (D + 8) + 32 * c, D + 8, vs + kb * 16 * (D + 8) + 32 * c, D + 8, dp);
-    }
-    const int key = k0 + kb * 16 + l16;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int rl = rb * 16 + 4 * g4 + j;
-        const int pos = r0 + rl;
-        const bool keep = key < p.seq_k && (!p.causal || key <= pos);
-        // Rows past the end carry lse2 = +inf: their P is exactly 0.
-        const float e = keep ? __builtin_amdgcn_exp2f(s[j] * p.c2 - lse2[rl]) : 0.f;
-        pv[j] = e;
-        dsv[j] = e * (dp[j] - drs[rl]);
-    }
 }
 
 template <typename T, int D>
@@ -353,40 +296,66 @@ __global__ __launch_bounds__(256) void attn_bwd_group_sum(const BwdParams p) {
     }
 }
 
+// dQ: a workgroup takes QW query rows, wavefront w owns rows [r0 + 16 w, + 16) with its Q
+// and dO fragments in registers (the A operands of S = Q K^T and dP = dO V^T).  Per
+// 32-key tile the workgroup stages K (row-major and transposed) and V once; each wavefront
+// forms dS of its rows, passes it through its own LDS rows and accumulates dQ += dS K.
+constexpr int QW = 64;
+
 template <typename T, int D>
 __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
+    typedef typename BwdMfma<T>::v8 v8;
     constexpr int RP = D + 8;
-    __shared__ __align__(16) T qs[BT * RP];
-    __shared__ __align__(16) T dos[BT * RP];
+    constexpr int DC = D / 32, DB = D / 16;
     __shared__ __align__(16) T ks[BT * RP];
     __shared__ __align__(16) T vs[BT * RP];
     __shared__ __align__(16) T kt[D * TP];
-    __shared__ __align__(16) T dss[BT * TP];
-    __shared__ float lse2[BT], drs[BT];
+    __shared__ __align__(16) T dss[4 * 16 * TP];  // per wavefront: dS [16 rows][32 keys]
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4, l16 = lane & 15;
-    const int nqb = (p.seq_q + BT - 1) / BT;
+    const int nqb = (p.seq_q + QW - 1) / QW;
     const int qb = blockIdx.x % nqb;
     const int bh = blockIdx.x / nqb;
     const int b = bh / p.hq, h = bh - b * p.hq;
     const int kvh = h / p.group;
-    const int r0 = qb * BT;
+    const int r0 = qb * QW;
+    const int rw0 = r0 + 16 * wave;  // this wavefront's first row
 
-    stage<T, D>(static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1], p.qs[2], r0, p.seq_q, qs, nullptr);
-    stage<T, D>(static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1], p.dos[2], r0, p.seq_q, dos, nullptr);
-    stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
-
-    const int rb = wave >> 1, kb = wave & 1;
-    const int rb2 = wave & 1;
-    constexpr int NDB = D / 32;
-    const int db0 = (wave >> 1) * NDB;
-    f32x4 dq[NDB];
+    // Q / dO fragments: lane (g4, l16) holds row rw0 + l16, dims 32 c + 8 g4 .. + 7; the
+    // row statistics of row rw0 + 4 g4 + j (the rows of its accumulator lanes).
+    v8 qf[DC], of[DC];
+    {
+        const int row = rw0 + l16;
+        const int rc = min(row, p.seq_q - 1);
+        const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1] + static_cast<int64_t>(rc) * p.qs[2];
+        const T* op = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1] + static_cast<int64_t>(rc) * p.dos[2];
 #pragma unroll
-    for (int i = 0; i < NDB; ++i) dq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < DC; ++c) {
+            const u32x4 qx = *reinterpret_cast<const u32x4*>(qp + 32 * c + 8 * g4);
+            const u32x4 ox = *reinterpret_cast<const u32x4*>(op + 32 * c + 8 * g4);
+            qf[c] = __builtin_bit_cast(v8, row < p.seq_q ? qx : u32x4{0u, 0u, 0u, 0u});
+            of[c] = __builtin_bit_cast(v8, row < p.seq_q ? ox : u32x4{0u, 0u, 0u, 0u});
+        }
+    }
+    float l2[4], drv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = rw0 + 4 * g4 + j;
+        const int rc = min(row, p.seq_q - 1);
+        const float lv = p.lse[b * p.ls[0] + h * p.ls[1] + static_cast<int64_t>(rc) * p.ls[2]];
+        const float dv = p.dr[(static_cast<int64_t>(b) * p.hq + h) * p.seq_q + rc];
+        // Rows past the end: lse2 = +inf makes their P exactly 0.
+        l2[j] = row < p.seq_q ? lv * kLog2e : INFINITY;
+        drv[j] = row < p.seq_q ? dv : 0.f;
+    }
+    f32x4 dq[DB];
+#pragma unroll
+    for (int i = 0; i < DB; ++i) dq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    T* dsw = dss + wave * 16 * TP;
 
-    const int kend = p.causal ? min(p.seq_k, r0 + BT) : p.seq_k;
+    const int kend = p.causal ? min(p.seq_k, r0 + QW) : p.seq_k;
     const T* kbase = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
     const T* vbase = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
     TileRegs<D> kr, vr;
@@ -401,24 +370,44 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
             load_regs<T, D>(kbase, p.ks[2], k0 + BT, p.seq_k, kr);
             load_regs<T, D>(vbase, p.vs[2], k0 + BT, p.seq_k, vr);
         }
-        float pv[4], dsv[4];
-        p_ds<T, D>(p, qs, dos, ks, vs, lse2, drs, rb, kb, r0, k0, pv, dsv);
-        (void)pv;
-        // dS row-major: rows rb 16 + 4 g4 + j, key kb 16 + l16.
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dss[(rb * 16 + 4 * g4 + j) * TP + kb * 16 + l16] = from_f32<T>(dsv[j]);
-        __syncthreads();
+        for (int kb = 0; kb < 2; ++kb) {
+            // S and dP of this wavefront's 16 rows x keys kb 16 .. + 15: lane (g4, l16)
+            // gets rows 4 g4 + j, key l16.
+            f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f}, dpv = sv;
 #pragma unroll
-        for (int i = 0; i < NDB; ++i) dq[i] = mma_lds<T>(dss + rb2 * 16 * TP, TP, kt + (db0 + i) * 16 * TP, TP, dq[i]);
+            for (int c = 0; c < DC; ++c) {
+                const v8 kbv = *reinterpret_cast<const v8*>(ks + (kb * 16 + l16) * RP + 32 * c + 8 * g4);
+                const v8 vbv = *reinterpret_cast<const v8*>(vs + (kb * 16 + l16) * RP + 32 * c + 8 * g4);
+                sv = BwdMfma<T>::run(qf[c], kbv, sv);
+                dpv = BwdMfma<T>::run(of[c], vbv, dpv);
+            }
+            const int key = k0 + kb * 16 + l16;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pos = rw0 + 4 * g4 + j;
+                const bool keep = key < p.seq_k && (!p.causal || key <= pos);
+                const float e = keep ? __builtin_amdgcn_exp2f(sv[j] * p.c2 - l2[j]) : 0.f;
+                dsw[(4 * g4 + j) * TP + kb * 16 + l16] = from_f32<T>(e * (dpv[j] - drv[j]));
+            }
+        }
+        // The compiler keeps this LDS read after the stores above (same array); the hardware
+        // runs one wavefront's LDS accesses in order.
+        __asm__ volatile("" ::: "memory");
+        const v8 da = *reinterpret_cast<const v8*>(dsw + l16 * TP + 8 * g4);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+            dq[db] = BwdMfma<T>::run(da, *reinterpret_cast<const v8*>(kt + (db * 16 + l16) * TP + 8 * g4), dq[db]);
     }
+    // Lane (g4, l16) of block db holds rows rw0 + 4 g4 + j, dim db 16 + l16.
     T* dqp = static_cast<T*>(p.dq) + b * p.dqs[0] + h * p.dqs[1];
 #pragma unroll
-    for (int i = 0; i < NDB; ++i) {
-        const int d = (db0 + i) * 16 + l16;
+    for (int db = 0; db < DB; ++db) {
+        const int d = db * 16 + l16;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int row = r0 + rb2 * 16 + 4 * g4 + j;
-            if (row < p.seq_q) dqp[static_cast<int64_t>(row) * p.dqs[2] + d] = from_f32<T>(dq[i][j] * p.scale);
+            const int row = rw0 + 4 * g4 + j;
+            if (row < p.seq_q) dqp[static_cast<int64_t>(row) * p.dqs[2] + d] = from_f32<T>(dq[db][j] * p.scale);
         }
     }
 }
@@ -456,7 +445,7 @@ template <typename T, int D>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
     const int64_t rows = static_cast<int64_t>(p.batch) * p.hq * p.seq_q;
     hipLaunchKernelGGL((attn_bwd_pre<T, D>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, s, p);
-    const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, BT);
+    const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, QW);
     hipLaunchKernelGGL((attn_bwd_dkdv<T, D>), dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk)),
                        dim3(BWD_THREADS), 0, s, p);
     if (p.pdk) {
