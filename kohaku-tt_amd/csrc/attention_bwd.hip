@@ -63,7 +63,9 @@ struct BwdParams {
 // Staging of rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) in two steps:
 // loads into registers (D / 64 16-byte chunks per thread, zeros past the end), issued a
 // tile ahead, and their LDS stores, row-major at pitch D + 8 and, when dstT is set,
-// transposed ([D][TP]).
+// transposed ([D][TP]).  Consecutive lanes take consecutive rows of one 8-column chunk, so
+// the transposed 2-byte stores of a wavefront spread over the banks (with consecutive
+// chunks per lane every chunk's column block starts on the same bank).
 template <int D>
 struct TileRegs {
     u32x4 v[D / 64];
@@ -71,11 +73,10 @@ struct TileRegs {
 
 template <typename T, int D>
 __device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int nrows, TileRegs<D>& t) {
-    constexpr int CH = D / 8;
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) {
         const int c = threadIdx.x + BWD_THREADS * j;
-        const int r = c / CH, ch = c - r * CH;
+        const int r = c % BT, ch = c / BT;
         const int row = min(r0 + r, nrows - 1);  // in range; rows past the end are dropped below
         const u32x4 val = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(row) * rs + 8 * ch);
         t.v[j] = r0 + r < nrows ? val : u32x4{0u, 0u, 0u, 0u};
@@ -84,11 +85,10 @@ __device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int 
 
 template <typename T, int D>
 __device__ __forceinline__ void store_regs(const TileRegs<D>& t, T* dst, T* dstT) {
-    constexpr int CH = D / 8;
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) {
         const int c = threadIdx.x + BWD_THREADS * j;
-        const int r = c / CH, ch = c - r * CH;
+        const int r = c % BT, ch = c / BT;
         *reinterpret_cast<u32x4*>(dst + r * (D + 8) + 8 * ch) = t.v[j];
         if (dstT) {
             const auto e = __builtin_bit_cast(typename BwdMfma<T>::v8, t.v[j]);
