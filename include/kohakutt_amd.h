@@ -134,7 +134,7 @@ int kmi_attn_fwd(const kmi_attn_args* args, void* workspace, size_t workspace_by
  *   query heads.  Layouts as kmi_attn_fwd's dense ones (element strides of the batch, head
  *   and sequence dims, head-dim stride 1); q, k, v, grad_out 16-byte aligned with strides
  *   multiples of 8.  Workspace: kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row
- *   dot products; with GQA also fp32 per-query-head dK / dV partials).
+ *   dot products; with GQA or split query ranges also fp32 dK / dV partials).
  * Replaces the reference's flash backward behind tt_sdpa_overrideable_backward's stats
  * route (aten_attention.cpp:716-812; bridge in device_attention.cpp:1208-1281;
  * docs/reference/kernels/flash.md:151-206).  Supported: BF16 / F16, head_dim 64 or 128.

@@ -20,6 +20,8 @@
 // v_mfma_f32_16x16x32_{bf16,f16}.  Every operand is read from LDS along its contraction
 // index (16 contiguous bytes per lane): tiles needed with either index contiguous are
 // staged twice, row-major and transposed.  lse is the forward's natural-log row LSE.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace kmi {
@@ -55,6 +57,9 @@ struct BwdParams {
     // GQA (group > 1): per-query-head dK / dV partials [batch][hq][seq_k][D] fp32, summed
     // over each group by attn_bwd_group_sum; null when every K/V head has one query head.
     float *pdk, *pdv;
+    // dK / dV workgroups per (query head, key tile): split q takes query blocks q, q + qsplit,
+    // ...; with qsplit > 1 every split writes fp32 partials (indexed [b][h][split][key][D]).
+    int qsplit;
     int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3], ls[3];
     int batch, hq, hkv, group, seq_q, seq_k, causal;
     float scale, c2;  // c2 = scale * log2(e)
@@ -152,8 +157,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4, l16 = lane & 15;
     const int ntk = (p.seq_k + KW - 1) / KW;
-    const int tile = blockIdx.x % ntk;
-    const int bh = blockIdx.x / ntk;  // (sequence, query head)
+    const int qsp = blockIdx.x % p.qsplit;
+    const int tile = (blockIdx.x / p.qsplit) % ntk;
+    const int bh = blockIdx.x / (p.qsplit * ntk);  // (sequence, query head)
     const int b = bh / p.hq, h = bh - b * p.hq;
     const int kvh = h / p.group;
     const int k0 = tile * KW;
@@ -181,7 +187,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     T* dsw = dst + wave * 16 * TP;
 
     // Causal (top-left): a query block sees this tile only if its last position reaches k0.
-    const int rstart = p.causal ? (k0 / BT) * BT : 0;
+    const int rstart = (p.causal ? (k0 / BT) * BT : 0) + qsp * BT;
+    const int rstep = p.qsplit * BT;
     const T* qbase = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1];
     const T* dobase = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1];
     TileRegs<D> qr, dor;
@@ -189,15 +196,15 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         load_regs<T, D>(qbase, p.qs[2], rstart, p.seq_q, qr);
         load_regs<T, D>(dobase, p.dos[2], rstart, p.seq_q, dor);
     }
-    for (int r0 = rstart; r0 < p.seq_q; r0 += BT) {
+    for (int r0 = rstart; r0 < p.seq_q; r0 += rstep) {
         __syncthreads();  // the previous block's LDS reads are done
         store_regs<T, D>(qr, qs, qt);
         store_regs<T, D>(dor, dos, dot);
         stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
         __syncthreads();
-        if (r0 + BT < p.seq_q) {  // the next block's loads overlap this block's products
-            load_regs<T, D>(qbase, p.qs[2], r0 + BT, p.seq_q, qr);
-            load_regs<T, D>(dobase, p.dos[2], r0 + BT, p.seq_q, dor);
+        if (r0 + rstep < p.seq_q) {  // the next block's loads overlap this block's products
+            load_regs<T, D>(qbase, p.qs[2], r0 + rstep, p.seq_q, qr);
+            load_regs<T, D>(dobase, p.dos[2], r0 + rstep, p.seq_q, dor);
         }
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
@@ -239,7 +246,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     }
     // Lane (g4, l16) of block db holds keys kw0 + 4 g4 + j, dim db 16 + l16.
     if (p.pdk) {
-        const int64_t base = (static_cast<int64_t>(b) * p.hq + h) * p.seq_k;
+        const int64_t base = ((static_cast<int64_t>(b) * p.hq + h) * p.qsplit + qsp) * p.seq_k;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const int d = db * 16 + l16;
@@ -270,7 +277,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     }
 }
 
-// dK / dV of a K/V head: the sum of its query heads' fp32 partials, in head order.
+// dK / dV of a K/V head: the sum of its query heads' fp32 partials (and of their query
+// splits), in a fixed order.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_group_sum(const BwdParams p) {
     constexpr int Q = D / 4;  // float4 items per key row
@@ -283,9 +291,12 @@ __global__ __launch_bounds__(256) void attn_bwd_group_sum(const BwdParams p) {
     const int b = static_cast<int>(bk / p.hkv), kvh = static_cast<int>(bk % p.hkv);
     f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = sk;
     for (int g = 0; g < p.group; ++g) {
-        const int64_t row = (static_cast<int64_t>(b) * p.hq + kvh * p.group + g) * p.seq_k + key;
-        sk += *reinterpret_cast<const f32x4*>(p.pdk + row * D + 4 * c);
-        sv += *reinterpret_cast<const f32x4*>(p.pdv + row * D + 4 * c);
+        for (int q = 0; q < p.qsplit; ++q) {
+            const int64_t row =
+                ((static_cast<int64_t>(b) * p.hq + kvh * p.group + g) * p.qsplit + q) * p.seq_k + key;
+            sk += *reinterpret_cast<const f32x4*>(p.pdk + row * D + 4 * c);
+            sv += *reinterpret_cast<const f32x4*>(p.pdv + row * D + 4 * c);
+        }
     }
     T* dkp = static_cast<T*>(p.dk) + b * p.dks[0] + kvh * p.dks[1] + static_cast<int64_t>(key) * p.dks[2] + 4 * c;
     T* dvp = static_cast<T*>(p.dv) + b * p.dvs[0] + kvh * p.dvs[1] + static_cast<int64_t>(key) * p.dvs[2] + 4 * c;
@@ -434,10 +445,20 @@ const char* check_bwd(const kmi_attn_bwd_args* a) {
     return nullptr;
 }
 
-// Row dot products (padded to 16 bytes), then with GQA the dK / dV partials.
+// dK / dV query splits: enough workgroups for about two per CU (at most 4 splits, at most
+// one per 32-row query block).
+int bwd_qsplit(const kmi_attn_bwd_args* a) {
+    const int64_t wgs = a->batch * a->heads_q * ceil_div(a->seq_k, KW);
+    int64_t qs = std::min<int64_t>(4, std::max<int64_t>(1, ceil_div(512, wgs)));
+    return static_cast<int>(std::min<int64_t>(qs, ceil_div(a->seq_q, BT)));
+}
+
+// Row dot products (padded to 16 bytes), then with GQA or query splits the dK / dV partials.
 size_t bwd_ws_bytes(const kmi_attn_bwd_args* a) {
     size_t floats = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
-    if (a->heads_q != a->heads_kv) floats += 2 * static_cast<size_t>(a->batch * a->heads_q * a->seq_k * a->head_dim);
+    const int qs = bwd_qsplit(a);
+    if (a->heads_q != a->heads_kv || qs > 1)
+        floats += 2 * static_cast<size_t>(a->batch * a->heads_q * qs * a->seq_k * a->head_dim);
     return floats * sizeof(float);
 }
 
@@ -446,7 +467,8 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
     const int64_t rows = static_cast<int64_t>(p.batch) * p.hq * p.seq_q;
     hipLaunchKernelGGL((attn_bwd_pre<T, D>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, s, p);
     const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, QW);
-    hipLaunchKernelGGL((attn_bwd_dkdv<T, D>), dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk)),
+    hipLaunchKernelGGL((attn_bwd_dkdv<T, D>),
+                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk * p.qsplit)),
                        dim3(BWD_THREADS), 0, s, p);
     if (p.pdk) {
         const int64_t items = static_cast<int64_t>(p.batch) * p.hkv * p.seq_k * (D / 4);
@@ -486,10 +508,11 @@ extern "C" int kmi_attn_bwd(const kmi_attn_bwd_args* a, void* workspace, size_t 
     p.dk = a->grad_k;
     p.dv = a->grad_v;
     p.dr = static_cast<float*>(workspace);
-    if (a->heads_q != a->heads_kv) {
+    p.qsplit = bwd_qsplit(a);
+    if (a->heads_q != a->heads_kv || p.qsplit > 1) {
         // Partials start 16-byte aligned after the row dot products.
         const size_t dr_floats = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
-        const size_t part = static_cast<size_t>(a->batch * a->heads_q * a->seq_k * a->head_dim);
+        const size_t part = static_cast<size_t>(a->batch * a->heads_q * p.qsplit * a->seq_k * a->head_dim);
         p.pdk = p.dr + dr_floats;
         p.pdv = p.pdk + part;
     }
