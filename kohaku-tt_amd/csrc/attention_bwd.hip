@@ -60,6 +60,10 @@ struct BwdParams {
     // dK / dV workgroups per (query head, key tile): split q takes query blocks q, q + qsplit,
     // ...; with qsplit > 1 every split writes fp32 partials (indexed [b][h][split][key][D]).
     int qsplit;
+    // dQ workgroups per (query head, row block): split k takes key tiles k, k + ksplit, ...;
+    // with ksplit > 1 every split writes fp32 partials pdq [b][h][split][row][D].
+    int ksplit;
+    float* pdq;
     int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3], ls[3];
     int batch, hq, hkv, group, seq_q, seq_k, causal;
     float scale, c2;  // c2 = scale * log2(e)
@@ -327,8 +331,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4, l16 = lane & 15;
     const int nqb = (p.seq_q + QW - 1) / QW;
-    const int qb = blockIdx.x % nqb;
-    const int bh = blockIdx.x / nqb;
+    const int ksp = blockIdx.x % p.ksplit;
+    const int qb = (blockIdx.x / p.ksplit) % nqb;
+    const int bh = blockIdx.x / (p.ksplit * nqb);
     const int b = bh / p.hq, h = bh - b * p.hq;
     const int kvh = h / p.group;
     const int r0 = qb * QW;
@@ -370,16 +375,17 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const T* kbase = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
     const T* vbase = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
     TileRegs<D> kr, vr;
-    load_regs<T, D>(kbase, p.ks[2], 0, p.seq_k, kr);
-    load_regs<T, D>(vbase, p.vs[2], 0, p.seq_k, vr);
-    for (int k0 = 0; k0 < kend; k0 += BT) {
+    const int kstep = p.ksplit * BT;
+    load_regs<T, D>(kbase, p.ks[2], ksp * BT, p.seq_k, kr);
+    load_regs<T, D>(vbase, p.vs[2], ksp * BT, p.seq_k, vr);
+    for (int k0 = ksp * BT; k0 < kend; k0 += kstep) {
         __syncthreads();
         store_regs<T, D>(kr, ks, kt);
         store_regs<T, D>(vr, vs, nullptr);
         __syncthreads();
-        if (k0 + BT < kend) {  // the next tile's loads overlap this tile's products
-            load_regs<T, D>(kbase, p.ks[2], k0 + BT, p.seq_k, kr);
-            load_regs<T, D>(vbase, p.vs[2], k0 + BT, p.seq_k, vr);
+        if (k0 + kstep < kend) {  // the next tile's loads overlap this tile's products
+            load_regs<T, D>(kbase, p.ks[2], k0 + kstep, p.seq_k, kr);
+            load_regs<T, D>(vbase, p.vs[2], k0 + kstep, p.seq_k, vr);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -411,6 +417,19 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
             dq[db] = BwdMfma<T>::run(da, *reinterpret_cast<const v8*>(kt + (db * 16 + l16) * TP + 8 * g4), dq[db]);
     }
     // Lane (g4, l16) of block db holds rows rw0 + 4 g4 + j, dim db 16 + l16.
+    if (p.pdq) {
+        float* dst = p.pdq + ((static_cast<int64_t>(b) * p.hq + h) * p.ksplit + ksp) * p.seq_q * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int d = db * 16 + l16;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = rw0 + 4 * g4 + j;
+                if (row < p.seq_q) dst[static_cast<int64_t>(row) * D + d] = dq[db][j] * p.scale;
+            }
+        }
+        return;
+    }
     T* dqp = static_cast<T*>(p.dq) + b * p.dqs[0] + h * p.dqs[1];
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -421,6 +440,25 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
             if (row < p.seq_q) dqp[static_cast<int64_t>(row) * p.dqs[2] + d] = from_f32<T>(dq[db][j] * p.scale);
         }
     }
+}
+
+// dQ: the sum of the key splits' fp32 partials, in split order.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_dq_sum(const BwdParams p) {
+    constexpr int Q = D / 4;
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t items = static_cast<int64_t>(p.batch) * p.hq * p.seq_q * Q;
+    if (item >= items) return;
+    const int c = static_cast<int>(item % Q);
+    const int row = static_cast<int>((item / Q) % p.seq_q);
+    const int64_t bh = item / (static_cast<int64_t>(Q) * p.seq_q);
+    const int b = static_cast<int>(bh / p.hq), h = static_cast<int>(bh % p.hq);
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < p.ksplit; ++k)
+        acc += *reinterpret_cast<const f32x4*>(p.pdq + ((bh * p.ksplit + k) * p.seq_q + row) * D + 4 * c);
+    T* dst = static_cast<T*>(p.dq) + b * p.dqs[0] + h * p.dqs[1] + static_cast<int64_t>(row) * p.dqs[2] + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(acc[e]);
 }
 
 const char* check_bwd(const kmi_attn_bwd_args* a) {
@@ -453,13 +491,32 @@ int bwd_qsplit(const kmi_attn_bwd_args* a) {
     return static_cast<int>(std::min<int64_t>(qs, ceil_div(a->seq_q, BT)));
 }
 
-// Row dot products (padded to 16 bytes), then with GQA or query splits the dK / dV partials.
-size_t bwd_ws_bytes(const kmi_attn_bwd_args* a) {
-    size_t floats = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
+// dQ key splits, by the same rule over (query head, 64-row block) workgroups.
+int bwd_ksplit(const kmi_attn_bwd_args* a) {
+    const int64_t wgs = a->batch * a->heads_q * ceil_div(a->seq_q, QW);
+    int64_t ks = std::min<int64_t>(4, std::max<int64_t>(1, ceil_div(512, wgs)));
+    return static_cast<int>(std::min<int64_t>(ks, ceil_div(a->seq_k, BT)));
+}
+
+// Workspace floats: row dot products (padded to 16 bytes); with GQA or query splits the
+// dK / dV partials; with key splits the dQ partials.
+struct BwdLayout {
+    size_t dr, part, pdq;
+};
+
+BwdLayout bwd_layout(const kmi_attn_bwd_args* a) {
+    BwdLayout l{};
+    l.dr = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
     const int qs = bwd_qsplit(a);
-    if (a->heads_q != a->heads_kv || qs > 1)
-        floats += 2 * static_cast<size_t>(a->batch * a->heads_q * qs * a->seq_k * a->head_dim);
-    return floats * sizeof(float);
+    if (a->heads_q != a->heads_kv || qs > 1) l.part = static_cast<size_t>(a->batch * a->heads_q * qs * a->seq_k * a->head_dim);
+    const int ks = bwd_ksplit(a);
+    if (ks > 1) l.pdq = static_cast<size_t>(a->batch * a->heads_q * ks * a->seq_q * a->head_dim);
+    return l;
+}
+
+size_t bwd_ws_bytes(const kmi_attn_bwd_args* a) {
+    const BwdLayout l = bwd_layout(a);
+    return (l.dr + 2 * l.part + l.pdq) * sizeof(float);
 }
 
 template <typename T, int D>
@@ -475,8 +532,14 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
         hipLaunchKernelGGL((attn_bwd_group_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0,
                            s, p);
     }
-    hipLaunchKernelGGL((attn_bwd_dq<T, D>), dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb)),
+    hipLaunchKernelGGL((attn_bwd_dq<T, D>),
+                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit)),
                        dim3(BWD_THREADS), 0, s, p);
+    if (p.pdq) {
+        const int64_t items = static_cast<int64_t>(p.batch) * p.hq * p.seq_q * (D / 4);
+        hipLaunchKernelGGL((attn_bwd_dq_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0, s,
+                           p);
+    }
     return hipGetLastError();
 }
 
@@ -509,12 +572,15 @@ extern "C" int kmi_attn_bwd(const kmi_attn_bwd_args* a, void* workspace, size_t 
     p.dv = a->grad_v;
     p.dr = static_cast<float*>(workspace);
     p.qsplit = bwd_qsplit(a);
-    if (a->heads_q != a->heads_kv || p.qsplit > 1) {
-        // Partials start 16-byte aligned after the row dot products.
-        const size_t dr_floats = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
-        const size_t part = static_cast<size_t>(a->batch * a->heads_q * p.qsplit * a->seq_k * a->head_dim);
-        p.pdk = p.dr + dr_floats;
-        p.pdv = p.pdk + part;
+    p.ksplit = bwd_ksplit(a);
+    {
+        // Partials start 16-byte aligned after the row dot products (D is a multiple of 4).
+        const BwdLayout l = bwd_layout(a);
+        if (l.part) {
+            p.pdk = p.dr + l.dr;
+            p.pdv = p.pdk + l.part;
+        }
+        if (l.pdq) p.pdq = p.dr + l.dr + 2 * l.part;
     }
     for (int i = 0; i < 3; ++i) {
         p.qs[i] = a->q_stride[i];

@@ -22,6 +22,9 @@ CASES = [
     (1, 4, 1, 200, 120, 64, True),
     (2, 6, 3, 77, 77, 128, True),
     (1, 2, 2, 1, 45, 64, False),
+    # Enough workgroups that dK/dV and dQ run unsplit (direct writes, no partials):
+    (16, 8, 8, 256, 256, 64, False),
+    (8, 16, 4, 256, 256, 128, True),
 ]
 
 
