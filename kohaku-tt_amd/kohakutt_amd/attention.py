@@ -202,20 +202,93 @@ def sdpa_varlen(
             f"kohakutt_amd.sdpa_varlen: attn_mask must be [{k.size(0)}] (one value per "
             f"packed key), got {tuple(attn_mask.shape)}"
         )
-    out, _ = torch.ops.ktt._sdpa_varlen(
-        q,
-        k,
-        v,
-        cu_q_t,
-        cu_k_t,
-        int(max_q),
-        int(max_k),
-        bool(is_causal),
-        None if scale is None else float(scale),
-        attn_mask,
-        packed_mask,
-    )
+    args = (cu_q_t, cu_k_t, int(max_q), int(max_k), bool(is_causal), None if scale is None else float(scale),
+            attn_mask, packed_mask)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _Varlen.apply(q, k, v, *args)
+    out, _ = torch.ops.ktt._sdpa_varlen(q, k, v, *args)
     return out
+
+
+class _Varlen(torch.autograd.Function):
+    """Packed attention with autograd (the reference's ``_sdpa_varlen_backward``,
+    ``aten_varlen.cpp:240-300``, behind ``varlen.py:62-104``).  The backward goes sequence
+    by sequence: an unmasked sequence whose causal rule is the dense one (non-causal, or
+    Lq == Lk, where bottom-right and top-left agree) runs the flash backward kernels
+    (``ktt::_sdpa_flash_backward``) on [1, H, L, D] head views of the packed tensors and
+    the forward's lse; any other sequence recomputes in float64 with the forward's mask
+    rules (masked keys at -5e5, so a fully-masked row is the softmax over its raw scores)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q_t, cu_k_t, max_q, max_k, causal, scale, attn_mask, packed_mask):
+        out, lse = torch.ops.ktt._sdpa_varlen(q, k, v, cu_q_t, cu_k_t, max_q, max_k, causal, scale, attn_mask,
+                                              packed_mask)
+        ctx.save_for_backward(q, k, v, out, lse, cu_q_t, cu_k_t, attn_mask, packed_mask)
+        ctx.args = (causal, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        q, k, v, out, lse, cu_q_t, cu_k_t, attn_mask, packed_mask = ctx.saved_tensors
+        causal, scale = ctx.args
+        cu_q, cu_k = offsets(cu_q_t), offsets(cu_k_t)
+        grad = grad.contiguous()
+        dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+        heads = lambda t, a, b: t[a:b].transpose(0, 1).unsqueeze(0)  # [1, H, L, D] view
+        kernels = q.dtype in (torch.bfloat16, torch.float16) and q.size(-1) in (64, 128)
+        off = 0  # packed-mask offset of this sequence's block
+        for i in range(len(cu_q) - 1):
+            a, b, c, d = cu_q[i], cu_q[i + 1], cu_k[i], cu_k[i + 1]
+            lq, lk = b - a, d - c
+            block = None
+            if packed_mask is not None:
+                block = packed_mask.reshape(-1)[off:off + lq * lk].view(lq, lk)
+            off += lq * lk
+            if lq == 0 or lk == 0:
+                continue
+            if kernels and attn_mask is None and block is None and (not causal or lq == lk):
+                gq, gk, gv = torch.ops.ktt._sdpa_flash_backward(
+                    heads(grad, a, b), heads(q, a, b), heads(k, c, d), heads(v, c, d), heads(out, a, b),
+                    lse[:, a:b].unsqueeze(0), bool(causal), scale)
+            else:
+                key = None if attn_mask is None else attn_mask[c:d]
+                gq, gk, gv = _varlen_recompute_grads(heads(q, a, b), heads(k, c, d), heads(v, c, d),
+                                                     heads(grad, a, b), causal, scale, key, block)
+            dq[a:b] = gq[0].transpose(0, 1).to(dq.dtype)
+            dk[c:d] = gk[0].transpose(0, 1).to(dk.dtype)
+            dv[c:d] = gv[0].transpose(0, 1).to(dv.dtype)
+        return dq, dk, dv, None, None, None, None, None, None, None, None
+
+
+def _varlen_recompute_grads(q, k, v, grad, causal, scale, key_mask, block):
+    """Gradients of one sequence in float64 with the forward's rules: bottom-right causal
+    (invisible keys excluded), masked keys at the -5e5 logit (bool False, or additive
+    values clamped there)."""
+    with torch.enable_grad():  # a Function's backward runs with grad mode off
+        return _recompute(q, k, v, grad, causal, scale, key_mask, block)
+
+
+def _recompute(q, k, v, grad, causal, scale, key_mask, block):
+    q64, k64, v64 = (t.detach().double().requires_grad_() for t in (q, k, v))
+    hq, hk, lq, lk = q.size(1), k.size(1), q.size(2), k.size(2)
+    kk, vv = k64.repeat_interleave(hq // hk, 1), v64.repeat_interleave(hq // hk, 1)
+    s = (scale if scale is not None else q.size(-1) ** -0.5) * (q64 @ kk.transpose(-2, -1))
+    add = torch.zeros(lq, lk, dtype=torch.float64, device=q.device)
+    for m in (None if key_mask is None else key_mask.reshape(1, lk), block):
+        if m is None:
+            continue
+        m = m.to(q.device)
+        if m.dtype == torch.bool:
+            add = add + torch.where(m, 0.0, _MASKED_LOGIT).to(torch.float64)
+        else:
+            add = add + m.to(torch.float64)
+    s = s + add.clamp_min(_MASKED_LOGIT)
+    if causal:
+        rows = torch.arange(lq, device=q.device)[:, None]
+        keys = torch.arange(lk, device=q.device)[None, :]
+        s = s.masked_fill(keys > rows + (lk - lq), float("-inf"))
+    out = torch.softmax(s, -1) @ vv
+    return torch.autograd.grad(out, (q64, k64, v64), grad.double())
 
 
 def _varlen_attn_gpu(query, key, value, cu_seq_q, cu_seq_k, max_q, max_k, is_causal=False):

@@ -112,3 +112,63 @@ def test_masked_calls_keep_the_recompute_backward(native, dev):
     q64 = q.double().requires_grad_()
     F.scaled_dot_product_attention(q64, k.double(), v.double(), attn_mask=mask.double()).sum().backward()
     assert (qd.grad.cpu().double() - q64.grad).abs().max().item() < 5e-2
+
+
+def _varlen_ref_grads(q, k, v, go, cu_q, cu_k, causal, key_mask=None):
+    """Per-sequence float64 autograd of torch CPU SDPA (bottom-right causal as an explicit
+    mask; a bool key mask keeps True keys); packed [T, H, D] gradients."""
+    grads = [torch.zeros(t.shape, dtype=torch.float64) for t in (q, k, v)]
+    hq, hk = q.size(1), k.size(1)
+    for i in range(len(cu_q) - 1):
+        a, b, c, d = cu_q[i], cu_q[i + 1], cu_k[i], cu_k[i + 1]
+        lq, lk = b - a, d - c
+        qs, ks, vs = (t.double().transpose(0, 1)[None].requires_grad_() for t in (q[a:b], k[c:d], v[c:d]))
+        keep = torch.ones(lq, lk, dtype=torch.bool)
+        if causal:
+            keep &= torch.arange(lk)[None, :] <= torch.arange(lq)[:, None] + (lk - lq)
+        if key_mask is not None:
+            keep &= key_mask[c:d][None, :]
+        out = F.scaled_dot_product_attention(qs, ks.repeat_interleave(hq // hk, 1), vs.repeat_interleave(hq // hk, 1),
+                                             attn_mask=keep)
+        out.backward(go[a:b].double().transpose(0, 1)[None])
+        for gsum, t, (lo, hi) in zip(grads, (qs, ks, vs), ((a, b), (c, d), (c, d))):
+            gsum[lo:hi] = t.grad[0].transpose(0, 1)
+    return grads
+
+
+@pytest.mark.parametrize("kind", ["causal_self", "cross_noncausal", "causal_fewer_queries", "key_mask"])
+def test_varlen_backward_matches_float64_autograd(native, dev, kind):
+    """Gradients through ``kohakutt_amd.sdpa_varlen``: sequences with the dense causal rule
+    and no mask take the flash backward kernels, the others the float64 recompute."""
+    g = C.gen(960 + len(kind))
+    hq, hk, d = 8, 2, 64
+    if kind == "causal_self":
+        lq = [70, 1, 130, 33]
+        lk = lq
+    elif kind == "cross_noncausal":
+        lq, lk = [40, 77, 5], [90, 12, 64]
+    else:
+        lq, lk = [20, 50, 3], [64, 50, 40]
+    cu_q = [0] + list(torch.tensor(lq).cumsum(0).tolist())
+    cu_k = [0] + list(torch.tensor(lk).cumsum(0).tolist())
+    causal = kind in ("causal_self", "causal_fewer_queries")
+    q, go = C.randn(g, cu_q[-1], hq, d), C.randn(g, cu_q[-1], hq, d)
+    k, v = C.randn(g, cu_k[-1], hk, d), C.randn(g, cu_k[-1], hk, d)
+    key_mask = None
+    if kind == "key_mask":
+        key_mask = torch.rand(cu_k[-1], generator=g) > 0.3
+        for c in cu_k[:-1]:
+            key_mask[c] = True  # every row keeps a key
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    native.reset_counters()
+    out = native.sdpa_varlen(qd, kd, vd, cu_q, cu_k, is_causal=causal,
+                             attn_mask=None if key_mask is None else key_mask.to(dev))
+    out.backward(go.to(dev))
+    torch.cuda.synchronize()
+    flash = native.counters()["attention_backward"]
+    expect = 0 if key_mask is not None else sum(1 for a, b in zip(lq, lk) if not causal or a == b)
+    assert flash == expect, (flash, expect)
+    ref = _varlen_ref_grads(q, k, v, go, cu_q, cu_k, causal, key_mask)
+    for name, got, want in zip(("dq", "dk", "dv"), (qd.grad, kd.grad, vd.grad), ref):
+        err = (got.cpu().double() - want).abs().max().item()
+        assert err <= 3e-2 * max(want.abs().max().item(), 1.0), (kind, name, err)
