@@ -195,6 +195,22 @@ int kmi_rms_norm_fwd(const void* x, const void* weight, const void* bias, void* 
                      float* rstd, int64_t rows, int64_t width, int32_t x_dtype,
                      int32_t w_dtype, int32_t b_dtype, double eps, void* stream);
 
+/*
+ * RMSNorm backward over rows of `width` contiguous elements, from the forward's fp32 rstd:
+ *   dx = rstd * (dy * weight) - x * rstd^3 * mean(dy * weight * x)   (per row),
+ *   dweight = sum over rows of dy * x * rstd                          (per column).
+ * dy / dx have x's dtype (BF16, F16 or F32); weight / dweight w_dtype; weight may be NULL
+ * (then dweight must be NULL).  dweight needs kmi_rms_norm_bwd_workspace_bytes of fp32
+ * workspace (per-chunk column sums, added in a fixed order: deterministic).
+ * Replaces the reference's RMSNorm training backward (RmsNormFunction, aten_norm.cpp:
+ * 548-599; ktt_norm backward and column-sum programs, layernorm.md:90-102).
+ */
+int kmi_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t width, size_t* bytes);
+
+int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weight, const float* rstd,
+                     void* dx, void* dweight, int64_t rows, int64_t width, int32_t x_dtype,
+                     int32_t w_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 /* The message of the last failed call on this thread ("" if none). */
 const char* kmi_last_error(void);
 

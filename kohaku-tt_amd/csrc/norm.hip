@@ -14,6 +14,7 @@
 // 256-thread block per row with element loads (any width and alignment).
 #include "common.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace kmi {
@@ -394,6 +395,64 @@ bool aligned(const void* p, int64_t bytes) {
     return p == nullptr || (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
+// RMSNorm backward (the reference's ktt_norm backward programs, ktt_norm/bwd_*.cpp, with
+// its column sum for the weight, colsum_*; layernorm.md:90-102).  y = x r w with
+// r = rstd of the row: dx = r (g w) - x r^3 mean(g w x), dw = sum over rows of g x r.
+// dx: one 256-thread block per row, fp32 sums; any width and alignment.
+__global__ __launch_bounds__(256) void rms_bwd_rows(const void* dy, const void* x, const void* weight,
+                                                    const float* rstd, void* dx, int64_t width, int x_dtype,
+                                                    int w_dtype) {
+    __shared__ float scratch[4];
+    const int64_t row = blockIdx.x;
+    const int64_t base = row * width;
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
+        float gw = load_any(dy, x_dtype, base + i);
+        if (weight) gw *= load_any(weight, w_dtype, i);
+        s += gw * load_any(x, x_dtype, base + i);
+    }
+    s = block_sum(s, scratch);
+    const float r = rstd[row];
+    const float c = r * r * r * s / static_cast<float>(width);
+    for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
+        float gw = load_any(dy, x_dtype, base + i);
+        if (weight) gw *= load_any(weight, w_dtype, i);
+        store_any(dx, x_dtype, base + i, r * gw - load_any(x, x_dtype, base + i) * c);
+    }
+}
+
+// dw, first stage: block (column group, chunk) sums g x r over the chunk's rows for 256
+// consecutive columns (coalesced across the threads) into fp32 partials [chunk][width].
+__global__ __launch_bounds__(256) void rms_bwd_dw_partial(const void* dy, const void* x, const float* rstd,
+                                                          float* part, int64_t rows, int64_t width,
+                                                          int64_t rows_per_chunk, int x_dtype) {
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (col >= width) return;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
+    const int64_t r1 = r0 + rows_per_chunk < rows ? r0 + rows_per_chunk : rows;
+    float acc = 0.f;
+    for (int64_t r = r0; r < r1; ++r)
+        acc += load_any(dy, x_dtype, r * width + col) * load_any(x, x_dtype, r * width + col) * rstd[r];
+    part[static_cast<int64_t>(blockIdx.y) * width + col] = acc;
+}
+
+// dw, second stage: the chunks' partials added in chunk order.
+__global__ __launch_bounds__(256) void rms_bwd_dw_final(const float* part, void* dw, int64_t chunks, int64_t width,
+                                                        int w_dtype) {
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (col >= width) return;
+    float acc = 0.f;
+    for (int64_t c = 0; c < chunks; ++c) acc += part[c * width + col];
+    store_any(dw, w_dtype, col, acc);
+}
+
+constexpr int64_t kRmsBwdRowsPerChunk = 64;
+constexpr int64_t kRmsBwdMaxChunks = 1024;
+
+int64_t rms_bwd_chunks(int64_t rows) {
+    return std::min<int64_t>(kRmsBwdMaxChunks, std::max<int64_t>(1, ceil_div(rows, kRmsBwdRowsPerChunk)));
+}
+
 template <bool LAYER>
 int norm_fwd(const char* name, const void* x, const void* w, const void* b, void* y,
              float* mean, float* rstd, int64_t rows, int64_t width, int x_dtype,
@@ -471,4 +530,46 @@ extern "C" int kmi_rms_norm_fwd(const void* x, const void* weight, const void* b
     return kmi::norm_fwd<false>("kmi_rms_norm_fwd", x, weight, bias, y, nullptr, rstd,
                                 rows, width, x_dtype, w_dtype, b_dtype, eps,
                                 static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kmi_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t width, size_t* bytes) {
+    using namespace kmi;
+    if (!bytes) return fail(KMI_EINVAL, "kmi_rms_norm_bwd_workspace_bytes: null bytes");
+    if (rows < 0 || width < 0) return fail(KMI_EINVAL, "kmi_rms_norm_bwd_workspace_bytes: negative size");
+    *bytes = rows == 0 ? 0 : static_cast<size_t>(rms_bwd_chunks(rows) * width) * sizeof(float);
+    return KMI_OK;
+}
+
+extern "C" int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weight, const float* rstd, void* dx,
+                                void* dweight, int64_t rows, int64_t width, int32_t x_dtype, int32_t w_dtype,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+    using namespace kmi;
+    const char* name = "kmi_rms_norm_bwd";
+    if (dtype_size(x_dtype) == 0) return fail(KMI_EINVAL, std::string(name) + ": x dtype must be BF16, F16 or F32");
+    if (weight && dtype_size(w_dtype) == 0)
+        return fail(KMI_EINVAL, std::string(name) + ": weight dtype must be BF16, F16 or F32");
+    if (rows < 0 || width < 0) return fail(KMI_EINVAL, std::string(name) + ": negative size");
+    if (rows == 0) return KMI_OK;
+    if (width == 0) return fail(KMI_EINVAL, std::string(name) + ": empty rows");
+    if (!dy || !x || !rstd || !dx) return fail(KMI_EINVAL, std::string(name) + ": null dy, x, rstd or dx");
+    if (dweight && !weight) return fail(KMI_EINVAL, std::string(name) + ": dweight needs weight");
+    if (rows > (int64_t{1} << 31) || width > (int64_t{1} << 30))
+        return fail(KMI_EUNSUPPORTED, std::string(name) + ": too many rows or too wide");
+    const int64_t chunks = rms_bwd_chunks(rows);
+    if (dweight && (!workspace || workspace_bytes < static_cast<size_t>(chunks * width) * sizeof(float) ||
+                    reinterpret_cast<uintptr_t>(workspace) % 4))
+        return fail(KMI_EWORKSPACE, std::string(name) + ": workspace missing or smaller than "
+                                                        "kmi_rms_norm_bwd_workspace_bytes");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(rms_bwd_rows, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, dy, x, weight, rstd, dx,
+                       width, static_cast<int>(x_dtype), static_cast<int>(w_dtype));
+    if (dweight) {
+        float* part = static_cast<float*>(workspace);
+        const unsigned gx = static_cast<unsigned>(ceil_div(width, 256));
+        hipLaunchKernelGGL(rms_bwd_dw_partial, dim3(gx, static_cast<unsigned>(chunks)), dim3(256), 0, s, dy, x, rstd,
+                           part, rows, width, ceil_div(rows, chunks), static_cast<int>(x_dtype));
+        hipLaunchKernelGGL(rms_bwd_dw_final, dim3(gx), dim3(256), 0, s, part, dweight, chunks, width,
+                           static_cast<int>(w_dtype));
+    }
+    return hip_status(hipGetLastError(), name);
 }

@@ -51,7 +51,8 @@ std::atomic<bool> g_norms{env_on("KMI_NORMS")};
 // KMI_PITCHED_OUT=0 (read at load) keeps the attention output dense for head-view inputs.
 const bool g_pitched_out = env_on("KMI_PITCHED_OUT");
 // Calls the kernels took, per family (ktt::counters).
-std::atomic<int64_t> g_attn_calls{0}, g_norm_calls{0}, g_attn_declined{0}, g_attn_bwd_calls{0};
+std::atomic<int64_t> g_attn_calls{0}, g_norm_calls{0}, g_attn_declined{0}, g_attn_bwd_calls{0},
+    g_norm_bwd_calls{0};
 
 void check(int status, const char* what) {
     TORCH_CHECK(status == KMI_OK, "kohakutt_amd: ", what, " failed (", status, "): ", kmi_last_error());
@@ -670,12 +671,13 @@ std::tuple<Tensor, Tensor> rms_forward(const Tensor& input, int64_t width, optio
 // RMSNorm with gradients: the kernel forward, an fp32 backward from the saved rstd (the
 // reference's RmsNormFunction, aten_norm.cpp:548-599).
 struct RmsNormFn : public torch::autograd::Function<RmsNormFn> {
-    static Tensor forward(torch::autograd::AutogradContext* ctx, const Tensor& x, const Tensor& w, int64_t nd,
-                          double eps) {
+    // The weight travels as an optional: an undefined Tensor argument is taken for a
+    // variable by the Function machinery (which then asks it for its device).
+    static Tensor forward(torch::autograd::AutogradContext* ctx, const Tensor& x, const optional<Tensor>& wo,
+                          int64_t nd, double eps) {
         int64_t width = 1;
         for (int64_t i = x.dim() - nd; i < x.dim(); ++i) width *= x.size(i);
-        optional<Tensor> wo;
-        if (w.defined()) wo = w;
+        const Tensor w = wo.has_value() ? *wo : Tensor();
         auto [y, rstd] = rms_forward(x, width, wo, std::nullopt, eps, nd);
         ctx->save_for_backward({x, w, rstd});
         ctx->saved_data["nd"] = nd;
@@ -692,6 +694,28 @@ struct RmsNormFn : public torch::autograd::Function<RmsNormFn> {
         for (int64_t i = x.dim() - nd; i < x.dim(); ++i) dims.push_back(i);
         int64_t width = 1;
         for (auto d : dims) width *= x.size(d);
+        if (g_norms.load() && code_of(x.scalar_type()) != 0 && code_of(x.scalar_type()) != KMI_BOOL &&
+            (!w.defined() || (code_of(w.scalar_type()) != 0 && code_of(w.scalar_type()) != KMI_BOOL)) &&
+            rstd.scalar_type() == at::kFloat && rstd.is_contiguous()) {
+            // The kernels: dx per row, dw as a fixed-order column sum (kmi_rms_norm_bwd).
+            c10::DeviceGuard guard(x.device());
+            const Tensor xc = x.contiguous(), gc = grads[0].to(x.scalar_type()).contiguous();
+            const Tensor wc = w.defined() ? w.contiguous() : Tensor();
+            const int64_t rows = xc.numel() / width;
+            Tensor dx = at::empty_like(xc);
+            Tensor dw = w.defined() ? at::empty_like(wc) : Tensor();
+            size_t ws = 0;
+            check(kmi_rms_norm_bwd_workspace_bytes(rows, width, &ws), "kmi_rms_norm_bwd_workspace_bytes");
+            Tensor work;
+            if (w.defined() && ws) work = at::empty({static_cast<int64_t>(ws)}, xc.options().dtype(at::kByte));
+            check(kmi_rms_norm_bwd(gc.data_ptr(), xc.data_ptr(), w.defined() ? wc.data_ptr() : nullptr,
+                                   rstd.data_ptr<float>(), dx.data_ptr(), w.defined() ? dw.data_ptr() : nullptr, rows,
+                                   width, code_of(xc.scalar_type()), w.defined() ? code_of(wc.scalar_type()) : 0,
+                                   work.defined() ? work.data_ptr() : nullptr, ws, stream_of(xc)),
+                  "kmi_rms_norm_bwd");
+            g_norm_bwd_calls.fetch_add(1);
+            return {dx, dw, Tensor(), Tensor()};
+        }
         Tensor g = grads[0].to(at::kFloat), xf = x.to(at::kFloat);
         Tensor xhat = xf * rstd;
         Tensor gw = w.defined() ? g * w.to(at::kFloat) : g;
@@ -723,7 +747,7 @@ Tensor rms_norm(const Tensor& input, c10::SymIntArrayRef normalized_shape, const
     if (!shape_ok || !norms_take(input, width, {&weight})) return at::compositeimplicitautograd::rms_norm_symint(input, normalized_shape, weight, eps);
     const bool hw = weight && weight->defined();
     const bool grads = at::GradMode::is_enabled() && (input.requires_grad() || (hw && weight->requires_grad()));
-    if (grads) return RmsNormFn::apply(input, hw ? *weight : Tensor(), nd, e);
+    if (grads) return RmsNormFn::apply(input, hw ? weight : optional<Tensor>(), nd, e);
     at::AutoDispatchBelowADInplaceOrView below;
     return std::get<0>(rms_forward(input, width, weight, std::nullopt, e, nd));
 }
@@ -762,11 +786,12 @@ void set_enabled(bool attention, bool norms) {
 
 std::vector<int64_t> counters() {
     return {g_attn_calls.load(), g_attn_declined.load(), g_norm_calls.load(),
-            g_attention.load() ? 1 : 0, g_norms.load() ? 1 : 0, g_attn_bwd_calls.load()};
+            g_attention.load() ? 1 : 0, g_norms.load() ? 1 : 0, g_attn_bwd_calls.load(), g_norm_bwd_calls.load()};
 }
 
 void reset_counters() {
     g_attn_bwd_calls.store(0);
+    g_norm_bwd_calls.store(0);
     g_attn_calls.store(0);
     g_attn_declined.store(0);
     g_norm_calls.store(0);

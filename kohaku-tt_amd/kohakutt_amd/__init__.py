@@ -72,6 +72,7 @@ def counters() -> dict:
         "attention_enabled": bool(c[3]),
         "norms_enabled": bool(c[4]),
         "attention_backward": c[5],
+        "norms_backward": c[6],
     }
 
 

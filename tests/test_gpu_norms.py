@@ -132,3 +132,46 @@ def test_norm_configs_and_repeat_bit_identical(native, dev):
             cpu = F.layer_norm(x, [W], w, b, eps)
         assert torch.equal(y, y2), name
         _check(name, y.cpu(), cpu, torch.from_numpy(yr), torch.bfloat16)
+
+
+@pytest.mark.parametrize(
+    "shape,x_dtype,w_dtype",
+    [
+        ((2048, 896), torch.bfloat16, torch.bfloat16),
+        ((8, 1, 2048), torch.float16, torch.float32),
+        ((3, 5, 77), torch.float32, None),
+        ((4100, 640), torch.bfloat16, torch.bfloat16),
+    ],
+)
+def test_rms_norm_backward_kernels_match_float64(native, dev, shape, x_dtype, w_dtype):
+    """F.rms_norm gradients from the backward kernels (dx per row, dw as a fixed-order
+    column sum over row chunks) against float64 autograd on the CPU; repeat calls are
+    bit-identical."""
+    g = torch.Generator().manual_seed(31 + len(shape))
+    width = shape[-1]
+    x = torch.randn(*shape, generator=g).to(x_dtype)
+    gy = torch.randn(*shape, generator=g).to(x_dtype)
+    w = None if w_dtype is None else (1 + 0.02 * torch.randn(width, generator=g)).to(w_dtype)
+    xd = x.to(dev).requires_grad_()
+    wd = None if w is None else w.to(dev).requires_grad_()
+    native.reset_counters()
+    F.rms_norm(xd, (width,), wd, 1e-6).backward(gy.to(dev))
+    torch.cuda.synchronize()
+    assert native.counters()["norms_backward"] == 1
+    x64 = x.double().requires_grad_()
+    w64 = None if w is None else w.double().requires_grad_()
+    F.rms_norm(x64, (width,), w64, 1e-6).backward(gy.double())
+    pairs = [(xd.grad, x64.grad)] + ([] if w is None else [(wd.grad, w64.grad)])
+    for got, want in pairs:
+        err = (got.cpu().double() - want).abs()
+        scale = want.abs().max().item()
+        tol = 2e-2 if got.dtype in (torch.bfloat16, torch.float16) else 1e-4
+        assert err.max().item() <= tol * max(scale, 1.0), (got.dtype, err.max().item(), scale)
+    first = [t.clone() for t, _ in pairs]
+    xd.grad = None
+    if wd is not None:
+        wd.grad = None
+    F.rms_norm(xd, (width,), wd, 1e-6).backward(gy.to(dev))
+    torch.cuda.synchronize()
+    again = [xd.grad] + ([] if wd is None else [wd.grad])
+    assert all(torch.equal(a, b) for a, b in zip(first, again))
