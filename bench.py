@@ -23,6 +23,7 @@ cores of the same box, a bounded sample timed in the same process, rank 0 only.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -158,6 +159,40 @@ def build_rows():
         "c1_attn_bwd", "extra: C1 attention backward (flash dQ/dK/dV from the forward's lse)", "mfma",
         2.5 * C.attn_flops(64, 14, C.causal_pairs(1, 2048)), None, (bwd_make, bwd_cpu), "attn_bwd_dkdv")
     norm_row("c1_rms", "C1 rms_norm [1,2048,896]", c1["x"], c1["w"], None, 1e-6, "rms")
+
+    def rms_bwd_make(dev, n):
+        # The backward kernels through the C ABI on the current stream (autograd would
+        # launch on the forward's stream, which a graph capture on another stream rejects).
+        from kohakutt_amd import capi
+
+        sets = _rotate(dev, [c1["x"], c1["w"], c1["x"]], n)
+        ws_n = ctypes.c_size_t()
+        capi.check(capi.lib().kmi_rms_norm_bwd_workspace_bytes(2048, 896, ctypes.byref(ws_n)))
+        calls = []
+        for s in sets:
+            x, w, gy = s
+            x2 = x.reshape(2048, 896)
+            rstd = (x2.float().pow(2).mean(-1) + 1e-6).rsqrt().contiguous()
+            dx, dw = torch.empty_like(x2), torch.empty_like(w)
+            ws = torch.empty(max(ws_n.value, 1), dtype=torch.uint8, device=dev)
+
+            def call(x2=x2, w=w, gy=gy, rstd=rstd, dx=dx, dw=dw, ws=ws):
+                capi.check(capi.lib().kmi_rms_norm_bwd(
+                    gy.data_ptr(), x2.data_ptr(), w.data_ptr(), rstd.data_ptr(), dx.data_ptr(), dw.data_ptr(),
+                    2048, 896, capi.KMI_BF16, capi.KMI_BF16, ws.data_ptr(), ws_n.value,
+                    torch.cuda.current_stream().cuda_stream))
+            calls.append(call)
+        return calls
+
+    def rms_bwd_cpu():
+        x, w = (t.detach().clone().requires_grad_() for t in (c1["x"], c1["w"]))
+        y = F.rms_norm(x, [896], w, 1e-6)
+        return lambda: torch.autograd.grad(y, (x, w), c1["x"], retain_graph=True)
+
+    # Bytes: dy and x read, dx written (M W 2 each), weight read and dweight written, rstd read.
+    rows["c1_rms_bwd"] = Row(
+        "c1_rms_bwd", "extra: C1 rms_norm backward [1,2048,896] (dx, dweight)", "hbm", None,
+        3 * 2048 * 896 * 2 + 2 * 896 * 2 + 2048 * 4, (rms_bwd_make, rms_bwd_cpu), "rms_bwd_rows")
 
     c2 = C.config2(1)
     norm_row("c2_ln", "C2 layer_norm [1,197,768]", c2["x"], c2["w"], c2["b"], 1e-6, "ln")
