@@ -399,40 +399,42 @@ bool aligned(const void* p, int64_t bytes) {
 // its column sum for the weight, colsum_*; layernorm.md:90-102).  y = x r w with
 // r = rstd of the row: dx = r (g w) - x r^3 mean(g w x), dw = sum over rows of g x r.
 // dx: one 256-thread block per row, fp32 sums; any width and alignment.
-__global__ __launch_bounds__(256) void rms_bwd_rows(const void* dy, const void* x, const void* weight,
-                                                    const float* rstd, void* dx, int64_t width, int x_dtype,
-                                                    int w_dtype) {
+template <typename T>
+__global__ __launch_bounds__(256) void rms_bwd_rows(const T* dy, const T* x, const void* weight, const float* rstd,
+                                                    T* dx, int64_t width, int w_dtype) {
     __shared__ float scratch[4];
     const int64_t row = blockIdx.x;
     const int64_t base = row * width;
     float s = 0.f;
+#pragma unroll 4
     for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
-        float gw = load_any(dy, x_dtype, base + i);
+        float gw = to_f32(dy[base + i]);
         if (weight) gw *= load_any(weight, w_dtype, i);
-        s += gw * load_any(x, x_dtype, base + i);
+        s += gw * to_f32(x[base + i]);
     }
     s = block_sum(s, scratch);
     const float r = rstd[row];
     const float c = r * r * r * s / static_cast<float>(width);
+#pragma unroll 4
     for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
-        float gw = load_any(dy, x_dtype, base + i);
+        float gw = to_f32(dy[base + i]);
         if (weight) gw *= load_any(weight, w_dtype, i);
-        store_any(dx, x_dtype, base + i, r * gw - load_any(x, x_dtype, base + i) * c);
+        dx[base + i] = from_f32<T>(r * gw - to_f32(x[base + i]) * c);
     }
 }
 
 // dw, first stage: block (column group, chunk) sums g x r over the chunk's rows for 256
 // consecutive columns (coalesced across the threads) into fp32 partials [chunk][width].
-__global__ __launch_bounds__(256) void rms_bwd_dw_partial(const void* dy, const void* x, const float* rstd,
-                                                          float* part, int64_t rows, int64_t width,
-                                                          int64_t rows_per_chunk, int x_dtype) {
+template <typename T>
+__global__ __launch_bounds__(256) void rms_bwd_dw_partial(const T* dy, const T* x, const float* rstd, float* part,
+                                                          int64_t rows, int64_t width, int64_t rows_per_chunk) {
     const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (col >= width) return;
     const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
     const int64_t r1 = r0 + rows_per_chunk < rows ? r0 + rows_per_chunk : rows;
     float acc = 0.f;
-    for (int64_t r = r0; r < r1; ++r)
-        acc += load_any(dy, x_dtype, r * width + col) * load_any(x, x_dtype, r * width + col) * rstd[r];
+#pragma unroll 8
+    for (int64_t r = r0; r < r1; ++r) acc += to_f32(dy[r * width + col]) * to_f32(x[r * width + col]) * rstd[r];
     part[static_cast<int64_t>(blockIdx.y) * width + col] = acc;
 }
 
@@ -442,12 +444,30 @@ __global__ __launch_bounds__(256) void rms_bwd_dw_final(const float* part, void*
     const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (col >= width) return;
     float acc = 0.f;
+#pragma unroll 8
     for (int64_t c = 0; c < chunks; ++c) acc += part[c * width + col];
     store_any(dw, w_dtype, col, acc);
 }
 
-constexpr int64_t kRmsBwdRowsPerChunk = 64;
-constexpr int64_t kRmsBwdMaxChunks = 1024;
+constexpr int64_t kRmsBwdRowsPerChunk = 16;
+constexpr int64_t kRmsBwdMaxChunks = 4096;
+
+template <typename T>
+hipError_t launch_rms_bwd(const void* dy, const void* x, const void* weight, const float* rstd, void* dx,
+                          void* dweight, int64_t rows, int64_t width, int w_dtype, float* part, int64_t chunks,
+                          hipStream_t s) {
+    hipLaunchKernelGGL((rms_bwd_rows<T>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+                       static_cast<const T*>(dy), static_cast<const T*>(x), weight, rstd, static_cast<T*>(dx), width,
+                       w_dtype);
+    if (dweight) {
+        const unsigned gx = static_cast<unsigned>(ceil_div(width, 256));
+        hipLaunchKernelGGL((rms_bwd_dw_partial<T>), dim3(gx, static_cast<unsigned>(chunks)), dim3(256), 0, s,
+                           static_cast<const T*>(dy), static_cast<const T*>(x), rstd, part, rows, width,
+                           ceil_div(rows, chunks));
+        hipLaunchKernelGGL(rms_bwd_dw_final, dim3(gx), dim3(256), 0, s, part, dweight, chunks, width, w_dtype);
+    }
+    return hipGetLastError();
+}
 
 int64_t rms_bwd_chunks(int64_t rows) {
     return std::min<int64_t>(kRmsBwdMaxChunks, std::max<int64_t>(1, ceil_div(rows, kRmsBwdRowsPerChunk)));
@@ -561,15 +581,13 @@ extern "C" int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weigh
         return fail(KMI_EWORKSPACE, std::string(name) + ": workspace missing or smaller than "
                                                         "kmi_rms_norm_bwd_workspace_bytes");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(rms_bwd_rows, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, dy, x, weight, rstd, dx,
-                       width, static_cast<int>(x_dtype), static_cast<int>(w_dtype));
-    if (dweight) {
-        float* part = static_cast<float*>(workspace);
-        const unsigned gx = static_cast<unsigned>(ceil_div(width, 256));
-        hipLaunchKernelGGL(rms_bwd_dw_partial, dim3(gx, static_cast<unsigned>(chunks)), dim3(256), 0, s, dy, x, rstd,
-                           part, rows, width, ceil_div(rows, chunks), static_cast<int>(x_dtype));
-        hipLaunchKernelGGL(rms_bwd_dw_final, dim3(gx), dim3(256), 0, s, part, dweight, chunks, width,
-                           static_cast<int>(w_dtype));
+    float* part = static_cast<float*>(workspace);
+    const int wd = static_cast<int>(w_dtype);
+    hipError_t err;
+    switch (x_dtype) {
+        case KMI_BF16: err = launch_rms_bwd<bf16>(dy, x, weight, rstd, dx, dweight, rows, width, wd, part, chunks, s); break;
+        case KMI_F16: err = launch_rms_bwd<f16>(dy, x, weight, rstd, dx, dweight, rows, width, wd, part, chunks, s); break;
+        default: err = launch_rms_bwd<float>(dy, x, weight, rstd, dx, dweight, rows, width, wd, part, chunks, s);
     }
-    return hip_status(hipGetLastError(), name);
+    return hip_status(err, name);
 }
