@@ -139,3 +139,20 @@ def test_backward_rejects_malformed_calls_before_launch():
     # fp32 row dot products, then (GQA) the dK / dV partials of every query head.
     assert n.value == (4 * 8 + 2 * 4 * 8 * 64) * 4
     assert capi.lib().kmi_attn_bwd(ctypes.byref(a), None, 0, None) == capi.KMI_EWORKSPACE
+
+
+def test_rms_norm_backward_rejects_malformed_calls_before_launch():
+    lib = capi.lib()
+    n = ctypes.c_size_t()
+    assert lib.kmi_rms_norm_bwd_workspace_bytes(2048, 896, ctypes.byref(n)) == capi.KMI_OK
+    assert n.value == 128 * 896 * 4  # 16-row chunks of fp32 column sums
+    assert lib.kmi_rms_norm_bwd_workspace_bytes(-1, 896, ctypes.byref(n)) == capi.KMI_EINVAL
+    p = 0x1000
+    # Unknown dtype, null operands, dweight without weight, missing workspace.
+    assert lib.kmi_rms_norm_bwd(p, p, p, p, p, p, 4, 64, 9, capi.KMI_BF16, None, 0, None) == capi.KMI_EINVAL
+    assert lib.kmi_rms_norm_bwd(None, p, p, p, p, p, 4, 64, capi.KMI_BF16, capi.KMI_BF16, None, 0, None) == capi.KMI_EINVAL
+    assert lib.kmi_rms_norm_bwd(p, p, None, p, p, p, 4, 64, capi.KMI_BF16, 0, None, 0, None) == capi.KMI_EINVAL
+    assert "dweight needs weight" in lib.kmi_last_error().decode()
+    assert lib.kmi_rms_norm_bwd(p, p, p, p, p, p, 4, 64, capi.KMI_BF16, capi.KMI_BF16, None, 0, None) == capi.KMI_EWORKSPACE
+    # No rows: nothing to do.
+    assert lib.kmi_rms_norm_bwd(p, p, p, p, p, p, 0, 64, capi.KMI_BF16, capi.KMI_BF16, None, 0, None) == capi.KMI_OK
