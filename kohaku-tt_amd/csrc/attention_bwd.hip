@@ -6,15 +6,15 @@
 // 1208-1281).  Here, for unmasked dense calls (causal top-left or not, GQA, head dim 64
 // or 128, bf16 / fp16):
 //
-//   attn_bwd_pre     Dr[row] = sum_d dO[row, d] * O[row, d]   (fp32)
+//   attn_bwd_dq      one workgroup per (sequence, query head, 64-row block): the row dots
+//                    Dr = sum_d dO O (fp32, kept for the next kernel), then over the key
+//                    tiles it sees P = exp2(c S - lse2), dP = dO V^T, dS = P (dP - Dr),
+//                    dQ += dS K
 //   attn_bwd_dkdv    one workgroup per (sequence, query head, 64-key tile): for every
-//                    32-row query block that sees the tile, P = exp2(c S - lse2),
-//                    dP = dO V^T, dS = P (dP - Dr); dV += P^T dO, dK += dS^T Q (fp32
-//                    accumulators in registers).  Without GQA it writes dK / dV; with GQA
-//                    fp32 per-query-head partials that
-//   attn_bwd_group_sum sums over each K/V head's query heads in a fixed order (no atomics)
-//   attn_bwd_dq      one workgroup per (sequence, query head, 64-row block): over the key
-//                    tiles it sees, the same P / dS, dQ += dS K
+//                    32-row query block that sees the tile the same P / dS; dV += P^T dO,
+//                    dK += dS^T Q (fp32 accumulators in registers).  Without GQA or query
+//                    splits it writes dK / dV; otherwise fp32 partials that
+//   attn_bwd_group_sum adds over each K/V head's query heads in a fixed order (no atomics)
 //
 // S = Q K^T, dP = dO V^T and the three gradient products run on
 // v_mfma_f32_16x16x32_{bf16,f16}.  Every operand is read from LDS along its contraction
@@ -105,24 +105,6 @@ __device__ __forceinline__ void store_regs(const TileRegs<D>& t, T* dst, T* dstT
             for (int i = 0; i < 8; ++i) dstT[(8 * ch + i) * TP + r] = e[i];
         }
     }
-}
-
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_pre(const BwdParams p) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int64_t rows = static_cast<int64_t>(p.batch) * p.hq * p.seq_q;
-    if (row >= rows) return;
-    const int i = static_cast<int>(row % p.seq_q);
-    const int h = static_cast<int>((row / p.seq_q) % p.hq);
-    const int b = static_cast<int>(row / (static_cast<int64_t>(p.seq_q) * p.hq));
-    const T* o = static_cast<const T*>(p.o) + b * p.os[0] + h * p.os[1] + i * p.os[2];
-    const T* d = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1] + i * p.dos[2];
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < D / 64; ++j) s += to_f32(o[lane + 64 * j]) * to_f32(d[lane + 64 * j]);
-    s = wave_sum(s);
-    if (lane == 0) p.dr[row] = s;
 }
 
 template <typename T, int D>
@@ -340,28 +322,39 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int rw0 = r0 + 16 * wave;  // this wavefront's first row
 
     // Q / dO fragments: lane (g4, l16) holds row rw0 + l16, dims 32 c + 8 g4 .. + 7; the
-    // row statistics of row rw0 + 4 g4 + j (the rows of its accumulator lanes).
+    // row statistics of row rw0 + 4 g4 + j (the rows of its accumulator lanes).  The row
+    // dot D = sum(dO * O) is formed here from the same dO fragments and written for the
+    // dK / dV kernel, which runs after this one.
     v8 qf[DC], of[DC];
+    float rdot = 0.f;
     {
         const int row = rw0 + l16;
         const int rc = min(row, p.seq_q - 1);
         const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1] + static_cast<int64_t>(rc) * p.qs[2];
         const T* op = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1] + static_cast<int64_t>(rc) * p.dos[2];
+        const T* outp = static_cast<const T*>(p.o) + b * p.os[0] + h * p.os[1] + static_cast<int64_t>(rc) * p.os[2];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
             const u32x4 qx = *reinterpret_cast<const u32x4*>(qp + 32 * c + 8 * g4);
             const u32x4 ox = *reinterpret_cast<const u32x4*>(op + 32 * c + 8 * g4);
+            const v8 yv = *reinterpret_cast<const v8*>(outp + 32 * c + 8 * g4);
             qf[c] = __builtin_bit_cast(v8, row < p.seq_q ? qx : u32x4{0u, 0u, 0u, 0u});
             of[c] = __builtin_bit_cast(v8, row < p.seq_q ? ox : u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+            for (int e = 0; e < 8; ++e) rdot += to_f32(of[c][e]) * to_f32(yv[e]);
         }
     }
+    // The four lanes of a row (g4 = 0..3) each hold a quarter of its dims.
+    rdot += __shfl_xor(rdot, 16, kWave);
+    rdot += __shfl_xor(rdot, 32, kWave);
+    if (ksp == 0 && g4 == 0 && rw0 + l16 < p.seq_q) p.dr[(static_cast<int64_t>(b) * p.hq + h) * p.seq_q + rw0 + l16] = rdot;
     float l2[4], drv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int row = rw0 + 4 * g4 + j;
         const int rc = min(row, p.seq_q - 1);
         const float lv = p.lse[b * p.ls[0] + h * p.ls[1] + static_cast<int64_t>(rc) * p.ls[2]];
-        const float dv = p.dr[(static_cast<int64_t>(b) * p.hq + h) * p.seq_q + rc];
+        const float dv = __shfl(rdot, 4 * g4 + j, kWave);  // lane 4 g4 + j holds that row's dot
         // Rows past the end: lse2 = +inf makes their P exactly 0.
         l2[j] = row < p.seq_q ? lv * kLog2e : INFINITY;
         drv[j] = row < p.seq_q ? dv : 0.f;
@@ -473,13 +466,13 @@ const char* check_bwd(const kmi_attn_bwd_args* a) {
     const void* ptrs[] = {a->q, a->k, a->v, a->out, a->grad_out, a->lse, a->grad_q, a->grad_k, a->grad_v};
     for (const void* ptr : ptrs)
         if (!ptr) return "null tensor pointer";
-    const void* vec[] = {a->q, a->k, a->v, a->grad_out};
+    const void* vec[] = {a->q, a->k, a->v, a->out, a->grad_out};
     for (const void* ptr : vec)
-        if (reinterpret_cast<uintptr_t>(ptr) % 16) return "q, k, v and grad_out must be 16-byte aligned";
-    const int64_t* strides[] = {a->q_stride, a->k_stride, a->v_stride, a->do_stride};
+        if (reinterpret_cast<uintptr_t>(ptr) % 16) return "q, k, v, out and grad_out must be 16-byte aligned";
+    const int64_t* strides[] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride, a->do_stride};
     for (const int64_t* s : strides)
         for (int i = 0; i < 3; ++i)
-            if (s[i] < 0 || s[i] % 8) return "q, k, v and grad_out strides must be non-negative multiples of 8";
+            if (s[i] < 0 || s[i] % 8) return "q, k, v, out and grad_out strides must be non-negative multiples of 8";
     return nullptr;
 }
 
@@ -521,17 +514,8 @@ size_t bwd_ws_bytes(const kmi_attn_bwd_args* a) {
 
 template <typename T, int D>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
-    const int64_t rows = static_cast<int64_t>(p.batch) * p.hq * p.seq_q;
-    hipLaunchKernelGGL((attn_bwd_pre<T, D>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, s, p);
     const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, QW);
-    hipLaunchKernelGGL((attn_bwd_dkdv<T, D>),
-                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk * p.qsplit)),
-                       dim3(BWD_THREADS), 0, s, p);
-    if (p.pdk) {
-        const int64_t items = static_cast<int64_t>(p.batch) * p.hkv * p.seq_k * (D / 4);
-        hipLaunchKernelGGL((attn_bwd_group_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0,
-                           s, p);
-    }
+    // dQ first: it writes the row dots that dK / dV read.
     hipLaunchKernelGGL((attn_bwd_dq<T, D>),
                        dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit)),
                        dim3(BWD_THREADS), 0, s, p);
@@ -539,6 +523,14 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
         const int64_t items = static_cast<int64_t>(p.batch) * p.hq * p.seq_q * (D / 4);
         hipLaunchKernelGGL((attn_bwd_dq_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0, s,
                            p);
+    }
+    hipLaunchKernelGGL((attn_bwd_dkdv<T, D>),
+                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk * p.qsplit)),
+                       dim3(BWD_THREADS), 0, s, p);
+    if (p.pdk) {
+        const int64_t items = static_cast<int64_t>(p.batch) * p.hkv * p.seq_k * (D / 4);
+        hipLaunchKernelGGL((attn_bwd_group_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0,
+                           s, p);
     }
     return hipGetLastError();
 }

@@ -273,7 +273,7 @@ std::tuple<Tensor, Tensor, Tensor> flash_backward(const Tensor& grad_out_in, con
                                                   bool is_causal, optional<double> scale) {
     const Tensor q = kernel_operand(q_in, 2), k = kernel_operand(k_in, 2), v = kernel_operand(v_in, 2);
     const Tensor go = kernel_operand(grad_out_in, 2);
-    const Tensor o = out_in.stride(3) == 1 ? out_in : out_in.contiguous();
+    const Tensor o = kernel_operand(out_in, 2);
     const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3), Hk = k.size(1), Sk = k.size(2);
     Tensor dq = at::empty({B, H, Sq, D}, q.options());
     Tensor dk = at::empty({B, Hk, Sk, D}, k.options());
