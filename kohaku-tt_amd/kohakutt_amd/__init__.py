@@ -23,8 +23,6 @@ from pathlib import Path
 
 import torch
 
-from .stats import diff_stats, format_stats  # noqa: F401
-
 _PKG = Path(__file__).resolve().parent
 CAPI_LIB = _PKG / "libkohakutt_amd.so"
 OPS_LIB = _PKG / "_torch_ops.so"

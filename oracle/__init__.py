@@ -15,9 +15,11 @@ Everything here is float64 numpy, restating the reference's semantics:
   mask and a per-sequence block-packed additive mask.
 * ``norms.layer_norm`` / ``norms.rms_norm`` -- LayerNorm and RMSNorm over the last dim,
   with the statistics the reference's kernels return.
+* ``ruler.diff_stats`` -- the float64 ruler: error statistics of a result against the
+  float64 reference (the median relative error is what the parity bar bounds).
 
 Pinning (which checks hold each function to something independent of this code) is
 listed in each module's header.
 """
 
-from . import attention, norms  # noqa: F401
+from . import attention, norms, ruler  # noqa: F401

@@ -133,7 +133,7 @@ def ruler_ok(gpu, cpu_same_dtype, ref64, factor=1.5, floor=0.0):
     """(ok, gpu stats, cpu stats): the GPU's median relative error against float64 is at
     most ``factor`` times the CPU same-dtype error (plus ``floor``), with no non-finite
     values.  The tolerance of the benchmark plan is factor 1.5."""
-    from kohakutt_amd import diff_stats
+    from oracle.ruler import diff_stats
 
     sg = diff_stats(gpu, ref64)
     sc = diff_stats(cpu_same_dtype, ref64)

@@ -55,10 +55,10 @@ def test_oracle_norms_match_golden():
 
 
 def _ruler(gpu, cpu, ref):
-    import kohakutt_amd
+    from oracle.ruler import diff_stats
 
-    sg = kohakutt_amd.diff_stats(gpu, torch.from_numpy(ref))
-    sc = kohakutt_amd.diff_stats(cpu, torch.from_numpy(ref))
+    sg = diff_stats(gpu, ref)
+    sc = diff_stats(cpu, ref)
     assert sg["nonfinite"] == 0 and sg["rel_median"] <= 1.5 * sc["rel_median"], (sg, sc)
 
 
