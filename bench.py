@@ -232,7 +232,7 @@ def build_rows():
             sets = _rotate(dev, [c4["q"], c4["k"], c4["v"], cu_t, mask], n)
             mx = max(L)
             return [
-                (lambda s=s: torch.ops.ktt._sdpa_varlen(s[0], s[1], s[2], s[3], s[3], mx, mx, True, None, None, s[4]))
+                (lambda s=s: torch.ops.ktt._sdpa_varlen_offsets(s[0], s[1], s[2], s[3], s[3], mx, mx, True, None, None, s[4]))
                 for s in sets
             ]
 

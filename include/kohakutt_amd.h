@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KMI_ABI_VERSION 2
+#define KMI_ABI_VERSION 3
 
 /* Element types of operands. */
 enum kmi_dtype {
@@ -77,7 +77,8 @@ enum kmi_mask_mode {
  *   its row keeps any key and a fully-masked row is the softmax over its raw scores.
  * lse (optional, fp32, natural log): dense [B, Hq, Sq] / varlen [Hq, Tq] with strides
  *   lse_stride (batch, head, seq); varlen ignores lse_stride[0].
- * Supported: dtype BF16 or F16, head_dim 64 or 128, heads_kv dividing heads_q.
+ * Supported: dtype BF16 or F16, head_dim a multiple of 8 up to 256, heads_kv dividing
+ * heads_q.
  */
 typedef struct kmi_attn_args {
     const void* q;
@@ -117,6 +118,9 @@ typedef struct kmi_attn_args {
      * reference's bridge::sdpa_lengths behind ktt::_sdpa_lengths (aten_lengths.cpp:69-101,
      * 175-197; docs/reference/kernels/flash.md, Key lengths). */
     const int32_t* key_lengths;
+    /* ABI 3, varlen with KMI_MASK_PACKED (NULL: the kernels add up the block sizes): device
+     * int64 [batch + 1], entry i = sum_{j<i} Lq_j * Lk_j, where sequence i's block starts. */
+    const int64_t* mask_offsets;
 } kmi_attn_args;
 
 /* Bytes of workspace kmi_attn_fwd needs for `args` (0 when it does not split). */
@@ -127,17 +131,23 @@ int kmi_attn_fwd(const kmi_attn_args* args, void* workspace, size_t workspace_by
                  void* stream);
 
 /*
- * Attention backward of an unmasked dense call (causal top-left or not):
- *   dq, dk, dv of out = softmax(scale * q k^T) v given grad_out and the forward's lse
- *   (fp32 natural log, as kmi_attn_fwd writes it).  The probabilities are recomputed per
- *   tile from lse; nothing of size Sq x Sk is stored.  GQA: dk / dv of a K/V head sum its
- *   query heads.  Layouts as kmi_attn_fwd's dense ones (element strides of the batch, head
- *   and sequence dims, head-dim stride 1); q, k, v, grad_out 16-byte aligned with strides
- *   multiples of 8.  Workspace: kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row
- *   dot products; with GQA or split query ranges also fp32 dK / dV partials).
+ * Attention backward of a kmi_attn_fwd call (dense or varlen, causal or not, masked or
+ * not): dq, dk, dv of out = softmax(scale * q k^T + mask) v given grad_out and the
+ * forward's lse (fp32 natural log, as kmi_attn_fwd writes it).  The probabilities are
+ * recomputed per tile from lse with the forward's mask rules (a row whose lse carries the
+ * -5e5 offset of a fully-masked row takes its raw scores); nothing of size Sq x Sk is
+ * stored.  GQA: dk / dv of a K/V head sum its query heads.  Layouts as kmi_attn_fwd's
+ * (dense: element strides of the batch, head and sequence dims; varlen: [T, H, D] with
+ * stride[1] the head and stride[2] the token stride, lse [Hq, Tq]); head-dim stride 1;
+ * q, k, v, out, grad_out 16-byte aligned with strides multiples of 8.  Masks take the
+ * forward's modes and strides and get no gradient.  Workspace:
+ * kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row dot products; with GQA or split
+ * query / key ranges also fp32 dK / dV and dQ partials, added in a fixed order).
  * Replaces the reference's flash backward behind tt_sdpa_overrideable_backward's stats
  * route (aten_attention.cpp:716-812; bridge in device_attention.cpp:1208-1281;
- * docs/reference/kernels/flash.md:151-206).  Supported: BF16 / F16, head_dim 64 or 128.
+ * docs/reference/kernels/flash.md:151-206) and its packed backward behind
+ * ktt::_sdpa_varlen_backward (aten_varlen.cpp:237-319).  Supported: BF16 / F16, head
+ * dims that are multiples of 8 up to 256.
  */
 typedef struct kmi_attn_bwd_args {
     const void* q;
@@ -162,6 +172,19 @@ typedef struct kmi_attn_bwd_args {
     int64_t dv_stride[3];
     int64_t lse_stride[3];
     double scale;
+    /* ABI 3: the forward's mask (as in kmi_attn_args) and varlen offsets (cu_seqlens_q !=
+     * NULL: `batch` packed sequences, seq_q / seq_k the longest lengths). */
+    const void* mask;
+    int32_t mask_dtype;
+    int32_t mask_mode;
+    int64_t mask_stride[4];
+    int64_t mask_numel;
+    const int64_t* mask_offsets;
+    const int32_t* cu_seqlens_q;
+    const int32_t* cu_seqlens_k;
+    int64_t total_q, total_k;
+    /* Dense calls only (NULL: every key): the forward's key_lengths (kmi_attn_args). */
+    const int32_t* key_lengths;
 } kmi_attn_bwd_args;
 
 /* Bytes of workspace kmi_attn_bwd needs for `args`. */

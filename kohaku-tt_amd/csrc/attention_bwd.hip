@@ -3,22 +3,28 @@
 // The reference's training route recomputes the probabilities from the forward's row
 // statistics and runs a dQ pass and a dK/dV pass (docs/reference/kernels/flash.md,
 // "Backward", flash.md:151-206; ktt_flash/bw_*.cpp; bridge in device_attention.cpp:
-// 1208-1281).  Here, for unmasked dense calls (causal top-left or not, GQA, head dim 64
-// or 128, bf16 / fp16):
+// 1208-1281), for dense calls and for packed sequences (aten_varlen.cpp:237-319, with a
+// key mask).  Here, for dense and packed (varlen) calls, causal or not, with or without a
+// mask (the forward's modes), GQA, any head dim that is a multiple of 8 up to 256 (padded
+// to DP with zeros in registers), bf16 / fp16:
 //
 //   attn_bwd_dq      one workgroup per (sequence, query head, 64-row block): the row dots
 //                    Dr = sum_d dO O (fp32, kept for the next kernel), then over the key
-//                    tiles it sees P = exp2(c S - lse2), dP = dO V^T, dS = P (dP - Dr),
-//                    dQ += dS K
-//   attn_bwd_dkdv    one workgroup per (sequence, query head, 64-key tile): for every
-//                    32-row query block that sees the tile the same P / dS; dV += P^T dO,
-//                    dK += dS^T Q (fp32 accumulators in registers).  Without GQA or query
-//                    splits it writes dK / dV; otherwise fp32 partials that
-//   attn_bwd_group_sum adds over each K/V head's query heads in a fixed order (no atomics)
+//                    tiles it sees P = exp2(c S + mask - lse2), dP = dO V^T,
+//                    dS = P (dP - Dr), dQ += dS K
+//   attn_bwd_dkdv    one workgroup per (sequence, K/V head, 64-key tile, split): over the
+//                    (query head of the group, 32-row query block) items that see the
+//                    tile -- split s takes items s, s + splits, ... -- the same P / dS;
+//                    dV += P^T dO, dK += dS^T Q in fp32 registers.  One split: it
+//                    writes dK / dV; several: fp32 partials per split that
+//   attn_bwd_kv_sum  adds in split order (no atomics: repeat calls are bit-identical)
 //
+// Probabilities follow the forward exactly: keys past the causal limit or masked
+// (logit <= -5e5) get P = 0; a row whose lse carries the -5e5 offset of a fully-masked
+// row (the forward ran it over its raw scores) takes every visible key's raw score.
 // S = Q K^T, dP = dO V^T and the three gradient products run on
-// v_mfma_f32_16x16x32_{bf16,f16}.  Every operand is read from LDS along its contraction
-// index (16 contiguous bytes per lane): tiles needed with either index contiguous are
+// v_mfma_f32_16x16x32_{bf16,f16}; every operand is read from LDS along its contraction
+// index (16 contiguous bytes per lane), so tiles needed with either index contiguous are
 // staged twice, row-major and transposed.  lse is the forward's natural-log row LSE.
 #include <algorithm>
 
@@ -31,6 +37,8 @@ constexpr int BT = 32;          // keys per K/V tile and rows per query block
 constexpr int TP = BT + 8;      // pitch of transposed / [32][32] tiles (elements)
 constexpr int BWD_THREADS = 256;
 constexpr float kLog2e = 1.4426950408889634f;
+// A forward lse below this carries the -5e5 offset of a row with no kept key.
+constexpr float kRawLse = 0.5f * kMaskedLogit;
 
 template <typename T>
 struct BwdMfma;
@@ -53,52 +61,151 @@ struct BwdParams {
     const void *q, *k, *v, *o, *dout;
     const float* lse;
     void *dq, *dk, *dv;
-    float* dr;  // [batch][hq][seq_q] fp32 workspace
-    // GQA (group > 1): per-query-head dK / dV partials [batch][hq][seq_k][D] fp32, summed
-    // over each group by attn_bwd_group_sum; null when every K/V head has one query head.
+    float* dr;  // [hq][rows_total] fp32 row dots
+    // dK / dV partials [hkv][splits][keys_total][DP] fp32 (splits > 1), else null.
     float *pdk, *pdv;
-    // dK / dV workgroups per (query head, key tile): split q takes query blocks q, q + qsplit,
-    // ...; with qsplit > 1 every split writes fp32 partials (indexed [b][h][split][key][D]).
-    int qsplit;
-    // dQ workgroups per (query head, row block): split k takes key tiles k, k + ksplit, ...;
-    // with ksplit > 1 every split writes fp32 partials pdq [b][h][split][row][D].
-    int ksplit;
+    // dQ partials [hq][ksplit][rows_total][DP] fp32 (ksplit > 1), else null.
     float* pdq;
+    int splits, ksplit;
     int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3], ls[3];
-    int batch, hq, hkv, group, seq_q, seq_k, causal;
+    const void* mask;
+    int64_t ms[4];
+    int64_t mask_numel;
+    int mask_mode;
+    const int64_t* mask_off;
+    const int32_t *cu_q, *cu_k;
+    const int32_t* klen;  // dense key lengths [batch] (or null)
+    int total_q, total_k;
+    int batch, hq, hkv, group, seq_q, seq_k, causal, d;
+    int64_t rows_total, keys_total;
     float scale, c2;  // c2 = scale * log2(e)
 };
 
-// Staging of rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) in two steps:
-// loads into registers (D / 64 16-byte chunks per thread, zeros past the end), issued a
-// tile ahead, and their LDS stores, row-major at pitch D + 8 and, when dstT is set,
-// transposed ([D][TP]).  Consecutive lanes take consecutive rows of one 8-column chunk, so
-// the transposed 2-byte stores of a wavefront spread over the banks (with consecutive
-// chunks per lane every chunk's column block starts on the same bank).
-template <int D>
-struct TileRegs {
-    u32x4 v[D / 64];
+// One sequence's geometry: query rows [q0, q0 + lq) and keys [k0, k0 + lk) of the packed
+// (varlen) tensors, or the whole batch entry (dense); causal: row i sees keys
+// j <= i + coff (top-left dense: coff = 0; bottom-right varlen: coff = lk - lq).
+struct Geo {
+    int q0, lq, k0, lk, coff;
+    int64_t row_base, key_base;       // row / key index in [rows_total] / [keys_total]
+    int64_t qb, kb, vb, ob, dob, dqb, dkb, dvb, lb;  // batch-entry element offsets (dense)
+    int64_t mbase;                    // the mask element of (head 0, row 0, key 0)
+    int64_t mrow;                     // mask elements per query row
+    int64_t mkey;                     // mask elements per key
+    int64_t mend;                     // mask elements (reads at or past it count as masked)
 };
 
-template <typename T, int D>
-__device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int nrows, TileRegs<D>& t) {
-#pragma unroll
-    for (int j = 0; j < D / 64; ++j) {
-        const int c = threadIdx.x + BWD_THREADS * j;
-        const int r = c % BT, ch = c / BT;
-        const int row = min(r0 + r, nrows - 1);  // in range; rows past the end are dropped below
-        const u32x4 val = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(row) * rs + 8 * ch);
-        t.v[j] = r0 + r < nrows ? val : u32x4{0u, 0u, 0u, 0u};
+__device__ __forceinline__ Geo geo_of(const BwdParams& p, int seq) {
+    Geo g;
+    if (p.cu_q) {
+        g.q0 = min(max(p.cu_q[seq], 0), p.total_q);
+        g.lq = min(min(max(p.cu_q[seq + 1], g.q0), p.total_q) - g.q0, p.seq_q);
+        g.k0 = min(max(p.cu_k[seq], 0), p.total_k);
+        g.lk = min(min(max(p.cu_k[seq + 1], g.k0), p.total_k) - g.k0, p.seq_k);
+        g.coff = g.lk - g.lq;
+        g.row_base = g.q0;
+        g.key_base = g.k0;
+        g.qb = g.kb = g.vb = g.ob = g.dob = g.dqb = g.dkb = g.dvb = g.lb = 0;
+    } else {
+        g.q0 = 0;
+        g.lq = p.seq_q;
+        g.k0 = 0;
+        g.lk = p.klen ? min(max(p.klen[seq], 1), p.seq_k) : p.seq_k;
+        g.coff = 0;
+        g.row_base = static_cast<int64_t>(seq) * p.seq_q;
+        g.key_base = static_cast<int64_t>(seq) * p.seq_k;
+        g.qb = seq * p.qs[0];
+        g.kb = seq * p.ks[0];
+        g.vb = seq * p.vs[0];
+        g.ob = seq * p.os[0];
+        g.dob = seq * p.dos[0];
+        g.dqb = seq * p.dqs[0];
+        g.dkb = seq * p.dks[0];
+        g.dvb = seq * p.dvs[0];
+        g.lb = seq * p.ls[0];
+    }
+    g.mbase = 0;
+    g.mrow = 0;
+    g.mkey = 0;
+    g.mend = INT64_MAX;
+    if (p.mask_mode == KMI_MASK_PACKED) {
+        int64_t off = 0;
+        if (p.mask_off) {
+            off = p.mask_off[seq];
+        } else {
+            for (int s = 0; s < seq; ++s) {
+                const int a0 = min(max(p.cu_q[s], 0), p.total_q), a1 = min(max(p.cu_q[s + 1], a0), p.total_q);
+                const int b0 = min(max(p.cu_k[s], 0), p.total_k), b1 = min(max(p.cu_k[s + 1], b0), p.total_k);
+                off += static_cast<int64_t>(a1 - a0) * (b1 - b0);
+            }
+        }
+        g.mbase = off;
+        g.mrow = g.lk;
+        g.mkey = 1;
+        g.mend = p.mask_numel;
+    } else if (p.mask_mode == KMI_MASK_STRIDED) {
+        g.mbase = p.cu_q ? static_cast<int64_t>(g.q0) * p.ms[2] + static_cast<int64_t>(g.k0) * p.ms[3] : seq * p.ms[0];
+        g.mrow = p.ms[2];
+        g.mkey = p.ms[3];
+    }
+    return g;
+}
+
+// The mask logit of (head h, row i, key j) of a sequence (0 without a mask).
+template <int MK>
+__device__ __forceinline__ float mask_at(const BwdParams& p, const Geo& g, int h, int i, int j) {
+    if constexpr (MK == MK_NONE) {
+        return 0.f;
+    } else {
+        typedef typename MaskRaw<MK>::type R;
+        const int64_t idx = g.mbase + h * p.ms[1] + i * g.mrow + j * g.mkey;
+        if (idx >= g.mend) return kMaskedLogit;
+        return mask_logit_of<MK>(static_cast<const R*>(p.mask)[idx]);
     }
 }
 
-template <typename T, int D>
-__device__ __forceinline__ void store_regs(const TileRegs<D>& t, T* dst, T* dstT) {
+// Row statistics of row i (i < lq): base-2 lse of the row's softmax and whether the row
+// ran over its raw scores (no kept key in the forward).  Rows past the end or without
+// keys get +inf (P = 0).
+__device__ __forceinline__ void row_stats(float lse_nat, bool valid, float& lse2, bool& raw) {
+    raw = valid && lse_nat < kRawLse;
+    const float l = raw ? lse_nat - kMaskedLogit : lse_nat;
+    lse2 = (valid && l != -INFINITY) ? l * kLog2e : INFINITY;
+}
+
+// Staging of rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) in two steps:
+// loads into registers (16-byte chunks, zeros past the last row and the head dim), issued
+// a tile ahead, and their LDS stores, row-major at pitch DP + 8 and, when dstT is set,
+// transposed ([DP][TP]).  Consecutive lanes take consecutive rows of one 8-column chunk,
+// so the transposed 2-byte stores of a wavefront spread over the banks.
+template <int DP>
+struct TileRegs {
+    static constexpr int NV = BT * DP / 8;  // 16-byte chunks of a tile
+    static constexpr int PER = (NV + BWD_THREADS - 1) / BWD_THREADS;
+    u32x4 v[PER];
+};
+
+template <typename T, int DP>
+__device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int nrows, int d, TileRegs<DP>& t) {
 #pragma unroll
-    for (int j = 0; j < D / 64; ++j) {
+    for (int j = 0; j < TileRegs<DP>::PER; ++j) {
         const int c = threadIdx.x + BWD_THREADS * j;
         const int r = c % BT, ch = c / BT;
-        *reinterpret_cast<u32x4*>(dst + r * (D + 8) + 8 * ch) = t.v[j];
+        const bool ok = c < TileRegs<DP>::NV && r0 + r < nrows && 8 * ch < d;
+        const int row = min(r0 + r, nrows - 1);  // in range; dropped below when past the end
+        const int col = min(8 * ch, d - 8);
+        const u32x4 val = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(row) * rs + col);
+        t.v[j] = ok ? val : u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+template <typename T, int DP>
+__device__ __forceinline__ void store_regs(const TileRegs<DP>& t, T* dst, T* dstT) {
+#pragma unroll
+    for (int j = 0; j < TileRegs<DP>::PER; ++j) {
+        const int c = threadIdx.x + BWD_THREADS * j;
+        if (c >= TileRegs<DP>::NV) break;
+        const int r = c % BT, ch = c / BT;
+        *reinterpret_cast<u32x4*>(dst + r * (DP + 8) + 8 * ch) = t.v[j];
         if (dstT) {
             const auto e = __builtin_bit_cast(typename BwdMfma<T>::v8, t.v[j]);
 #pragma unroll
@@ -107,63 +214,64 @@ __device__ __forceinline__ void store_regs(const TileRegs<D>& t, T* dst, T* dstT
     }
 }
 
-template <typename T, int D>
-__device__ __forceinline__ void stage_rows_stats(const BwdParams& p, int b, int h, int r0, float* lse2, float* drs) {
-    if (threadIdx.x < BT) {
-        const int i = r0 + threadIdx.x;
-        const bool ok = i < p.seq_q;
-        lse2[threadIdx.x] = ok ? p.lse[b * p.ls[0] + h * p.ls[1] + static_cast<int64_t>(i) * p.ls[2]] * kLog2e
-                               : INFINITY;
-        drs[threadIdx.x] = ok ? p.dr[(static_cast<int64_t>(b) * p.hq + h) * p.seq_q + i] : 0.f;
-    }
+// A 16-byte fragment of row `row` (< nrows) at column `col` of a [S, D] operand, zeros
+// past the last row or the head dim.
+template <typename T>
+__device__ __forceinline__ u32x4 frag(const T* base, int64_t rs, int row, int nrows, int col, int d) {
+    const int rc = min(max(row, 0), nrows - 1);
+    const int cc = min(col, d - 8);
+    const u32x4 x = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(rc) * rs + cc);
+    return (row >= 0 && row < nrows && col < d) ? x : u32x4{0u, 0u, 0u, 0u};
 }
 
-// dK / dV: a workgroup takes KW keys, wavefront w owns keys [k0 + 16 w, + 16) with its K
-// and V fragments in registers (the A operands of S^T = K Q^T and dP^T = V dO^T).  Per
-// 32-row query block the workgroup stages Q and dO (row-major and transposed) once; each
-// wavefront then forms P^T and dS^T of its keys, passes them through its own LDS rows (one
-// wavefront's LDS accesses stay in order: no barrier) and accumulates dV += P^T dO and
-// dK += dS^T Q.  Two barriers per query block.
+// dK / dV: a workgroup takes KW keys of one K/V head; wavefront w owns keys
+// [kt0 + 16 w, + 16) with its K and V fragments in registers (the A operands of
+// S^T = K Q^T and dP^T = V dO^T).  Per (query head, 32-row query block) item the
+// workgroup stages Q and dO (row-major and transposed) once; each wavefront then forms P^T
+// and dS^T of its keys, passes them through its own LDS rows (one wavefront's LDS accesses
+// stay in order: no barrier) and accumulates dV += P^T dO and dK += dS^T Q over every
+// query head of the group.  Two barriers per item.
 constexpr int KW = 64;
 
-template <typename T, int D>
+template <typename T, int DP, int MK>
 __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) {
     typedef typename BwdMfma<T>::v8 v8;
-    constexpr int RP = D + 8;
-    constexpr int DC = D / 32, DB = D / 16;
+    constexpr int RP = DP + 8;
+    constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T qs[BT * RP];
     __shared__ __align__(16) T dos[BT * RP];
-    __shared__ __align__(16) T qt[D * TP];
-    __shared__ __align__(16) T dot[D * TP];
+    __shared__ __align__(16) T qt[DP * TP];
+    __shared__ __align__(16) T dot[DP * TP];
     __shared__ __align__(16) T pt[4 * 16 * TP];   // per wavefront: P^T [16 keys][32 rows]
     __shared__ __align__(16) T dst[4 * 16 * TP];  // per wavefront: dS^T
     __shared__ float lse2[BT], drs[BT];
+    __shared__ int raws[BT];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4, l16 = lane & 15;
     const int ntk = (p.seq_k + KW - 1) / KW;
-    const int qsp = blockIdx.x % p.qsplit;
-    const int tile = (blockIdx.x / p.qsplit) % ntk;
-    const int bh = blockIdx.x / (p.qsplit * ntk);  // (sequence, query head)
-    const int b = bh / p.hq, h = bh - b * p.hq;
-    const int kvh = h / p.group;
-    const int k0 = tile * KW;
-    const int kw0 = k0 + 16 * wave;  // this wavefront's first key
+    const int split = blockIdx.x % p.splits;
+    const int tile = (blockIdx.x / p.splits) % ntk;
+    const int bkv = blockIdx.x / (p.splits * ntk);  // (sequence, K/V head)
+    const int seq = bkv / p.hkv, kvh = bkv - seq * p.hkv;
+    const Geo g = geo_of(p, seq);
+    const int kt0 = tile * KW;
+    // Keys written: the sequence's (varlen) or every key row of the batch entry (dense:
+    // keys past a key length get zero gradients).
+    const int kwrite = p.cu_q ? g.lk : p.seq_k;
+    if (kt0 >= kwrite) return;  // uniform: no barrier has run
+    const int kw0 = kt0 + 16 * wave;  // this wavefront's first key
 
     // K / V fragments: lane (g4, l16) holds key kw0 + l16, dims 32 c + 8 g4 .. + 7.
     v8 kf[DC], vf[DC];
     {
-        const int key = kw0 + l16;
-        const int kc = min(key, p.seq_k - 1);
-        const T* kp = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1] + static_cast<int64_t>(kc) * p.ks[2];
-        const T* vp = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1] + static_cast<int64_t>(kc) * p.vs[2];
+        const T* kp = static_cast<const T*>(p.k) + g.kb + kvh * p.ks[1] + static_cast<int64_t>(g.k0) * p.ks[2];
+        const T* vp = static_cast<const T*>(p.v) + g.vb + kvh * p.vs[1] + static_cast<int64_t>(g.k0) * p.vs[2];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
-            const u32x4 kx = *reinterpret_cast<const u32x4*>(kp + 32 * c + 8 * g4);
-            const u32x4 vx = *reinterpret_cast<const u32x4*>(vp + 32 * c + 8 * g4);
-            kf[c] = __builtin_bit_cast(v8, key < p.seq_k ? kx : u32x4{0u, 0u, 0u, 0u});
-            vf[c] = __builtin_bit_cast(v8, key < p.seq_k ? vx : u32x4{0u, 0u, 0u, 0u});
+            kf[c] = __builtin_bit_cast(v8, frag(kp, p.ks[2], kw0 + l16, g.lk, 32 * c + 8 * g4, p.d));
+            vf[c] = __builtin_bit_cast(v8, frag(vp, p.vs[2], kw0 + l16, g.lk, 32 * c + 8 * g4, p.d));
         }
     }
     f32x4 dk[DB], dv[DB];
@@ -172,25 +280,53 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     T* ptw = pt + wave * 16 * TP;
     T* dsw = dst + wave * 16 * TP;
 
-    // Causal (top-left): a query block sees this tile only if its last position reaches k0.
-    const int rstart = (p.causal ? (k0 / BT) * BT : 0) + qsp * BT;
-    const int rstep = p.qsplit * BT;
-    const T* qbase = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1];
-    const T* dobase = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1];
-    TileRegs<D> qr, dor;
-    if (rstart < p.seq_q) {
-        load_regs<T, D>(qbase, p.qs[2], rstart, p.seq_q, qr);
-        load_regs<T, D>(dobase, p.dos[2], rstart, p.seq_q, dor);
+    // Items: (query head of the group, 32-row query block), blocks from the first that
+    // sees this tile (causal: rows i >= kt0 - coff); split s takes items s, s + splits, ...
+    const int rfirst = p.causal ? max(0, kt0 - g.coff) / BT : 0;
+    const int nblk = (kt0 < g.lk && g.lq > rfirst * BT) ? (g.lq + BT - 1) / BT - rfirst : 0;
+    const int items = nblk * p.group;
+    auto item_at = [&](int it, int& h, int& r0) {
+        const int gi = it / nblk;
+        h = kvh * p.group + gi;
+        r0 = (rfirst + (it - gi * nblk)) * BT;
+    };
+    auto q_of = [&](int h) {
+        return static_cast<const T*>(p.q) + g.qb + h * p.qs[1] + static_cast<int64_t>(g.q0) * p.qs[2];
+    };
+    auto do_of = [&](int h) {
+        return static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
+    };
+    TileRegs<DP> qr, dor;
+    if (split < items) {
+        int h, r0;
+        item_at(split, h, r0);
+        load_regs<T, DP>(q_of(h), p.qs[2], r0, g.lq, p.d, qr);
+        load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, p.d, dor);
     }
-    for (int r0 = rstart; r0 < p.seq_q; r0 += rstep) {
-        __syncthreads();  // the previous block's LDS reads are done
-        store_regs<T, D>(qr, qs, qt);
-        store_regs<T, D>(dor, dos, dot);
-        stage_rows_stats<T, D>(p, b, h, r0, lse2, drs);
+    for (int it = split; it < items; it += p.splits) {
+        int h, r0;
+        item_at(it, h, r0);
+        __syncthreads();  // the previous item's LDS reads are done
+        store_regs<T, DP>(qr, qs, qt);
+        store_regs<T, DP>(dor, dos, dot);
+        if (threadIdx.x < BT) {
+            const int i = r0 + threadIdx.x;
+            const bool ok = i < g.lq;
+            const int ic = min(i, g.lq - 1);
+            const float lv = p.lse[g.lb + h * p.ls[1] + static_cast<int64_t>(g.q0 + ic) * p.ls[2]];
+            float l2;
+            bool raw;
+            row_stats(lv, ok, l2, raw);
+            lse2[threadIdx.x] = l2;
+            raws[threadIdx.x] = raw ? 1 : 0;
+            drs[threadIdx.x] = ok ? p.dr[h * p.rows_total + g.row_base + ic] : 0.f;
+        }
         __syncthreads();
-        if (r0 + rstep < p.seq_q) {  // the next block's loads overlap this block's products
-            load_regs<T, D>(qbase, p.qs[2], r0 + rstep, p.seq_q, qr);
-            load_regs<T, D>(dobase, p.dos[2], r0 + rstep, p.seq_q, dor);
+        if (it + p.splits < items) {  // the next item's loads overlap this item's products
+            int h2, r2;
+            item_at(it + p.splits, h2, r2);
+            load_regs<T, DP>(q_of(h2), p.qs[2], r2, g.lq, p.d, qr);
+            load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, p.d, dor);
         }
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
@@ -205,14 +341,21 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
                 dpt = BwdMfma<T>::run(vf[c], ob, dpt);
             }
             const int rl = rb * 16 + l16;
-            const int pos = r0 + rl;
+            const int row = r0 + rl;
             const float l2 = lse2[rl], dr = drs[rl];
+            const bool raw = raws[rl] != 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int key = kw0 + 4 * g4 + j;
-                const bool keep = key < p.seq_k && (!p.causal || key <= pos);
+                bool keep = key < g.lk && (!p.causal || key <= row + g.coff);
+                float add = 0.f;
+                if constexpr (MK != MK_NONE) {
+                    const float ml = (keep && row < g.lq) ? mask_at<MK>(p, g, h, row, key) : 0.f;
+                    keep = keep && (raw || ml > kMaskedLogit);
+                    add = raw ? 0.f : ml * kLog2e;
+                }
                 // Rows past the end carry lse2 = +inf: their P is exactly 0.
-                const float e = keep ? __builtin_amdgcn_exp2f(st[j] * p.c2 - l2) : 0.f;
+                const float e = keep ? __builtin_amdgcn_exp2f(st[j] * p.c2 + add - l2) : 0.f;
                 ptw[(4 * g4 + j) * TP + rl] = from_f32<T>(e);
                 dsw[(4 * g4 + j) * TP + rl] = from_f32<T>(e * (dpt[j] - dr));
             }
@@ -232,30 +375,30 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     }
     // Lane (g4, l16) of block db holds keys kw0 + 4 g4 + j, dim db 16 + l16.
     if (p.pdk) {
-        const int64_t base = ((static_cast<int64_t>(b) * p.hq + h) * p.qsplit + qsp) * p.seq_k;
+        const int64_t base = (static_cast<int64_t>(kvh) * p.splits + split) * p.keys_total + g.key_base;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const int d = db * 16 + l16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int key = kw0 + 4 * g4 + j;
-                if (key < p.seq_k) {
-                    p.pdk[(base + key) * D + d] = dk[db][j] * p.scale;
-                    p.pdv[(base + key) * D + d] = dv[db][j];
+                if (key < kwrite && d < p.d) {
+                    p.pdk[(base + key) * DP + d] = dk[db][j] * p.scale;
+                    p.pdv[(base + key) * DP + d] = dv[db][j];
                 }
             }
         }
         return;
     }
-    T* dkp = static_cast<T*>(p.dk) + b * p.dks[0] + kvh * p.dks[1];
-    T* dvp = static_cast<T*>(p.dv) + b * p.dvs[0] + kvh * p.dvs[1];
+    T* dkp = static_cast<T*>(p.dk) + g.dkb + kvh * p.dks[1] + static_cast<int64_t>(g.k0) * p.dks[2];
+    T* dvp = static_cast<T*>(p.dv) + g.dvb + kvh * p.dvs[1] + static_cast<int64_t>(g.k0) * p.dvs[2];
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
         const int d = db * 16 + l16;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int key = kw0 + 4 * g4 + j;
-            if (key < p.seq_k) {
+            if (key < kwrite && d < p.d) {
                 dkp[static_cast<int64_t>(key) * p.dks[2] + d] = from_f32<T>(dk[db][j] * p.scale);
                 dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[db][j]);
             }
@@ -263,29 +406,34 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     }
 }
 
-// dK / dV of a K/V head: the sum of its query heads' fp32 partials (and of their query
-// splits), in a fixed order.
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_group_sum(const BwdParams p) {
-    constexpr int Q = D / 4;  // float4 items per key row
+// dK / dV rows from the splits' fp32 partials, added in split order.  One item per
+// (K/V head, key row, 4 head-dim columns).
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void attn_bwd_kv_sum(const BwdParams p) {
+    const int nq = p.d / 4;  // float4 items per key row (head dims are multiples of 8)
     const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t items = static_cast<int64_t>(p.batch) * p.hkv * p.seq_k * Q;
+    const int64_t items = static_cast<int64_t>(p.hkv) * p.keys_total * nq;
     if (item >= items) return;
-    const int c = static_cast<int>(item % Q);
-    const int key = static_cast<int>((item / Q) % p.seq_k);
-    const int64_t bk = item / (static_cast<int64_t>(Q) * p.seq_k);  // b * hkv + kvh
-    const int b = static_cast<int>(bk / p.hkv), kvh = static_cast<int>(bk % p.hkv);
+    const int c = static_cast<int>(item % nq);
+    const int64_t krow = (item / nq) % p.keys_total;
+    const int kvh = static_cast<int>(item / (static_cast<int64_t>(nq) * p.keys_total));
     f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = sk;
-    for (int g = 0; g < p.group; ++g) {
-        for (int q = 0; q < p.qsplit; ++q) {
-            const int64_t row =
-                ((static_cast<int64_t>(b) * p.hq + kvh * p.group + g) * p.qsplit + q) * p.seq_k + key;
-            sk += *reinterpret_cast<const f32x4*>(p.pdk + row * D + 4 * c);
-            sv += *reinterpret_cast<const f32x4*>(p.pdv + row * D + 4 * c);
-        }
+    for (int s = 0; s < p.splits; ++s) {
+        const int64_t row = (static_cast<int64_t>(kvh) * p.splits + s) * p.keys_total + krow;
+        sk += *reinterpret_cast<const f32x4*>(p.pdk + row * DP + 4 * c);
+        sv += *reinterpret_cast<const f32x4*>(p.pdv + row * DP + 4 * c);
     }
-    T* dkp = static_cast<T*>(p.dk) + b * p.dks[0] + kvh * p.dks[1] + static_cast<int64_t>(key) * p.dks[2] + 4 * c;
-    T* dvp = static_cast<T*>(p.dv) + b * p.dvs[0] + kvh * p.dvs[1] + static_cast<int64_t>(key) * p.dvs[2] + 4 * c;
+    int64_t koff, voff;
+    if (p.cu_q) {
+        koff = krow * p.dks[2];
+        voff = krow * p.dvs[2];
+    } else {
+        const int64_t b = krow / p.seq_k, key = krow - b * p.seq_k;
+        koff = b * p.dks[0] + key * p.dks[2];
+        voff = b * p.dvs[0] + key * p.dvs[2];
+    }
+    T* dkp = static_cast<T*>(p.dk) + koff + kvh * p.dks[1] + 4 * c;
+    T* dvp = static_cast<T*>(p.dv) + voff + kvh * p.dvs[1] + 4 * c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         dkp[e] = from_f32<T>(sk[e]);
@@ -299,14 +447,14 @@ __global__ __launch_bounds__(256) void attn_bwd_group_sum(const BwdParams p) {
 // forms dS of its rows, passes it through its own LDS rows and accumulates dQ += dS K.
 constexpr int QW = 64;
 
-template <typename T, int D>
+template <typename T, int DP, int MK>
 __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     typedef typename BwdMfma<T>::v8 v8;
-    constexpr int RP = D + 8;
-    constexpr int DC = D / 32, DB = D / 16;
+    constexpr int RP = DP + 8;
+    constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T ks[BT * RP];
     __shared__ __align__(16) T vs[BT * RP];
-    __shared__ __align__(16) T kt[D * TP];
+    __shared__ __align__(16) T kt[DP * TP];
     __shared__ __align__(16) T dss[4 * 16 * TP];  // per wavefront: dS [16 rows][32 keys]
 
     const int lane = threadIdx.x & 63;
@@ -316,30 +464,29 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int ksp = blockIdx.x % p.ksplit;
     const int qb = (blockIdx.x / p.ksplit) % nqb;
     const int bh = blockIdx.x / (p.ksplit * nqb);
-    const int b = bh / p.hq, h = bh - b * p.hq;
+    const int seq = bh / p.hq, h = bh - seq * p.hq;
     const int kvh = h / p.group;
+    const Geo g = geo_of(p, seq);
     const int r0 = qb * QW;
+    if (r0 >= g.lq || g.lk <= 0) return;  // uniform: no barrier has run
     const int rw0 = r0 + 16 * wave;  // this wavefront's first row
 
     // Q / dO fragments: lane (g4, l16) holds row rw0 + l16, dims 32 c + 8 g4 .. + 7; the
-    // row statistics of row rw0 + 4 g4 + j (the rows of its accumulator lanes).  The row
+    // row statistics of rows rw0 + 4 g4 + j (the rows of its accumulator lanes).  The row
     // dot D = sum(dO * O) is formed here from the same dO fragments and written for the
     // dK / dV kernel, which runs after this one.
     v8 qf[DC], of[DC];
     float rdot = 0.f;
     {
-        const int row = rw0 + l16;
-        const int rc = min(row, p.seq_q - 1);
-        const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1] + static_cast<int64_t>(rc) * p.qs[2];
-        const T* op = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1] + static_cast<int64_t>(rc) * p.dos[2];
-        const T* outp = static_cast<const T*>(p.o) + b * p.os[0] + h * p.os[1] + static_cast<int64_t>(rc) * p.os[2];
+        const T* qp = static_cast<const T*>(p.q) + g.qb + h * p.qs[1] + static_cast<int64_t>(g.q0) * p.qs[2];
+        const T* dp = static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
+        const T* op = static_cast<const T*>(p.o) + g.ob + h * p.os[1] + static_cast<int64_t>(g.q0) * p.os[2];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
-            const u32x4 qx = *reinterpret_cast<const u32x4*>(qp + 32 * c + 8 * g4);
-            const u32x4 ox = *reinterpret_cast<const u32x4*>(op + 32 * c + 8 * g4);
-            const v8 yv = *reinterpret_cast<const v8*>(outp + 32 * c + 8 * g4);
-            qf[c] = __builtin_bit_cast(v8, row < p.seq_q ? qx : u32x4{0u, 0u, 0u, 0u});
-            of[c] = __builtin_bit_cast(v8, row < p.seq_q ? ox : u32x4{0u, 0u, 0u, 0u});
+            const int col = 32 * c + 8 * g4;
+            qf[c] = __builtin_bit_cast(v8, frag(qp, p.qs[2], rw0 + l16, g.lq, col, p.d));
+            of[c] = __builtin_bit_cast(v8, frag(dp, p.dos[2], rw0 + l16, g.lq, col, p.d));
+            const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], rw0 + l16, g.lq, col, p.d));
 #pragma unroll
             for (int e = 0; e < 8; ++e) rdot += to_f32(of[c][e]) * to_f32(yv[e]);
         }
@@ -347,38 +494,41 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     // The four lanes of a row (g4 = 0..3) each hold a quarter of its dims.
     rdot += __shfl_xor(rdot, 16, kWave);
     rdot += __shfl_xor(rdot, 32, kWave);
-    if (ksp == 0 && g4 == 0 && rw0 + l16 < p.seq_q) p.dr[(static_cast<int64_t>(b) * p.hq + h) * p.seq_q + rw0 + l16] = rdot;
+    if (ksp == 0 && g4 == 0 && rw0 + l16 < g.lq) p.dr[h * p.rows_total + g.row_base + rw0 + l16] = rdot;
     float l2[4], drv[4];
+    bool raw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int row = rw0 + 4 * g4 + j;
-        const int rc = min(row, p.seq_q - 1);
-        const float lv = p.lse[b * p.ls[0] + h * p.ls[1] + static_cast<int64_t>(rc) * p.ls[2]];
+        const int rc = min(row, g.lq - 1);
+        const float lv = p.lse[g.lb + h * p.ls[1] + static_cast<int64_t>(g.q0 + rc) * p.ls[2]];
         const float dv = __shfl(rdot, 4 * g4 + j, kWave);  // lane 4 g4 + j holds that row's dot
-        // Rows past the end: lse2 = +inf makes their P exactly 0.
-        l2[j] = row < p.seq_q ? lv * kLog2e : INFINITY;
-        drv[j] = row < p.seq_q ? dv : 0.f;
+        row_stats(lv, row < g.lq, l2[j], raw[j]);
+        drv[j] = row < g.lq ? dv : 0.f;
     }
     f32x4 dq[DB];
 #pragma unroll
     for (int i = 0; i < DB; ++i) dq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     T* dsw = dss + wave * 16 * TP;
 
-    const int kend = p.causal ? min(p.seq_k, r0 + QW) : p.seq_k;
-    const T* kbase = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
-    const T* vbase = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
-    TileRegs<D> kr, vr;
+    // Causal: the block's last row sees keys up to its position + coff.
+    const int kend = p.causal ? min(g.lk, max(0, min(r0 + QW, g.lq) - 1 + g.coff + 1)) : g.lk;
+    const T* kbase = static_cast<const T*>(p.k) + g.kb + kvh * p.ks[1] + static_cast<int64_t>(g.k0) * p.ks[2];
+    const T* vbase = static_cast<const T*>(p.v) + g.vb + kvh * p.vs[1] + static_cast<int64_t>(g.k0) * p.vs[2];
+    TileRegs<DP> kr, vr;
     const int kstep = p.ksplit * BT;
-    load_regs<T, D>(kbase, p.ks[2], ksp * BT, p.seq_k, kr);
-    load_regs<T, D>(vbase, p.vs[2], ksp * BT, p.seq_k, vr);
+    if (ksp * BT < kend) {
+        load_regs<T, DP>(kbase, p.ks[2], ksp * BT, g.lk, p.d, kr);
+        load_regs<T, DP>(vbase, p.vs[2], ksp * BT, g.lk, p.d, vr);
+    }
     for (int k0 = ksp * BT; k0 < kend; k0 += kstep) {
         __syncthreads();
-        store_regs<T, D>(kr, ks, kt);
-        store_regs<T, D>(vr, vs, nullptr);
+        store_regs<T, DP>(kr, ks, kt);
+        store_regs<T, DP>(vr, vs, nullptr);
         __syncthreads();
         if (k0 + kstep < kend) {  // the next tile's loads overlap this tile's products
-            load_regs<T, D>(kbase, p.ks[2], k0 + kstep, p.seq_k, kr);
-            load_regs<T, D>(vbase, p.vs[2], k0 + kstep, p.seq_k, vr);
+            load_regs<T, DP>(kbase, p.ks[2], k0 + kstep, g.lk, p.d, kr);
+            load_regs<T, DP>(vbase, p.vs[2], k0 + kstep, g.lk, p.d, vr);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -395,9 +545,15 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
             const int key = k0 + kb * 16 + l16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int pos = rw0 + 4 * g4 + j;
-                const bool keep = key < p.seq_k && (!p.causal || key <= pos);
-                const float e = keep ? __builtin_amdgcn_exp2f(sv[j] * p.c2 - l2[j]) : 0.f;
+                const int row = rw0 + 4 * g4 + j;
+                bool keep = key < g.lk && (!p.causal || key <= row + g.coff);
+                float add = 0.f;
+                if constexpr (MK != MK_NONE) {
+                    const float ml = (keep && row < g.lq) ? mask_at<MK>(p, g, h, row, key) : 0.f;
+                    keep = keep && (raw[j] || ml > kMaskedLogit);
+                    add = raw[j] ? 0.f : ml * kLog2e;
+                }
+                const float e = keep ? __builtin_amdgcn_exp2f(sv[j] * p.c2 + add - l2[j]) : 0.f;
                 dsw[(4 * g4 + j) * TP + kb * 16 + l16] = from_f32<T>(e * (dpv[j] - drv[j]));
             }
         }
@@ -411,45 +567,53 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     }
     // Lane (g4, l16) of block db holds rows rw0 + 4 g4 + j, dim db 16 + l16.
     if (p.pdq) {
-        float* dst = p.pdq + ((static_cast<int64_t>(b) * p.hq + h) * p.ksplit + ksp) * p.seq_q * D;
+        float* dst = p.pdq + ((static_cast<int64_t>(h) * p.ksplit + ksp) * p.rows_total + g.row_base) * DP;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const int d = db * 16 + l16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = rw0 + 4 * g4 + j;
-                if (row < p.seq_q) dst[static_cast<int64_t>(row) * D + d] = dq[db][j] * p.scale;
+                if (row < g.lq && d < p.d) dst[static_cast<int64_t>(row) * DP + d] = dq[db][j] * p.scale;
             }
         }
         return;
     }
-    T* dqp = static_cast<T*>(p.dq) + b * p.dqs[0] + h * p.dqs[1];
+    T* dqp = static_cast<T*>(p.dq) + g.dqb + h * p.dqs[1] + static_cast<int64_t>(g.q0) * p.dqs[2];
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
         const int d = db * 16 + l16;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = rw0 + 4 * g4 + j;
-            if (row < p.seq_q) dqp[static_cast<int64_t>(row) * p.dqs[2] + d] = from_f32<T>(dq[db][j] * p.scale);
+            if (row < g.lq && d < p.d) dqp[static_cast<int64_t>(row) * p.dqs[2] + d] = from_f32<T>(dq[db][j] * p.scale);
         }
     }
 }
 
-// dQ: the sum of the key splits' fp32 partials, in split order.
-template <typename T, int D>
+// dQ rows from the key splits' fp32 partials, in split order.  One item per (query head,
+// query row, 4 head-dim columns).
+template <typename T, int DP>
 __global__ __launch_bounds__(256) void attn_bwd_dq_sum(const BwdParams p) {
-    constexpr int Q = D / 4;
+    const int nq = p.d / 4;
     const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t items = static_cast<int64_t>(p.batch) * p.hq * p.seq_q * Q;
+    const int64_t items = static_cast<int64_t>(p.hq) * p.rows_total * nq;
     if (item >= items) return;
-    const int c = static_cast<int>(item % Q);
-    const int row = static_cast<int>((item / Q) % p.seq_q);
-    const int64_t bh = item / (static_cast<int64_t>(Q) * p.seq_q);
-    const int b = static_cast<int>(bh / p.hq), h = static_cast<int>(bh % p.hq);
+    const int c = static_cast<int>(item % nq);
+    const int64_t row = (item / nq) % p.rows_total;
+    const int h = static_cast<int>(item / (static_cast<int64_t>(nq) * p.rows_total));
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < p.ksplit; ++k)
-        acc += *reinterpret_cast<const f32x4*>(p.pdq + ((bh * p.ksplit + k) * p.seq_q + row) * D + 4 * c);
-    T* dst = static_cast<T*>(p.dq) + b * p.dqs[0] + h * p.dqs[1] + static_cast<int64_t>(row) * p.dqs[2] + 4 * c;
+        acc += *reinterpret_cast<const f32x4*>(p.pdq + ((static_cast<int64_t>(h) * p.ksplit + k) * p.rows_total + row) * DP +
+                                               4 * c);
+    int64_t off;
+    if (p.cu_q) {
+        off = row * p.dqs[2];
+    } else {
+        const int64_t b = row / p.seq_q, i = row - b * p.seq_q;
+        off = b * p.dqs[0] + i * p.dqs[2];
+    }
+    T* dst = static_cast<T*>(p.dq) + off + h * p.dqs[1] + 4 * c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(acc[e]);
 }
@@ -457,11 +621,17 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_sum(const BwdParams p) {
 const char* check_bwd(const kmi_attn_bwd_args* a) {
     if (!a) return "null args";
     if (a->dtype != KMI_BF16 && a->dtype != KMI_F16) return "dtype must be BF16 or F16";
-    if (a->head_dim != 64 && a->head_dim != 128) return "head_dim must be 64 or 128";
+    if (!head_dim_supported(a->head_dim)) return "head_dim must be a multiple of 8 up to 256";
     if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seq_q <= 0 || a->seq_k <= 0)
         return "sizes must be positive";
     if (a->heads_q % a->heads_kv != 0) return "heads_kv must divide heads_q";
-    if (a->batch * a->heads_q * a->seq_q > (int64_t{1} << 31) || a->seq_q > (1 << 30) || a->seq_k > (1 << 30))
+    const bool varlen = a->cu_seqlens_q != nullptr;
+    if (varlen != (a->cu_seqlens_k != nullptr)) return "cu_seqlens_q and cu_seqlens_k go together";
+    const int64_t rows = varlen ? a->total_q : a->batch * a->seq_q;
+    const int64_t keys = varlen ? a->total_k : a->batch * a->seq_k;
+    if (varlen && (a->total_q <= 0 || a->total_k <= 0)) return "varlen totals must be positive";
+    if (rows * a->heads_q > (int64_t{1} << 31) || keys * a->heads_q > (int64_t{1} << 31) || a->seq_q > (1 << 30) ||
+        a->seq_k > (1 << 30))
         return "sizes too large";
     const void* ptrs[] = {a->q, a->k, a->v, a->out, a->grad_out, a->lse, a->grad_q, a->grad_k, a->grad_v};
     for (const void* ptr : ptrs)
@@ -473,37 +643,54 @@ const char* check_bwd(const kmi_attn_bwd_args* a) {
     for (const int64_t* s : strides)
         for (int i = 0; i < 3; ++i)
             if (s[i] < 0 || s[i] % 8) return "q, k, v, out and grad_out strides must be non-negative multiples of 8";
+    const int64_t* ostrides[] = {a->dq_stride, a->dk_stride, a->dv_stride};
+    for (const int64_t* s : ostrides)
+        for (int i = 0; i < 3; ++i)
+            if (s[i] % 4) return "grad_q, grad_k and grad_v strides must be multiples of 4";
+    if (a->mask_mode != KMI_MASK_NONE) {
+        if (!a->mask) return "mask_mode set without a mask";
+        if (a->mask_dtype < KMI_BF16 || a->mask_dtype > KMI_BOOL) return "bad mask dtype";
+        if (a->mask_mode != KMI_MASK_STRIDED && a->mask_mode != KMI_MASK_PACKED) return "bad mask mode";
+        if (a->mask_mode == KMI_MASK_PACKED && (!varlen || a->mask_numel <= 0 || a->mask_stride[1] != 0))
+            return "packed masks are varlen only, need mask_numel and are shared by the heads";
+    }
     return nullptr;
 }
 
-// dK / dV query splits: enough workgroups for about two per CU (at most 4 splits, at most
-// one per 32-row query block).
-int bwd_qsplit(const kmi_attn_bwd_args* a) {
-    const int64_t wgs = a->batch * a->heads_q * ceil_div(a->seq_k, KW);
-    int64_t qs = std::min<int64_t>(4, std::max<int64_t>(1, ceil_div(512, wgs)));
-    return static_cast<int>(std::min<int64_t>(qs, ceil_div(a->seq_q, BT)));
+int64_t rows_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q; }
+int64_t keys_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_k : a->batch * a->seq_k; }
+
+// dK / dV splits: enough workgroups for about two per CU (at most 16 splits, at most one
+// per (query head, query block) item).
+int bwd_splits(const kmi_attn_bwd_args* a) {
+    const int64_t wgs = a->batch * a->heads_kv * ceil_div(a->seq_k, KW);
+    const int64_t items = (a->heads_q / a->heads_kv) * ceil_div(a->seq_q, BT);
+    const int64_t s = std::min<int64_t>(16, std::max<int64_t>(1, ceil_div(512, wgs)));
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(s, items)));
 }
 
 // dQ key splits, by the same rule over (query head, 64-row block) workgroups.
 int bwd_ksplit(const kmi_attn_bwd_args* a) {
     const int64_t wgs = a->batch * a->heads_q * ceil_div(a->seq_q, QW);
-    int64_t ks = std::min<int64_t>(4, std::max<int64_t>(1, ceil_div(512, wgs)));
+    const int64_t ks = std::min<int64_t>(4, std::max<int64_t>(1, ceil_div(512, wgs)));
     return static_cast<int>(std::min<int64_t>(ks, ceil_div(a->seq_k, BT)));
 }
 
-// Workspace floats: row dot products (padded to 16 bytes); with GQA or query splits the
-// dK / dV partials; with key splits the dQ partials.
+// Workspace floats: row dot products (padded to 16 bytes); with GQA or splits the dK / dV
+// partials; with key splits the dQ partials.
 struct BwdLayout {
     size_t dr, part, pdq;
 };
 
 BwdLayout bwd_layout(const kmi_attn_bwd_args* a) {
     BwdLayout l{};
-    l.dr = static_cast<size_t>(ceil_div(a->batch * a->heads_q * a->seq_q, 4) * 4);
-    const int qs = bwd_qsplit(a);
-    if (a->heads_q != a->heads_kv || qs > 1) l.part = static_cast<size_t>(a->batch * a->heads_q * qs * a->seq_k * a->head_dim);
+    const int64_t dp = padded_head_dim(a->head_dim);
+    l.dr = static_cast<size_t>(ceil_div(a->heads_q * rows_total_of(a), 4) * 4);
+    // One split sums the query heads of a K/V head in its registers and writes dK / dV.
+    const int s = bwd_splits(a);
+    if (s > 1) l.part = static_cast<size_t>(a->heads_kv * s * keys_total_of(a) * dp);
     const int ks = bwd_ksplit(a);
-    if (ks > 1) l.pdq = static_cast<size_t>(a->batch * a->heads_q * ks * a->seq_q * a->head_dim);
+    if (ks > 1) l.pdq = static_cast<size_t>(a->heads_q * ks * rows_total_of(a) * dp);
     return l;
 }
 
@@ -512,27 +699,50 @@ size_t bwd_ws_bytes(const kmi_attn_bwd_args* a) {
     return (l.dr + 2 * l.part + l.pdq) * sizeof(float);
 }
 
-template <typename T, int D>
+template <typename T, int DP, int MK>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
     const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, QW);
     // dQ first: it writes the row dots that dK / dV read.
-    hipLaunchKernelGGL((attn_bwd_dq<T, D>),
+    hipLaunchKernelGGL((attn_bwd_dq<T, DP, MK>),
                        dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit)),
                        dim3(BWD_THREADS), 0, s, p);
     if (p.pdq) {
-        const int64_t items = static_cast<int64_t>(p.batch) * p.hq * p.seq_q * (D / 4);
-        hipLaunchKernelGGL((attn_bwd_dq_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0, s,
+        const int64_t items = static_cast<int64_t>(p.hq) * p.rows_total * (p.d / 4);
+        hipLaunchKernelGGL((attn_bwd_dq_sum<T, DP>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0, s,
                            p);
     }
-    hipLaunchKernelGGL((attn_bwd_dkdv<T, D>),
-                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * ntk * p.qsplit)),
+    hipLaunchKernelGGL((attn_bwd_dkdv<T, DP, MK>),
+                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hkv * ntk * p.splits)),
                        dim3(BWD_THREADS), 0, s, p);
     if (p.pdk) {
-        const int64_t items = static_cast<int64_t>(p.batch) * p.hkv * p.seq_k * (D / 4);
-        hipLaunchKernelGGL((attn_bwd_group_sum<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0,
-                           s, p);
+        const int64_t items = static_cast<int64_t>(p.hkv) * p.keys_total * (p.d / 4);
+        hipLaunchKernelGGL((attn_bwd_kv_sum<T, DP>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0, s,
+                           p);
     }
     return hipGetLastError();
+}
+
+template <typename T, int DP>
+hipError_t launch_bwd_mask(const BwdParams& p, int mk, hipStream_t s) {
+    switch (mk) {
+        case MK_NONE: return launch_bwd<T, DP, MK_NONE>(p, s);
+        case MK_BOOL: return launch_bwd<T, DP, MK_BOOL>(p, s);
+        case MK_BF16: return launch_bwd<T, DP, MK_BF16>(p, s);
+        case MK_F16: return launch_bwd<T, DP, MK_F16>(p, s);
+        default: return launch_bwd<T, DP, MK_F32>(p, s);
+    }
+}
+
+template <typename T>
+hipError_t launch_bwd_dim(const BwdParams& p, int mk, hipStream_t s) {
+    switch (padded_head_dim(p.d)) {
+        case 32: return launch_bwd_mask<T, 32>(p, mk, s);
+        case 64: return launch_bwd_mask<T, 64>(p, mk, s);
+        case 96: return launch_bwd_mask<T, 96>(p, mk, s);
+        case 128: return launch_bwd_mask<T, 128>(p, mk, s);
+        case 192: return launch_bwd_mask<T, 192>(p, mk, s);
+        default: return launch_bwd_mask<T, 256>(p, mk, s);
+    }
 }
 
 }  // namespace
@@ -563,10 +773,10 @@ extern "C" int kmi_attn_bwd(const kmi_attn_bwd_args* a, void* workspace, size_t 
     p.dk = a->grad_k;
     p.dv = a->grad_v;
     p.dr = static_cast<float*>(workspace);
-    p.qsplit = bwd_qsplit(a);
+    p.splits = bwd_splits(a);
     p.ksplit = bwd_ksplit(a);
     {
-        // Partials start 16-byte aligned after the row dot products (D is a multiple of 4).
+        // Partials start 16-byte aligned after the row dot products (DP is a multiple of 4).
         const BwdLayout l = bwd_layout(a);
         if (l.part) {
             p.pdk = p.dr + l.dr;
@@ -585,6 +795,17 @@ extern "C" int kmi_attn_bwd(const kmi_attn_bwd_args* a, void* workspace, size_t 
         p.dvs[i] = a->dv_stride[i];
         p.ls[i] = a->lse_stride[i];
     }
+    const int mk = mask_kind_of(a->mask_mode, a->mask_dtype);
+    p.mask = mk == MK_NONE ? nullptr : a->mask;
+    p.mask_mode = mk == MK_NONE ? KMI_MASK_NONE : a->mask_mode;
+    for (int i = 0; i < 4; ++i) p.ms[i] = a->mask_stride[i];
+    p.mask_numel = a->mask_numel;
+    p.mask_off = a->mask_mode == KMI_MASK_PACKED ? a->mask_offsets : nullptr;
+    p.cu_q = a->cu_seqlens_q;
+    p.cu_k = a->cu_seqlens_k;
+    p.klen = a->cu_seqlens_q ? nullptr : a->key_lengths;
+    p.total_q = static_cast<int>(a->total_q);
+    p.total_k = static_cast<int>(a->total_k);
     p.batch = static_cast<int>(a->batch);
     p.hq = static_cast<int>(a->heads_q);
     p.hkv = static_cast<int>(a->heads_kv);
@@ -592,13 +813,12 @@ extern "C" int kmi_attn_bwd(const kmi_attn_bwd_args* a, void* workspace, size_t 
     p.seq_q = static_cast<int>(a->seq_q);
     p.seq_k = static_cast<int>(a->seq_k);
     p.causal = a->causal ? 1 : 0;
+    p.d = static_cast<int>(a->head_dim);
+    p.rows_total = rows_total_of(a);
+    p.keys_total = keys_total_of(a);
     p.scale = static_cast<float>(a->scale);
     p.c2 = static_cast<float>(a->scale * 1.4426950408889634);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t err;
-    if (a->dtype == KMI_BF16)
-        err = a->head_dim == 64 ? launch_bwd<bf16, 64>(p, s) : launch_bwd<bf16, 128>(p, s);
-    else
-        err = a->head_dim == 64 ? launch_bwd<f16, 64>(p, s) : launch_bwd<f16, 128>(p, s);
+    const hipError_t err = a->dtype == KMI_BF16 ? launch_bwd_dim<bf16>(p, mk, s) : launch_bwd_dim<f16>(p, mk, s);
     return hip_status(err, "kmi_attn_bwd");
 }

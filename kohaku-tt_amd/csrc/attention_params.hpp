@@ -1,0 +1,72 @@
+// Parameters shared by the host side of the attention forward (attention.hip) and its
+// kernels (attention_kernels.hpp, instantiated per padded head dim in attention_d*.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace kmi {
+namespace fwd {
+
+constexpr int NWAVES = 4;  // wavefronts per workgroup
+constexpr int NTHREADS = NWAVES * kWave;
+// Keys per wavefront tile.
+constexpr int WN = 32;
+// Row split stages a unit's whole key range in LDS up to this many tiles (eight measured
+// slower: fewer workgroups fit per CU).
+constexpr int kRsTiles = 4;
+
+struct AttnParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    float* lse;
+    float* part_o;    // [splits][rows_total][hq][D] fp32 (normalised partial outputs)
+    float* part_lse;  // [splits][rows_total][hq][2] fp32: base-2 log-sum-exp, raw-mode flag
+    int64_t qs[3], ks[3], vs[3], os[3], ls[3];
+    const void* mask;
+    int64_t ms[4];
+    int64_t mask_numel;
+    const int32_t* cu_q;
+    const int32_t* cu_k;
+    // Dense key lengths [batch] (or null): sequence b sees keys [0, clamp(klen[b], 1, seq_k)).
+    const int32_t* klen;
+    int mask_dtype, mask_mode;
+    // Mask rows with unit key stride (every packed mask; strided masks with key stride 1):
+    // whole tiles read their mask values four keys per load (element-aligned vector loads).
+    int mask_vec4;
+    // Row split with the unit's whole key range staged once in the workgroup's LDS
+    // (rs_shared: the dynamic LDS holds every key tile, K then V).
+    int rs_shared;
+    // Packed masks: device int64 [batch + 1] block offsets (or null: added up in-kernel).
+    const int64_t* mask_off;
+    int batch, hq, hkv, group, seq_q, seq_k;
+    int d;  // head dim (the kernels' D template argument is it padded to a multiple of 32)
+    int causal;
+    float scale_log2;
+    int splits, tiles_per_split;
+    int nx;  // query tiles per (sequence, K/V head)
+    int npair;  // causal: the 2 npair shortest query tiles of a unit run two per workgroup
+    int total_q, total_k;  // varlen packed token counts
+    int64_t rows_total;
+};
+
+struct Plan {
+    bool decode;  // attn_decode_kernel: per-wavefront key ranges, fp32 partials + merge
+    bool rs;      // row split: short key ranges, one row block per wavefront
+    bool rs_shared;  // row split with the unit's key tiles (at most four) staged in LDS once
+    int nqb, nx, splits, tiles_per_split;
+    int64_t rows_total;
+    size_t ws_bytes;
+};
+
+// Compute units of the current device (cached per device id).
+int cu_count();
+
+// Enqueues the forward of a planned call for element type T and padded head dim D
+// (explicit instantiations in attention_d<D>.hip).
+template <typename T, int D>
+hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream);
+
+}  // namespace fwd
+}  // namespace kmi

@@ -61,6 +61,74 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// ---------------------------------------------------------------- attention masks
+//
+// Mask element types are a template parameter of the attention kernels (no mask code in
+// the mask-free variants).  A mask value becomes a logit offset clamped at the
+// reference's masked logit -5e5 (ktt_flash/program.cpp:912-919, varlen_plan.hpp:17):
+// bool keep -> 0, drop -> -5e5; float masks max(x, -5e5) (-inf and NaN -> -5e5).  A key
+// at -5e5 is "masked": it gets exactly zero weight when its row keeps any key, and a row
+// whose every key is masked is the softmax over its raw scores.
+constexpr float kMaskedLogit = -5e5f;
+
+enum MaskKind { MK_NONE = 0, MK_BOOL = 1, MK_BF16 = 2, MK_F16 = 3, MK_F32 = 4 };
+
+// The raw element type a mask kind is loaded as.
+template <int MK>
+struct MaskRaw {
+    typedef float type;
+};
+template <>
+struct MaskRaw<MK_BOOL> {
+    typedef uint8_t type;
+};
+template <>
+struct MaskRaw<MK_BF16> {
+    typedef uint16_t type;
+};
+template <>
+struct MaskRaw<MK_F16> {
+    typedef uint16_t type;
+};
+
+// A loaded mask element in logit units, clamped at the masked logit.
+template <int MK, typename R>
+__device__ __forceinline__ float mask_logit_of(R raw) {
+    if constexpr (MK == MK_BOOL) {
+        return raw ? 0.f : kMaskedLogit;
+    } else if constexpr (MK == MK_BF16) {
+        return fmaxf(static_cast<float>(__builtin_bit_cast(bf16, raw)), kMaskedLogit);
+    } else if constexpr (MK == MK_F16) {
+        return fmaxf(static_cast<float>(__builtin_bit_cast(f16, raw)), kMaskedLogit);
+    } else {
+        return fmaxf(static_cast<float>(raw), kMaskedLogit);
+    }
+}
+
+// The mask kind of a kmi_dtype code (MK_NONE for none).
+inline int mask_kind_of(int32_t mask_mode, int32_t mask_dtype) {
+    if (mask_mode == KMI_MASK_NONE) return MK_NONE;
+    switch (mask_dtype) {
+        case KMI_BOOL: return MK_BOOL;
+        case KMI_BF16: return MK_BF16;
+        case KMI_F16: return MK_F16;
+        default: return MK_F32;
+    }
+}
+
+// Head dims: the kernels take multiples of 8 up to 256 and pad them to DP, a whole number
+// of 32-wide MFMA blocks (the padded columns hold zeros in registers; no memory past the
+// head dim is read or written).
+inline bool head_dim_supported(int64_t d) { return d >= 8 && d <= 256 && d % 8 == 0; }
+inline int padded_head_dim(int64_t d) {
+    if (d <= 32) return 32;
+    if (d <= 64) return 64;
+    if (d <= 96) return 96;
+    if (d <= 128) return 128;
+    if (d <= 192) return 192;
+    return 256;
+}
+
 // Error plumbing of the C ABI (defined in capi.cpp).
 int fail(int status, const std::string& message);
 int hip_status(hipError_t err, const char* what);

@@ -27,6 +27,8 @@
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "../../include/kohakutt_amd.h"
@@ -76,34 +78,47 @@ void* stream_of(const Tensor& t) {
 
 bool mask_given(const optional<Tensor>& m) { return m.has_value() && m->defined(); }
 
+// Head dims the kernels take: multiples of 8 (16-byte rows) up to 256; the kernels pad
+// the head dim to a whole number of 32-wide MFMA blocks with zeros.
+bool head_dim_ok(int64_t d) { return d >= 8 && d <= 256 && d % 8 == 0; }
+
+// Tensors whose data the kernels can read: not meta, not fake / functional wrappers
+// (torch.compile and export trace with those; they must take the composite route).
+bool real_data(const Tensor& t) {
+    constexpr c10::DispatchKeySet traced({c10::DispatchKey::Python, c10::DispatchKey::PythonTLSSnapshot,
+                                          c10::DispatchKey::Functionalize});
+    return t.defined() && !t.is_meta() && (t.key_set() & traced).empty() && t.has_storage();
+}
+
 // Why the kernels do not take SDPA(q, k, v, mask, ...), or "" when they do.  The
 // conditions of the reference's fused_refusal (aten_attention.cpp:62-127): 4-D non-empty
 // q/k/v of one float type, fp32 only without gradients (cast to bf16 at entry), no
 // dropout, one head dim, K/V heads dividing Q heads, causal without a mask, a mask that
-// broadcasts to [B, H, Sq, Sk]; plus what these kernels cover: CUDA tensors, head dim 64
-// or 128, bool / bf16 / f16 / f32 / f64 masks.
+// broadcasts to [B, H, Sq, Sk]; plus what these kernels cover: GPU tensors (meta tensors
+// answer by their sizes and dtypes), head dims that are multiples of 8 up to 256,
+// bool / bf16 / f16 / f32 / f64 masks.
 std::string sdpa_refusal_impl(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask,
                               double dropout_p, bool is_causal) {
     if (!g_attention.load()) return "kohakutt_amd attention is switched off";
     const bool grads = q.requires_grad() || k.requires_grad() || v.requires_grad();
     for (const Tensor* t : {&q, &k, &v}) {
         const auto st = t->scalar_type();
-        if (!t->is_cuda() || t->dim() != 4 || t->numel() == 0 ||
+        if (!(t->is_cuda() || t->is_meta()) || t->dim() != 4 || t->numel() == 0 ||
             !(st == at::kBFloat16 || st == at::kHalf || (st == at::kFloat && !grads)) ||
-            st != q.scalar_type())
+            st != q.scalar_type() || t->device() != q.device())
             return "q, k and v must be non-empty 4-D bf16 / fp16 GPU tensors (fp32 without gradients)";
     }
     if (dropout_p != 0.0) return "dropout";
     const int64_t d = q.size(3);
     if (k.size(3) != d || v.size(3) != d) return "q, k and v need one head dim";
-    if (d != 64 && d != 128) return "head dim must be 64 or 128";
+    if (!head_dim_ok(d)) return "head dim must be a multiple of 8 up to 256";
     if (k.size(0) != q.size(0) || v.size(0) != q.size(0) || v.size(1) != k.size(1) || q.size(1) % k.size(1) != 0 ||
         v.size(2) != k.size(2))
         return "q, k and v shapes do not match (K / V heads must divide Q heads)";
     if (is_causal && mask.has_value()) return "causal takes no mask";
     if (mask_given(mask)) {
         const Tensor& m = *mask;
-        if (!m.is_cuda() || m.device() != q.device()) return "the mask must be on q's device";
+        if (m.device() != q.device()) return "the mask must be on q's device";
         if (m.dim() > 4) return "the mask must broadcast to [B, H, Sq, Sk]";
         const int64_t full[4] = {q.size(0), q.size(1), q.size(2), k.size(2)};
         for (int64_t i = 0; i < m.dim(); ++i) {
@@ -252,68 +267,153 @@ SdpaResult sdpa_overrideable(const Tensor& q, const Tensor& k, const Tensor& v, 
     return {out, lse, Tensor(), Tensor(), c10::SymInt(sq), c10::SymInt(sk), seed, offset, Tensor()};
 }
 
-// The flash backward (kmi_attn_bwd) takes unmasked calls whose forward ran the kernels:
-// their lse is a contiguous fp32 [B, H, Sq] (a declined forward leaves a stride-0 one).
+// The flash backward (kmi_attn_bwd) takes calls whose forward ran the kernels -- their
+// lse is a contiguous fp32 [B, H, Sq] (a declined forward leaves a stride-0 one) -- with
+// the forward's mask, if any.
 bool flash_backward_takes(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& attn_bias,
                           const Tensor& out, const Tensor& lse, const Tensor& grad_out) {
-    if (!g_attention.load() || attn_bias.defined() || !lse.defined()) return false;
+    if (!g_attention.load() || !lse.defined()) return false;
     const auto st = q.scalar_type();
     if (!(st == at::kBFloat16 || st == at::kHalf) || k.scalar_type() != st || v.scalar_type() != st ||
         grad_out.scalar_type() != st || out.scalar_type() != st)
         return false;
     if (q.dim() != 4 || k.dim() != 4 || v.dim() != 4 || !q.is_cuda()) return false;
     const int64_t d = q.size(3);
-    if ((d != 64 && d != 128) || k.size(3) != d || v.size(3) != d || q.size(1) % k.size(1) != 0) return false;
+    if (!head_dim_ok(d) || k.size(3) != d || v.size(3) != d || q.size(1) % k.size(1) != 0) return false;
+    if (attn_bias.defined()) {
+        // The forward's mask: it took bool or floating masks that broadcast to [B, H, Sq, Sk].
+        if (attn_bias.device() != q.device() || attn_bias.dim() > 4) return false;
+        const auto mt = attn_bias.scalar_type();
+        if (!(mt == at::kBool || mt == at::kBFloat16 || mt == at::kHalf || mt == at::kFloat || mt == at::kDouble))
+            return false;
+        const int64_t full[4] = {q.size(0), q.size(1), q.size(2), k.size(2)};
+        for (int64_t i = 0; i < attn_bias.dim(); ++i) {
+            const int64_t sz = attn_bias.size(attn_bias.dim() - 1 - i);
+            if (sz != 1 && sz != full[3 - i]) return false;
+        }
+    }
     return lse.scalar_type() == at::kFloat && lse.dim() == 3 && lse.size(0) == q.size(0) &&
            lse.size(1) == q.size(1) && lse.size(2) == q.size(2) && lse.stride(2) == 1 && lse.stride(1) >= q.size(2);
 }
 
-std::tuple<Tensor, Tensor, Tensor> flash_backward(const Tensor& grad_out_in, const Tensor& q_in, const Tensor& k_in,
-                                                  const Tensor& v_in, const Tensor& out_in, const Tensor& lse,
-                                                  bool is_causal, optional<double> scale) {
-    const Tensor q = kernel_operand(q_in, 2), k = kernel_operand(k_in, 2), v = kernel_operand(v_in, 2);
-    const Tensor go = kernel_operand(grad_out_in, 2);
-    const Tensor o = kernel_operand(out_in, 2);
-    const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3), Hk = k.size(1), Sk = k.size(2);
-    Tensor dq = at::empty({B, H, Sq, D}, q.options());
-    Tensor dk = at::empty({B, Hk, Sk, D}, k.options());
-    Tensor dv = at::empty({B, Hk, Sk, D}, v.options());
+// The operands of one kmi_attn_bwd call.  Dense: [B, H, S, D] tensors, lse [B, H, Sq], an
+// optional mask broadcast to [B, H, Sq, Sk].  Varlen (cu_q defined): [T, H, D] tensors,
+// lse [H, Tq], device int32 offsets, an optional [Tk] key mask or block-packed mask.
+struct BwdCall {
+    Tensor grad, q, k, v, out, lse;
+    Tensor mask;      // strided (dense [B, H, Sq, Sk] view or varlen [Tk]) or packed
+    bool packed = false;
+    Tensor mask_offsets;  // varlen packed masks: device int64 [n + 1] block offsets (optional)
+    Tensor cu_q, cu_k;
+    Tensor key_lengths;  // dense: int32 [B] key counts (optional)
+    int64_t nseq = 0, max_q = 0, max_k = 0;
+    bool causal = false;
+    double scale = 0.0;
+};
+
+std::tuple<Tensor, Tensor, Tensor> run_backward(const BwdCall& c) {
+    const bool varlen = c.cu_q.defined();
+    const int64_t row_dim = varlen ? 0 : 2;
+    const Tensor q = kernel_operand(c.q, row_dim), k = kernel_operand(c.k, row_dim), v = kernel_operand(c.v, row_dim);
+    const Tensor go = kernel_operand(c.grad, row_dim);
+    const Tensor o = kernel_operand(c.out, row_dim);
+    Tensor dq = at::empty(q.sizes(), q.options());
+    Tensor dk = at::empty(k.sizes(), k.options());
+    Tensor dv = at::empty(v.sizes(), v.options());
     kmi_attn_bwd_args a{};
     a.q = q.data_ptr();
     a.k = k.data_ptr();
     a.v = v.data_ptr();
     a.out = o.data_ptr();
     a.grad_out = go.data_ptr();
-    a.lse = lse.data_ptr<float>();
+    a.lse = c.lse.data_ptr<float>();
     a.grad_q = dq.data_ptr();
     a.grad_k = dk.data_ptr();
     a.grad_v = dv.data_ptr();
     a.dtype = code_of(q.scalar_type());
-    a.causal = is_causal ? 1 : 0;
-    a.batch = B;
-    a.heads_q = H;
-    a.heads_kv = Hk;
-    a.seq_q = Sq;
-    a.seq_k = Sk;
+    a.causal = c.causal ? 1 : 0;
+    const int64_t D = q.size(-1);
     a.head_dim = D;
-    for (int i = 0; i < 3; ++i) {
-        a.q_stride[i] = q.stride(i);
-        a.k_stride[i] = k.stride(i);
-        a.v_stride[i] = v.stride(i);
-        a.o_stride[i] = o.stride(i);
-        a.do_stride[i] = go.stride(i);
-        a.dq_stride[i] = dq.stride(i);
-        a.dk_stride[i] = dk.stride(i);
-        a.dv_stride[i] = dv.stride(i);
-        a.lse_stride[i] = lse.stride(i);
+    if (varlen) {
+        a.batch = c.nseq;
+        a.heads_q = q.size(1);
+        a.heads_kv = k.size(1);
+        a.seq_q = std::max<int64_t>(1, c.max_q);
+        a.seq_k = std::max<int64_t>(1, c.max_k);
+        a.cu_seqlens_q = c.cu_q.data_ptr<int32_t>();
+        a.cu_seqlens_k = c.cu_k.data_ptr<int32_t>();
+        a.total_q = q.size(0);
+        a.total_k = k.size(0);
+        // [T, H, D]: stride[1] heads, stride[2] tokens; lse [H, Tq].
+        const Tensor* ts[] = {&q, &k, &v, &o, &go, &dq, &dk, &dv};
+        int64_t* ss[] = {a.q_stride, a.k_stride, a.v_stride, a.o_stride, a.do_stride, a.dq_stride, a.dk_stride,
+                         a.dv_stride};
+        for (int i = 0; i < 8; ++i) {
+            ss[i][0] = 0;
+            ss[i][1] = ts[i]->stride(1);
+            ss[i][2] = ts[i]->stride(0);
+        }
+        a.lse_stride[0] = 0;
+        a.lse_stride[1] = c.lse.stride(0);
+        a.lse_stride[2] = c.lse.stride(1);
+    } else {
+        a.batch = q.size(0);
+        a.heads_q = q.size(1);
+        a.heads_kv = k.size(1);
+        a.seq_q = q.size(2);
+        a.seq_k = k.size(2);
+        for (int i = 0; i < 3; ++i) {
+            a.q_stride[i] = q.stride(i);
+            a.k_stride[i] = k.stride(i);
+            a.v_stride[i] = v.stride(i);
+            a.o_stride[i] = o.stride(i);
+            a.do_stride[i] = go.stride(i);
+            a.dq_stride[i] = dq.stride(i);
+            a.dk_stride[i] = dk.stride(i);
+            a.dv_stride[i] = dv.stride(i);
+            a.lse_stride[i] = c.lse.stride(i);
+        }
     }
-    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
+    a.scale = c.scale;
+    if (c.key_lengths.defined()) a.key_lengths = c.key_lengths.data_ptr<int32_t>();
+    if (c.mask.defined()) {
+        a.mask = c.mask.data_ptr();
+        a.mask_dtype = code_of(c.mask.scalar_type());
+        if (c.packed) {
+            a.mask_mode = KMI_MASK_PACKED;
+            a.mask_numel = c.mask.numel();
+            if (c.mask_offsets.defined()) a.mask_offsets = c.mask_offsets.data_ptr<int64_t>();
+        } else {
+            a.mask_mode = KMI_MASK_STRIDED;
+            if (varlen) {
+                a.mask_stride[3] = c.mask.stride(0);  // a [Tk] key mask
+            } else {
+                for (int i = 0; i < 4; ++i) a.mask_stride[i] = c.mask.stride(i);
+            }
+        }
+    }
     size_t ws = 0;
     check(kmi_attn_bwd_workspace_bytes(&a, &ws), "kmi_attn_bwd_workspace_bytes");
     Tensor work = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
     check(kmi_attn_bwd(&a, work.data_ptr(), ws, stream_of(q)), "kmi_attn_bwd");
     g_attn_bwd_calls.fetch_add(1);
     return {dq, dk, dv};
+}
+
+std::tuple<Tensor, Tensor, Tensor> flash_backward(const Tensor& grad_out, const Tensor& q, const Tensor& k,
+                                                  const Tensor& v, const Tensor& out, const Tensor& lse,
+                                                  const Tensor& attn_bias, bool is_causal, optional<double> scale) {
+    BwdCall c;
+    c.grad = grad_out;
+    c.q = q;
+    c.k = k;
+    c.v = v;
+    c.out = out;
+    c.lse = lse;
+    if (attn_bias.defined()) c.mask = mask_operand(attn_bias, q, k.size(2));
+    c.causal = is_causal;
+    c.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(q.size(3)));
+    return run_backward(c);
 }
 
 // ktt::_sdpa_flash_backward(grad, q, k, v, out, lse, is_causal, scale): the flash
@@ -323,11 +423,12 @@ std::tuple<Tensor, Tensor, Tensor> sdpa_flash_backward_op(const Tensor& grad, co
                                                           bool is_causal, optional<double> scale) {
     TORCH_CHECK(flash_backward_takes(q, k, v, Tensor(), out, lse, grad),
                 "kohakutt_amd: _sdpa_flash_backward needs bf16 / fp16 [B, H, S, D] GPU tensors of one dtype, "
-                "head dim 64 or 128, K/V heads dividing Q heads and the forward's contiguous fp32 lse [B, H, Sq]");
+                "a head dim that is a multiple of 8 up to 256, K/V heads dividing Q heads and the forward's "
+                "contiguous fp32 lse [B, H, Sq]");
     TORCH_CHECK(grad.sizes() == q.sizes() && out.sizes() == q.sizes(),
                 "kohakutt_amd: _sdpa_flash_backward grad and out must be shaped as q");
     c10::DeviceGuard guard(q.device());
-    return flash_backward(grad, q, k, v, out, lse, is_causal, scale);
+    return flash_backward(grad, q, k, v, out, lse, Tensor(), is_causal, scale);
 }
 
 // The math backward of the overrideable op, in fp32 (the reference's
@@ -342,8 +443,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> sdpa_overrideable_backward(
     (void)philox_seed, (void)philox_offset;
     TORCH_CHECK(dropout_p == 0.0, "kohakutt_amd: attention backward takes no dropout");
     c10::DeviceGuard guard(q.device());
-    if (flash_backward_takes(q, k, v, attn_bias, out, logsumexp, grad_out)) {
-        auto g = flash_backward(grad_out, q, k, v, out, logsumexp, is_causal, scale);
+    // A mask that asks for its own gradient takes the fp32 recompute (the kernels give none).
+    const bool bias_grad = grad_input_mask[3] && attn_bias.defined() && attn_bias.is_floating_point();
+    if (!bias_grad && flash_backward_takes(q, k, v, attn_bias, out, logsumexp, grad_out)) {
+        auto g = flash_backward(grad_out, q, k, v, out, logsumexp, attn_bias, is_causal, scale);
         return {grad_input_mask[0] ? std::get<0>(g) : Tensor(), grad_input_mask[1] ? std::get<1>(g) : Tensor(),
                 grad_input_mask[2] ? std::get<2>(g) : Tensor(), Tensor()};
     }
@@ -407,7 +510,10 @@ int64_t fused_sdp_choice(const Tensor& q, const Tensor& k, const Tensor& v, cons
 Tensor sdpa_entry(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask, double dropout_p,
                   bool is_causal, optional<double> scale, bool enable_gqa) {
     const bool grads = at::GradMode::is_enabled() && (q.requires_grad() || k.requires_grad() || v.requires_grad());
-    if (!grads && mask_given(mask) && mask->scalar_type() == at::kBool &&
+    // Traced (fake / functional) and meta tensors take the composite, which the tracer
+    // understands; only tensors with device data reach the kernels from here.
+    const bool data = real_data(q) && real_data(k) && real_data(v) && (!mask_given(mask) || real_data(*mask));
+    if (!grads && data && mask_given(mask) && mask->scalar_type() == at::kBool &&
         at::globalContext().userEnabledOverrideableSDP() &&
         sdpa_refusal_impl(q, k, v, mask, dropout_p, is_causal).empty()) {
         at::AutoDispatchBelowADInplaceOrView below;
@@ -417,9 +523,14 @@ Tensor sdpa_entry(const Tensor& q, const Tensor& k, const Tensor& v, const optio
                                                                        enable_gqa);
 }
 
+// ktt::sdpa_refusal(q, k, v, mask, dropout_p, is_causal, scale): why the kernels do not
+// take this call ("" when they do), from sizes, dtypes and devices only, so meta tensors
+// answer too (the reference's schema and dispatch key, aten_attention.cpp:910-952; its
+// compile pass asks it on meta tensors, torch_backend/chains.py:595-606).
 std::string sdpa_refusal_op(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask,
-                            bool is_causal) {
-    return sdpa_refusal_impl(q, k, v, mask, 0.0, is_causal);
+                            double dropout_p, bool is_causal, optional<double> scale) {
+    (void)scale;  // any scale is taken
+    return sdpa_refusal_impl(q, k, v, mask, dropout_p, is_causal);
 }
 
 // ---------------------------------------------------------------- key lengths
@@ -465,53 +576,99 @@ std::tuple<Tensor, Tensor, Tensor> sdpa_lengths_backward(const Tensor& grad, con
     TORCH_CHECK(grad.sizes() == out.sizes() && grad.scalar_type() == q.scalar_type(),
                 "kohakutt_amd: _sdpa_lengths_backward grad must be shaped and typed as the output");
     c10::DeviceGuard guard(q.device());
-    const int64_t B = q.size(0), Sk = k.size(2);
-    const Tensor len = lengths.clamp(1, Sk).view({B, 1, 1, 1});
-    const Tensor keep = at::arange(Sk, lengths.options()).view({1, 1, 1, Sk}) < len;
-    auto g = sdpa_overrideable_backward(grad, q, k, v, keep, {true, true, true, false}, out, Tensor(), Tensor(),
-                                        Tensor(), c10::SymInt(q.size(2)), c10::SymInt(Sk), 0.0, is_causal, Tensor(),
-                                        Tensor(), scale);
-    return {std::get<0>(g), std::get<1>(g), std::get<2>(g)};
+    // The schema carries no statistics: one forward pass on the kernels gives the lse, then
+    // the backward kernels stop every batch entry's keys at its length (keys past it get
+    // zero gradients).
+    const Tensor len = lengths.contiguous();
+    const AttnOut fwd = run_attention(q, k, v, std::nullopt, is_causal, scale, &len);
+    BwdCall c;
+    c.grad = grad;
+    c.q = q;
+    c.k = k;
+    c.v = v;
+    c.out = out;
+    c.lse = fwd.lse;
+    c.key_lengths = len;
+    c.causal = is_causal;
+    c.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(q.size(3)));
+    return run_backward(c);
 }
 
 // ---------------------------------------------------------------- varlen
 
-// ktt::_sdpa_varlen: packed attention over cu_seqlens (the reference's
-// aten_varlen.cpp:165-231 / bridge::sdpa_varlen).  key_mask: [Tk] bool keep-mask or
-// additive; attn_mask: every sequence's [Lq_i, Lk_i] block, concatenated (additive or
-// bool), shared by the heads.  Returns (out [Tq, H, D], lse [H, Tq] fp32).
-std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in,
-                                       const Tensor& cu_q_in, const Tensor& cu_k_in, int64_t max_q, int64_t max_k,
-                                       bool is_causal, optional<double> scale, const optional<Tensor>& key_mask,
-                                       const optional<Tensor>& attn_mask) {
-    TORCH_CHECK(q_in.is_cuda() && k_in.is_cuda() && v_in.is_cuda(), "kohakutt_amd: sdpa_varlen needs GPU tensors");
-    TORCH_CHECK(q_in.dim() == 3 && k_in.dim() == 3 && v_in.dim() == 3,
-                "kohakutt_amd: sdpa_varlen takes q [Tq, H, D], k / v [Tk, Hk, D]");
-    TORCH_CHECK(k_in.size(0) == v_in.size(0) && k_in.size(1) == v_in.size(1) && q_in.size(1) % k_in.size(1) == 0,
-                "kohakutt_amd: sdpa_varlen shapes do not match (K / V heads must divide Q heads)");
-    TORCH_CHECK(q_in.size(2) == k_in.size(2) && v_in.size(2) == q_in.size(2),
-                "kohakutt_amd: sdpa_varlen needs one head dim");
-    TORCH_CHECK(!(mask_given(key_mask) && mask_given(attn_mask)),
-                "kohakutt_amd: sdpa_varlen takes key_mask or attn_mask, not both");
-    c10::DeviceGuard guard(q_in.device());
-    Tensor q = q_in, k = k_in, v = v_in;
-    const bool fp32 = q.scalar_type() == at::kFloat;
-    if (fp32) {
-        q = q.to(at::kBFloat16);
-        k = k.to(at::kBFloat16);
-        v = v.to(at::kBFloat16);
+// Per-sequence lengths of host offsets under the reference's rules and messages
+// (varlen::intervals, ktt_flash/varlen_plan.hpp:43-82): equal counts starting at 0,
+// non-decreasing, a sequence with queries has keys, causal (bottom-right) leaves no query
+// without keys.
+struct HostLengths {
+    int64_t nseq = 0, max_q = 0, max_k = 0, mask_values = 0;
+};
+
+HostLengths host_lengths(at::IntArrayRef cu_q, at::IntArrayRef cu_k, bool causal) {
+    TORCH_CHECK_VALUE(cu_q.size() >= 2 && cu_q.size() == cu_k.size() && cu_q[0] == 0 && cu_k[0] == 0,
+                      "kohakutt_amd: sdpa_varlen needs cumulative offsets [0, ..., total] of equal count for queries "
+                      "and keys");
+    HostLengths h;
+    h.nseq = static_cast<int64_t>(cu_q.size()) - 1;
+    for (int64_t i = 0; i < h.nseq; ++i) {
+        const int64_t lq = cu_q[i + 1] - cu_q[i], lk = cu_k[i + 1] - cu_k[i];
+        TORCH_CHECK_VALUE(lq >= 0 && lk >= 0 && !(lq > 0 && lk == 0),
+                          "kohakutt_amd: sdpa_varlen offsets must not decrease, and a sequence with queries needs keys");
+        TORCH_CHECK_VALUE(!(causal && lq > lk),
+                          "kohakutt_amd: causal sdpa_varlen with more queries than keys in a sequence leaves queries "
+                          "without keys");
+        h.max_q = std::max(h.max_q, lq);
+        h.max_k = std::max(h.max_k, lk);
+        h.mask_values += lq * lk;
     }
-    TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type() &&
-                    (q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf),
-                "kohakutt_amd: sdpa_varlen takes bf16 / fp16 (or fp32, cast to bf16)");
-    q = kernel_operand(q, 0);
-    k = kernel_operand(k, 0);
-    v = kernel_operand(v, 0);
-    const int64_t nseq = cu_q_in.numel() - 1;
-    TORCH_CHECK(nseq >= 1 && cu_k_in.numel() == cu_q_in.numel(),
-                "kohakutt_amd: sdpa_varlen needs cumulative offsets [0, ..., total] of equal count for queries and keys");
-    Tensor cu_q = cu_q_in.to(q.device(), at::kInt).contiguous();
-    Tensor cu_k = cu_k_in.to(q.device(), at::kInt).contiguous();
+    return h;
+}
+
+Tensor offsets_tensor(at::IntArrayRef cu) {
+    Tensor t = at::empty({static_cast<int64_t>(cu.size())}, at::dtype(at::kInt));
+    int32_t* d = t.data_ptr<int32_t>();
+    for (size_t i = 0; i < cu.size(); ++i) {
+        TORCH_CHECK_VALUE(cu[i] >= 0 && cu[i] <= INT32_MAX, "kohakutt_amd: sdpa_varlen offsets must fit int32");
+        d[i] = static_cast<int32_t>(cu[i]);
+    }
+    return t;
+}
+
+// ktt::_varlen_plan(cu_q, cu_k, is_causal, scale, key_side): this build's plan of an
+// offset set, as CPU tensors the caller keeps on the device (the reference's plan,
+// aten_varlen.cpp:32-70, is Tensix tile records and mask tiles).  The kernels need only the
+// offsets: records = int32 [2, n + 1] (row 0 the query offsets, row 1 the key offsets);
+// masks = int64 [n + 1], entry i = sum_{j<i} Lq_j * Lk_j (where sequence i's block of a
+// block-packed per-row mask starts).  The offsets are validated here with the reference's
+// rules; key_side gives the same tables (the backward kernels read offsets, not tile rows).
+std::tuple<Tensor, Tensor> varlen_plan(at::IntArrayRef cu_q, at::IntArrayRef cu_k, bool is_causal, double scale,
+                                       bool key_side) {
+    (void)key_side;
+    TORCH_CHECK_NOT_IMPLEMENTED(scale > 0, "kohakutt_amd: _varlen_plan: the scale must be positive");
+    const HostLengths h = host_lengths(cu_q, cu_k, is_causal);
+    Tensor records = at::stack({offsets_tensor(cu_q), offsets_tensor(cu_k)});
+    Tensor masks = at::empty({h.nseq + 1}, at::dtype(at::kLong));
+    int64_t* m = masks.data_ptr<int64_t>();
+    m[0] = 0;
+    for (int64_t i = 0; i < h.nseq; ++i) m[i + 1] = m[i] + (cu_q[i + 1] - cu_q[i]) * (cu_k[i + 1] - cu_k[i]);
+    return {records, masks};
+}
+
+// One packed call's operands (after validation).
+struct VarlenCall {
+    Tensor q, k, v;                // bf16 / fp16 [T, H, D] (fp32 inputs cast at entry)
+    Tensor cu_q, cu_k;             // device int32 [n + 1]
+    Tensor mask_offsets;           // device int64 [n + 1] (packed masks; optional)
+    int64_t nseq = 0, max_q = 0, max_k = 0;
+    bool causal = false;
+    double scale = 0.0;
+    Tensor mask;                   // [Tk] key mask in logit units, or a block-packed mask
+    bool packed = false;
+};
+
+// Forward of a packed call: (out [Tq, H, D] in the input dtype, lse [H, Tq] fp32).
+std::tuple<Tensor, Tensor> run_varlen(const VarlenCall& c, bool fp32) {
+    const Tensor q = kernel_operand(c.q, 0), k = kernel_operand(c.k, 0), v = kernel_operand(c.v, 0);
     const int64_t Tq = q.size(0), H = q.size(1), D = q.size(2), Tk = k.size(0);
     Tensor out = at::empty({Tq, H, D}, q.options());
     Tensor lse = at::empty({H, Tq}, q.options().dtype(at::kFloat));
@@ -524,12 +681,12 @@ std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, c
     a.out = out.data_ptr();
     a.lse = lse.data_ptr<float>();
     a.dtype = code_of(q.scalar_type());
-    a.causal = is_causal ? 1 : 0;
-    a.batch = nseq;
+    a.causal = c.causal ? 1 : 0;
+    a.batch = c.nseq;
     a.heads_q = H;
     a.heads_kv = k.size(1);
-    a.seq_q = std::max<int64_t>(1, max_q);
-    a.seq_k = std::max<int64_t>(1, max_k);
+    a.seq_q = std::max<int64_t>(1, c.max_q);
+    a.seq_k = std::max<int64_t>(1, c.max_k);
     a.head_dim = D;
     // [T, H, D] tensors: stride[1] is the head stride, stride[2] the token stride.
     a.q_stride[1] = q.stride(1);
@@ -542,44 +699,23 @@ std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, c
     a.o_stride[2] = out.stride(0);
     a.lse_stride[1] = lse.stride(0);
     a.lse_stride[2] = lse.stride(1);
-    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
-    a.cu_seqlens_q = cu_q.data_ptr<int32_t>();
-    a.cu_seqlens_k = cu_k.data_ptr<int32_t>();
+    a.scale = c.scale;
+    a.cu_seqlens_q = c.cu_q.data_ptr<int32_t>();
+    a.cu_seqlens_k = c.cu_k.data_ptr<int32_t>();
     a.total_q = Tq;
     a.total_k = Tk;
-    Tensor m;
-    if (mask_given(key_mask)) {
-        m = *key_mask;
-        TORCH_CHECK(m.dim() == 1 && m.size(0) == Tk, "kohakutt_amd: sdpa_varlen key_mask must be [", Tk,
-                    "] (one value per packed key)");
-        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
-        m = m.to(q.device()).contiguous();
-        a.mask_mode = KMI_MASK_STRIDED;
-        a.mask_stride[3] = 1;
-    } else if (mask_given(attn_mask)) {
-        // The block-packed mask holds sum(Lq_i * Lk_i) values.  Host offsets are checked
-        // against it here; with device offsets the kernels treat reads past its end as
-        // masked (no host sync, so the call can be captured in a graph).
-        m = *attn_mask;
-        if (!cu_q_in.is_cuda() && !cu_k_in.is_cuda()) {
-            Tensor hq = cu_q_in.to(at::kLong).contiguous(), hk = cu_k_in.to(at::kLong).contiguous();
-            const int64_t* pq = hq.data_ptr<int64_t>();
-            const int64_t* pk = hk.data_ptr<int64_t>();
-            int64_t need = 0;
-            for (int64_t i = 0; i < nseq; ++i) need += (pq[i + 1] - pq[i]) * (pk[i + 1] - pk[i]);
-            TORCH_CHECK(m.numel() == need, "kohakutt_amd: sdpa_varlen packed mask must hold sum(Lq_i * Lk_i) = ",
-                        need, " values, got ", m.numel());
-        }
-        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
-        m = m.to(q.device()).contiguous().view({-1});
-        TORCH_CHECK(m.numel() > 0, "kohakutt_amd: sdpa_varlen packed mask is empty");
-        a.mask_mode = KMI_MASK_PACKED;
-        a.mask_numel = m.numel();
-    }
-    if (m.defined()) {
-        a.mask = m.data_ptr();
-        a.mask_dtype = code_of(m.scalar_type());
+    if (c.mask.defined()) {
+        a.mask = c.mask.data_ptr();
+        a.mask_dtype = code_of(c.mask.scalar_type());
         TORCH_CHECK(a.mask_dtype != 0, "kohakutt_amd: sdpa_varlen mask dtype must be bool or floating");
+        if (c.packed) {
+            a.mask_mode = KMI_MASK_PACKED;
+            a.mask_numel = c.mask.numel();
+            if (c.mask_offsets.defined()) a.mask_offsets = c.mask_offsets.data_ptr<int64_t>();
+        } else {
+            a.mask_mode = KMI_MASK_STRIDED;
+            a.mask_stride[3] = c.mask.stride(0);
+        }
     }
     size_t ws = 0;
     check(kmi_attn_workspace_bytes(&a, &ws), "kmi_attn_workspace_bytes");
@@ -588,6 +724,275 @@ std::tuple<Tensor, Tensor> sdpa_varlen(const Tensor& q_in, const Tensor& k_in, c
     check(kmi_attn_fwd(&a, ws ? work.data_ptr() : nullptr, ws, stream_of(q)), "kmi_attn_fwd (varlen)");
     g_attn_calls.fetch_add(1);
     return {fp32 ? out.to(at::kFloat) : out, lse};
+}
+
+// q, k, v of a packed call as the kernels take them: [T, H, D] of one dtype (fp32 cast to
+// bf16 at entry, like the dense route), K/V heads dividing Q heads, one head dim.
+void packed_operands(const char* op, const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, VarlenCall& c,
+                     bool& fp32) {
+    TORCH_CHECK(q_in.is_cuda() && k_in.is_cuda() && v_in.is_cuda() && k_in.device() == q_in.device() &&
+                    v_in.device() == q_in.device(),
+                "kohakutt_amd: ", op, " needs GPU tensors on one device");
+    TORCH_CHECK_NOT_IMPLEMENTED(q_in.dim() == 3 && k_in.dim() == 3 && v_in.dim() == 3,
+                                "kohakutt_amd: ", op, " takes q [Tq, H, D], k / v [Tk, Hk, D]");
+    TORCH_CHECK_NOT_IMPLEMENTED(k_in.size(0) == v_in.size(0) && k_in.size(1) == v_in.size(1) &&
+                                    k_in.size(1) > 0 && q_in.size(1) % k_in.size(1) == 0,
+                                "kohakutt_amd: ", op, " q / k / v shapes do not match (K / V heads must divide Q heads)");
+    TORCH_CHECK_NOT_IMPLEMENTED(q_in.size(2) == k_in.size(2) && v_in.size(2) == q_in.size(2) &&
+                                    head_dim_ok(q_in.size(2)),
+                                "kohakutt_amd: ", op, " needs one head dim, a multiple of 8 up to 256");
+    fp32 = q_in.scalar_type() == at::kFloat;
+    c.q = fp32 ? q_in.to(at::kBFloat16) : q_in;
+    c.k = fp32 ? k_in.to(at::kBFloat16) : k_in;
+    c.v = fp32 ? v_in.to(at::kBFloat16) : v_in;
+    const auto st = c.q.scalar_type();
+    TORCH_CHECK_NOT_IMPLEMENTED(c.k.scalar_type() == st && c.v.scalar_type() == st &&
+                                    (st == at::kBFloat16 || st == at::kHalf),
+                                "kohakutt_amd: ", op, " takes bf16 / fp16 tensors of one dtype (or fp32, cast to bf16)");
+}
+
+// The reference's key mask form (varlen.py:165-183: bf16 [Tk], already divided by the
+// scale, the -5e5 floor divided too) in logit units for the kernels: values at the floor
+// (within bf16 rounding) become -inf, which the kernels read as masked.
+Tensor key_mask_logits(const Tensor& key_mask, double scale, const Tensor& k) {
+    TORCH_CHECK_NOT_IMPLEMENTED(key_mask.dim() == 1 && key_mask.size(0) == k.size(0) && key_mask.is_floating_point(),
+                                "kohakutt_amd: _sdpa_varlen the key mask must be floating [key tokens]");
+    Tensor m = key_mask.to(k.device(), at::kFloat) * scale;
+    return m.masked_fill(m <= kMaskedLogit * (1.0 - 1.0 / 128.0), -INFINITY).contiguous();
+}
+
+// Row statistics of _sdpa_varlen outputs, by output storage: the reference keeps them
+// with the output's device handle for _sdpa_varlen_backward (aten_varlen.cpp:72-104).
+struct StatsEntry {
+    c10::weak_intrusive_ptr<c10::StorageImpl> out;
+    Tensor lse;
+};
+std::mutex g_stats_mutex;
+std::map<const c10::StorageImpl*, StatsEntry>& stats_table() {
+    static auto* table = new std::map<const c10::StorageImpl*, StatsEntry>();
+    return *table;
+}
+
+void remember_stats(const Tensor& out, const Tensor& lse) {
+    std::lock_guard<std::mutex> lock(g_stats_mutex);
+    auto& t = stats_table();
+    for (auto it = t.begin(); it != t.end();) it = it->second.out.expired() ? t.erase(it) : std::next(it);
+    c10::StorageImpl* impl = out.storage().unsafeGetStorageImpl();
+    t.insert_or_assign(impl, StatsEntry{out.storage().getWeakStorageImpl(), lse});
+}
+
+Tensor stats_of(const Tensor& out) {
+    std::lock_guard<std::mutex> lock(g_stats_mutex);
+    auto& t = stats_table();
+    auto it = t.find(out.storage().unsafeGetStorageImpl());
+    if (it == t.end() || it->second.out.expired()) return Tensor();
+    return it->second.lse;
+}
+
+// ktt::_sdpa_varlen (the reference's schema, aten_varlen.cpp:165-231,328-334): packed q
+// [Tq, H, D], k / v [Tk, Hk, D] with host offsets cu_q / cu_k and their _varlen_plan
+// tables (plan: records, masks) on q's device; returns (out [Tq, H, D], lse [H, Tq] when
+// `stats`, else an empty tensor).  key_mask: the reference's form (bf16 [Tk], divided by
+// the scale).  center: the reference's kernel takes centred keys for Tensix numerics (the
+// same output); these kernels take the keys as they are.
+std::tuple<Tensor, Tensor> sdpa_varlen_ref(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& plan,
+                                           const Tensor& masks, at::IntArrayRef cu_q, at::IntArrayRef cu_k,
+                                           bool is_causal, optional<double> scale, bool stats,
+                                           const optional<Tensor>& key_mask, bool center) {
+    (void)center;
+    const char* op = "_sdpa_varlen";
+    VarlenCall c;
+    bool fp32 = false;
+    packed_operands(op, q, k, v, c, fp32);
+    const HostLengths h = host_lengths(cu_q, cu_k, is_causal);
+    TORCH_CHECK_NOT_IMPLEMENTED(cu_q.back() == q.size(0) && cu_k.back() == k.size(0),
+                                "kohakutt_amd: ", op, " the offsets must end at the token counts");
+    TORCH_CHECK(plan.dim() == 2 && plan.size(0) == 2 && plan.size(1) == h.nseq + 1 && plan.scalar_type() == at::kInt,
+                "kohakutt_amd: ", op, " plan must be _varlen_plan's records [2, ", h.nseq + 1, "] of these offsets");
+    c10::DeviceGuard guard(q.device());
+    const Tensor rec = plan.to(q.device()).contiguous();
+    c.cu_q = rec[0];
+    c.cu_k = rec[1];
+    c.nseq = h.nseq;
+    c.max_q = h.max_q;
+    c.max_k = h.max_k;
+    c.causal = is_causal;
+    c.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(q.size(2)));
+    if (mask_given(key_mask)) c.mask = key_mask_logits(*key_mask, c.scale, c.k);
+    (void)masks;  // per-row mask offsets: the reference's schema carries no per-row mask
+    auto [out, lse] = run_varlen(c, fp32);
+    if (!stats) return {out, at::empty({0}, q.options().dtype(at::kFloat))};
+    remember_stats(out, lse);
+    return {out, lse};
+}
+
+// ktt::_sdpa_varlen_backward (the reference's schema, aten_varlen.cpp:237-319,336-340):
+// (dq, dk, dv) of a _sdpa_varlen call with `stats` from its output `out`, in one set of
+// kernel launches over every sequence (the forward's key mask and causal rule).
+std::tuple<Tensor, Tensor, Tensor> sdpa_varlen_backward_ref(
+    const Tensor& grad, const Tensor& out, const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& plan,
+    const Tensor& masks, const Tensor& key_plan, const Tensor& key_masks, at::IntArrayRef cu_q, at::IntArrayRef cu_k,
+    bool is_causal, optional<double> scale, const optional<Tensor>& key_mask) {
+    (void)masks, (void)key_plan, (void)key_masks;
+    const char* op = "_sdpa_varlen_backward";
+    VarlenCall c;
+    bool fp32 = false;
+    packed_operands(op, q, k, v, c, fp32);
+    TORCH_CHECK_NOT_IMPLEMENTED(!fp32, "kohakutt_amd: ", op, " takes bf16 / fp16 tensors");
+    const HostLengths h = host_lengths(cu_q, cu_k, is_causal);
+    TORCH_CHECK_NOT_IMPLEMENTED(cu_q.back() == q.size(0) && cu_k.back() == k.size(0),
+                                "kohakutt_amd: ", op, " the offsets must end at the token counts");
+    TORCH_CHECK_NOT_IMPLEMENTED(grad.sizes() == out.sizes() && grad.scalar_type() == q.scalar_type() &&
+                                    out.dim() == 3 && out.sizes() == q.sizes(),
+                                "kohakutt_amd: ", op, " grad and out must be the forward's [query tokens, heads, value dim]");
+    const Tensor lse = stats_of(out);
+    TORCH_CHECK_NOT_IMPLEMENTED(lse.defined(), "kohakutt_amd: ", op,
+                                " out is not an output of _sdpa_varlen with statistics");
+    TORCH_CHECK(plan.dim() == 2 && plan.size(0) == 2 && plan.size(1) == h.nseq + 1 && plan.scalar_type() == at::kInt,
+                "kohakutt_amd: ", op, " plan must be _varlen_plan's records [2, ", h.nseq + 1, "] of these offsets");
+    c10::DeviceGuard guard(q.device());
+    const Tensor rec = plan.to(q.device()).contiguous();
+    BwdCall b;
+    b.grad = grad;
+    b.q = q;
+    b.k = k;
+    b.v = v;
+    b.out = out;
+    b.lse = lse;
+    b.cu_q = rec[0];
+    b.cu_k = rec[1];
+    b.nseq = h.nseq;
+    b.max_q = h.max_q;
+    b.max_k = h.max_k;
+    b.causal = is_causal;
+    b.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(q.size(2)));
+    if (mask_given(key_mask)) b.mask = key_mask_logits(*key_mask, b.scale, k);
+    return run_backward(b);
+}
+
+// The offsets of a call that holds them as tensors: device int32 copies, and (when they
+// are host tensors) their validated lengths.  Device offsets are trusted: the kernels clamp
+// them into the packed token ranges, and max_q / max_k must cover every sequence.
+struct OffsetArgs {
+    Tensor cu_q, cu_k;
+    bool host = false;
+    HostLengths h;
+};
+
+OffsetArgs offset_args(const char* op, const Tensor& cu_q_in, const Tensor& cu_k_in, bool causal, int64_t tq,
+                       int64_t tk, int64_t max_q, int64_t max_k, const Tensor& q) {
+    TORCH_CHECK(cu_q_in.dim() == 1 && cu_k_in.dim() == 1 && cu_q_in.numel() >= 2 && cu_k_in.numel() == cu_q_in.numel(),
+                "kohakutt_amd: ", op, " needs cumulative offsets [0, ..., total] of equal count for queries and keys");
+    OffsetArgs o;
+    o.host = !cu_q_in.is_cuda() && !cu_k_in.is_cuda();
+    if (o.host) {
+        const Tensor hq = cu_q_in.to(at::kLong).contiguous(), hk = cu_k_in.to(at::kLong).contiguous();
+        const at::IntArrayRef aq(hq.data_ptr<int64_t>(), hq.numel()), ak(hk.data_ptr<int64_t>(), hk.numel());
+        o.h = host_lengths(aq, ak, causal);
+        TORCH_CHECK_VALUE(aq.back() == tq && ak.back() == tk, "kohakutt_amd: ", op,
+                          " the offsets must end at the token counts");
+        TORCH_CHECK_VALUE(max_q >= o.h.max_q && max_k >= o.h.max_k, "kohakutt_amd: ", op, " max_q / max_k (", max_q,
+                          ", ", max_k, ") are below the longest sequence (", o.h.max_q, ", ", o.h.max_k, ")");
+    }
+    o.cu_q = cu_q_in.to(q.device(), at::kInt).contiguous();
+    o.cu_k = cu_k_in.to(q.device(), at::kInt).contiguous();
+    return o;
+}
+
+// ktt::_sdpa_varlen_offsets: this build's packed op with the offsets as tensors (host or
+// device; device offsets need no host sync, so the call can be captured in a graph) --
+// what kohakutt_amd.sdpa_varlen and torch_attn::_varlen_attn call.  key_mask: [Tk] bool
+// keep-mask or additive (logit units); packed_mask: every sequence's row-major
+// [Lq_i, Lk_i] block, concatenated (bool or additive, shared by the heads, usable with
+// is_causal).  Returns (out [Tq, H, D], lse [H, Tq] fp32).
+std::tuple<Tensor, Tensor> sdpa_varlen_offsets(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in,
+                                               const Tensor& cu_q_in, const Tensor& cu_k_in, int64_t max_q,
+                                               int64_t max_k, bool is_causal, optional<double> scale,
+                                               const optional<Tensor>& key_mask, const optional<Tensor>& packed_mask) {
+    const char* op = "_sdpa_varlen_offsets";
+    VarlenCall c;
+    bool fp32 = false;
+    packed_operands(op, q_in, k_in, v_in, c, fp32);
+    TORCH_CHECK(!(mask_given(key_mask) && mask_given(packed_mask)),
+                "kohakutt_amd: sdpa_varlen takes key_mask or packed_mask, not both");
+    c10::DeviceGuard guard(q_in.device());
+    const OffsetArgs o = offset_args(op, cu_q_in, cu_k_in, is_causal, q_in.size(0), k_in.size(0), max_q, max_k, c.q);
+    c.cu_q = o.cu_q;
+    c.cu_k = o.cu_k;
+    c.nseq = cu_q_in.numel() - 1;
+    c.max_q = max_q;
+    c.max_k = max_k;
+    c.causal = is_causal;
+    c.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(q_in.size(2)));
+    if (mask_given(key_mask)) {
+        Tensor m = *key_mask;
+        TORCH_CHECK(m.dim() == 1 && m.size(0) == k_in.size(0), "kohakutt_amd: sdpa_varlen key_mask must be [",
+                    k_in.size(0), "] (one value per packed key)");
+        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
+        c.mask = m.to(q_in.device()).contiguous();
+    } else if (mask_given(packed_mask)) {
+        Tensor m = *packed_mask;
+        if (o.host)
+            TORCH_CHECK(m.numel() == o.h.mask_values, "kohakutt_amd: sdpa_varlen packed mask must hold sum(Lq_i * Lk_i) = ",
+                        o.h.mask_values, " values, got ", m.numel());
+        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
+        c.mask = m.to(q_in.device()).contiguous().view({-1});
+        TORCH_CHECK(c.mask.numel() > 0, "kohakutt_amd: sdpa_varlen packed mask is empty");
+        c.packed = true;
+        // Block offsets: prefix sums of Lq_i * Lk_i on the device (no host sync).
+        const Tensor lq = (c.cu_q.slice(0, 1) - c.cu_q.slice(0, 0, -1)).to(at::kLong);
+        const Tensor lk = (c.cu_k.slice(0, 1) - c.cu_k.slice(0, 0, -1)).to(at::kLong);
+        c.mask_offsets = at::cat({at::zeros({1}, lq.options()), (lq * lk).cumsum(0)});
+    }
+    return run_varlen(c, fp32);
+}
+
+// ktt::_sdpa_varlen_offsets_backward: (dq, dk, dv) of a _sdpa_varlen_offsets call from
+// its output and lse, in one set of kernel launches over every sequence.
+std::tuple<Tensor, Tensor, Tensor> sdpa_varlen_offsets_backward(
+    const Tensor& grad, const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out, const Tensor& lse,
+    const Tensor& cu_q_in, const Tensor& cu_k_in, int64_t max_q, int64_t max_k, bool is_causal,
+    optional<double> scale, const optional<Tensor>& key_mask, const optional<Tensor>& packed_mask) {
+    const char* op = "_sdpa_varlen_offsets_backward";
+    VarlenCall c;
+    bool fp32 = false;
+    packed_operands(op, q, k, v, c, fp32);
+    TORCH_CHECK_NOT_IMPLEMENTED(!fp32, "kohakutt_amd: ", op, " takes bf16 / fp16 tensors");
+    TORCH_CHECK(grad.sizes() == q.sizes() && out.sizes() == q.sizes() && grad.scalar_type() == q.scalar_type(),
+                "kohakutt_amd: ", op, " grad and out must be shaped and typed as q");
+    TORCH_CHECK(lse.dim() == 2 && lse.size(0) == q.size(1) && lse.size(1) == q.size(0) &&
+                    lse.scalar_type() == at::kFloat,
+                "kohakutt_amd: ", op, " lse must be the forward's fp32 [H, Tq]");
+    c10::DeviceGuard guard(q.device());
+    const OffsetArgs o = offset_args(op, cu_q_in, cu_k_in, is_causal, q.size(0), k.size(0), max_q, max_k, q);
+    BwdCall b;
+    b.grad = grad;
+    b.q = q;
+    b.k = k;
+    b.v = v;
+    b.out = out;
+    b.lse = lse.contiguous();
+    b.cu_q = o.cu_q;
+    b.cu_k = o.cu_k;
+    b.nseq = cu_q_in.numel() - 1;
+    b.max_q = max_q;
+    b.max_k = max_k;
+    b.causal = is_causal;
+    b.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(q.size(2)));
+    if (mask_given(key_mask)) {
+        Tensor m = *key_mask;
+        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
+        b.mask = m.to(q.device()).contiguous();
+    } else if (mask_given(packed_mask)) {
+        Tensor m = *packed_mask;
+        if (m.scalar_type() == at::kDouble) m = m.to(at::kFloat);
+        b.mask = m.to(q.device()).contiguous().view({-1});
+        b.packed = true;
+        const Tensor lq = (o.cu_q.slice(0, 1) - o.cu_q.slice(0, 0, -1)).to(at::kLong);
+        const Tensor lk = (o.cu_k.slice(0, 1) - o.cu_k.slice(0, 0, -1)).to(at::kLong);
+        b.mask_offsets = at::cat({at::zeros({1}, lq.options()), (lq * lk).cumsum(0)});
+    }
+    return run_backward(b);
 }
 
 // ---------------------------------------------------------------- norms
@@ -744,7 +1149,9 @@ Tensor rms_norm(const Tensor& input, c10::SymIntArrayRef normalized_shape, const
         shape_ok = s.has_value() && input.size(input.dim() - nd + i) == *s;
         if (shape_ok) width *= *s;
     }
-    if (!shape_ok || !norms_take(input, width, {&weight})) return at::compositeimplicitautograd::rms_norm_symint(input, normalized_shape, weight, eps);
+    if (!shape_ok || !norms_take(input, width, {&weight}) || !real_data(input) ||
+        (weight && weight->defined() && !real_data(*weight)))
+        return at::compositeimplicitautograd::rms_norm_symint(input, normalized_shape, weight, eps);
     const bool hw = weight && weight->defined();
     const bool grads = at::GradMode::is_enabled() && (input.requires_grad() || (hw && weight->requires_grad()));
     if (grads) return RmsNormFn::apply(input, hw ? weight : optional<Tensor>(), nd, e);
@@ -806,12 +1213,27 @@ struct StubInstall {
 }  // namespace kta
 
 TORCH_LIBRARY(ktt, m) {
-    m.def("rms_norm(Tensor x, Tensor? weight=None, Tensor? bias=None, float eps=1e-6) -> Tensor");
+    m.def("rms_norm(Tensor x, Tensor? weight, Tensor? bias, float eps) -> Tensor");  // aten_fused.cpp:114-116
+    // The reference's packed-attention ops (aten_varlen.cpp:323-341).
+    m.def("_varlen_plan(int[] cu_q, int[] cu_k, bool is_causal, float scale, bool key_side) -> (Tensor, Tensor)",
+          &kta::varlen_plan);
     m.def(
-        "_sdpa_varlen(Tensor q, Tensor k, Tensor v, Tensor cu_seq_q, Tensor cu_seq_k, int max_q, int max_k, "
-        "bool is_causal=False, float? scale=None, Tensor? key_mask=None, Tensor? attn_mask=None) -> (Tensor, Tensor)");
-    m.def("sdpa_refusal(Tensor q, Tensor k, Tensor v, Tensor? mask=None, bool is_causal=False) -> str",
-          TORCH_FN(kta::sdpa_refusal_op));
+        "_sdpa_varlen(Tensor q, Tensor k, Tensor v, Tensor plan, Tensor masks, int[] cu_q, int[] cu_k, "
+        "bool is_causal, float? scale, bool stats, Tensor? key_mask=None, bool center=False) -> (Tensor, Tensor)");
+    m.def(
+        "_sdpa_varlen_backward(Tensor grad, Tensor out, Tensor q, Tensor k, Tensor v, Tensor plan, Tensor masks, "
+        "Tensor key_plan, Tensor key_masks, int[] cu_q, int[] cu_k, bool is_causal, float? scale, "
+        "Tensor? key_mask=None) -> (Tensor, Tensor, Tensor)");
+    // This build's packed op with tensor offsets (host or device) and block-packed masks.
+    m.def(
+        "_sdpa_varlen_offsets(Tensor q, Tensor k, Tensor v, Tensor cu_seq_q, Tensor cu_seq_k, int max_q, int max_k, "
+        "bool is_causal=False, float? scale=None, Tensor? key_mask=None, Tensor? packed_mask=None) -> (Tensor, Tensor)");
+    m.def(
+        "_sdpa_varlen_offsets_backward(Tensor grad, Tensor q, Tensor k, Tensor v, Tensor out, Tensor lse, "
+        "Tensor cu_seq_q, Tensor cu_seq_k, int max_q, int max_k, bool is_causal=False, float? scale=None, "
+        "Tensor? key_mask=None, Tensor? packed_mask=None) -> (Tensor, Tensor, Tensor)");
+    m.def("sdpa_refusal(Tensor q, Tensor k, Tensor v, Tensor? mask, float dropout_p, bool is_causal, float? scale) "
+          "-> str");
     m.def("_set_enabled(bool attention, bool norms) -> ()", TORCH_FN(kta::set_enabled));
     m.def("counters() -> int[]", TORCH_FN(kta::counters));
     m.def("_sdpa_flash_backward(Tensor grad, Tensor q, Tensor k, Tensor v, Tensor out, Tensor lse, "
@@ -826,7 +1248,10 @@ TORCH_LIBRARY(ktt, m) {
 
 TORCH_LIBRARY_IMPL(ktt, CUDA, m) {
     m.impl("rms_norm", TORCH_FN(kta::ktt_rms_norm_cuda));
-    m.impl("_sdpa_varlen", TORCH_FN(kta::sdpa_varlen));
+    m.impl("_sdpa_varlen", TORCH_FN(kta::sdpa_varlen_ref));
+    m.impl("_sdpa_varlen_backward", TORCH_FN(kta::sdpa_varlen_backward_ref));
+    m.impl("_sdpa_varlen_offsets", TORCH_FN(kta::sdpa_varlen_offsets));
+    m.impl("_sdpa_varlen_offsets_backward", TORCH_FN(kta::sdpa_varlen_offsets_backward));
     m.impl("_sdpa_flash_backward", TORCH_FN(kta::sdpa_flash_backward_op));
     m.impl("_sdpa_lengths", TORCH_FN(kta::sdpa_lengths));
     m.impl("_sdpa_lengths_supported", TORCH_FN(kta::sdpa_lengths_supported));
@@ -835,6 +1260,7 @@ TORCH_LIBRARY_IMPL(ktt, CUDA, m) {
 
 TORCH_LIBRARY_IMPL(ktt, CompositeExplicitAutograd, m) {
     m.impl("rms_norm", TORCH_FN(kta::ktt_rms_norm_composite));
+    m.impl("sdpa_refusal", TORCH_FN(kta::sdpa_refusal_op));
 }
 
 TORCH_LIBRARY_IMPL(aten, CUDA, m) {

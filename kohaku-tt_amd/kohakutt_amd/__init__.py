@@ -10,8 +10,12 @@ PrivateUse1 when ``kohakutt`` is imported, ``src/kohakutt/torch_backend/registra
   ``aten::_scaled_dot_product_fused_attention_overrideable`` on the gfx950 kernels;
 * ``F.layer_norm`` (``aten::native_layer_norm``) and ``F.rms_norm`` (``aten::rms_norm`` at
   AutogradCUDA) run the gfx950 norm kernels with fp32 statistics;
-* ``torch.ops.ktt.rms_norm``, ``torch.ops.ktt._sdpa_varlen``, ``torch.ops.ktt.sdpa_refusal``;
-* ``torch.nn.attention.varlen.varlen_attn`` (``torch_attn::_varlen_attn``) on GPU tensors.
+* ``torch.ops.ktt.rms_norm``, ``torch.ops.ktt.sdpa_refusal`` and the reference's packed ops
+  ``torch.ops.ktt._varlen_plan`` / ``_sdpa_varlen`` / ``_sdpa_varlen_backward``, plus this
+  build's ``_sdpa_varlen_offsets`` (tensor offsets, per-row packed masks), all
+  differentiable where the reference's are;
+* ``torch.nn.attention.varlen.varlen_attn`` (``torch_attn::_varlen_attn`` and its
+  backward) on GPU tensors.
 
 Calls the kernels do not take keep torch's own CUDA/HIP paths.  The package raises
 ImportError when its native libraries are missing: there is no CPU or eager fallback.
@@ -44,7 +48,7 @@ _load()
 from . import attention  # noqa: E402
 from .attention import sdpa, sdpa_varlen  # noqa: E402,F401
 
-attention.install_varlen_kernel()
+attention.install()
 
 AVAILABLE = True
 
@@ -78,6 +82,9 @@ def reset_counters() -> None:
     torch.ops.ktt.reset_counters()
 
 
-def sdpa_refusal(q, k, v, mask=None, is_causal=False) -> str:
-    """Why the kernels do not take this attention call ('' when they do)."""
-    return torch.ops.ktt.sdpa_refusal(q, k, v, mask, bool(is_causal))
+def sdpa_refusal(q, k, v, mask=None, dropout_p=0.0, is_causal=False, scale=None) -> str:
+    """Why the kernels do not take this attention call ('' when they do); sizes, dtypes
+    and devices only, so meta tensors answer too (``ktt::sdpa_refusal``)."""
+    return torch.ops.ktt.sdpa_refusal(
+        q, k, v, mask, float(dropout_p), bool(is_causal), None if scale is None else float(scale)
+    )

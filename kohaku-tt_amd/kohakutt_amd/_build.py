@@ -30,7 +30,13 @@ ARCH = "gfx950"
 CAPI_LIB = PKG / "libkohakutt_amd.so"
 OPS_LIB = PKG / "_torch_ops.so"
 
-HIP_SOURCES = ["capi.hip", "norm.hip", "attention.hip", "attention_bwd.hip"]
+HIP_SOURCES = [
+    "capi.hip",
+    "norm.hip",
+    "attention.hip",
+    *[f"attention_d{d}.hip" for d in (32, 64, 96, 128, 192, 256)],
+    "attention_bwd.hip",
+]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -61,10 +67,10 @@ def _run(cmd):
 
 # Per-source extra flags.  The attention kernels never produce NaN from finite inputs
 # (masked logits are -inf or clamped), so max needs no NaN canonicalisation there.
-SOURCE_FLAGS = {"attention.hip": ["-fno-honor-nans"]}
+SOURCE_FLAGS = {f"attention_d{d}.hip": ["-fno-honor-nans"] for d in (32, 64, 96, 128, 192, 256)}
 
 
-def build_capi(jobs: int = 4) -> Path:
+def build_capi(jobs: int = 8) -> Path:
     """Compiles the HIP kernels and links ``libkohakutt_amd.so``."""
     BUILD.mkdir(exist_ok=True)
     objs = []

@@ -69,6 +69,7 @@ class AttnArgs(ctypes.Structure):
         ("num_splits", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
         ("key_lengths", ctypes.c_void_p),
+        ("mask_offsets", ctypes.c_void_p),
     ]
 
 
@@ -103,6 +104,17 @@ class AttnBwdArgs(ctypes.Structure):
         ("dv_stride", _I64x3),
         ("lse_stride", _I64x3),
         ("scale", ctypes.c_double),
+        ("mask", ctypes.c_void_p),
+        ("mask_dtype", ctypes.c_int32),
+        ("mask_mode", ctypes.c_int32),
+        ("mask_stride", _I64x4),
+        ("mask_numel", ctypes.c_int64),
+        ("mask_offsets", ctypes.c_void_p),
+        ("cu_seqlens_q", ctypes.c_void_p),
+        ("cu_seqlens_k", ctypes.c_void_p),
+        ("total_q", ctypes.c_int64),
+        ("total_k", ctypes.c_int64),
+        ("key_lengths", ctypes.c_void_p),
     ]
 
 

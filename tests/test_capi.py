@@ -68,7 +68,8 @@ def _args(**kw):
 @pytest.mark.parametrize(
     "kw,msg",
     [
-        (dict(head_dim=80), "head_dim must be 64 or 128"),
+        (dict(head_dim=84), "head_dim must be a multiple of 8 up to 256"),
+        (dict(head_dim=264), "head_dim must be a multiple of 8 up to 256"),
         (dict(dtype=capi.KMI_F32), "dtype must be BF16 or F16"),
         (dict(heads_kv=3), "heads_kv must divide heads_q"),
         (dict(q=0), "null q"),

@@ -107,7 +107,7 @@ def test_varlen_decode_output_and_lse(native, dev, nseq, hk):
     k = C.randn(g, cu_k[-1], hk, 128)
     v = C.randn(g, cu_k[-1], hk, 128)
     native.reset_counters()
-    out, lse = torch.ops.ktt._sdpa_varlen(
+    out, lse = torch.ops.ktt._sdpa_varlen_offsets(
         q.to(dev), k.to(dev), v.to(dev),
         torch.tensor(cu_q, dtype=torch.int32, device=dev), torch.tensor(cu_k, dtype=torch.int32, device=dev),
         1, max(lk), True, None, None, None,

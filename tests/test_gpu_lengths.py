@@ -11,6 +11,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 import attn_cases as C
 from oracle import attention as oatt
@@ -97,9 +98,10 @@ def test_lengths_match_the_mask_route(native, dev):
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     ln = torch.tensor(lengths, dtype=torch.int32, device=dev)
     a = torch.ops.ktt._sdpa_lengths(qd, kd, vd, ln, causal, None, False)
-    from kohakutt_amd.attention import _lengths_masked
+    from kohakutt_amd.attention import _padding_mask
 
-    b = _lengths_masked(qd, kd, vd, ln, causal, None)
+    keep = _padding_mask(ln, qd.size(2), kd.size(2), causal)
+    b = F.scaled_dot_product_attention(qd, kd, vd, attn_mask=keep, enable_gqa=qd.size(1) != kd.size(1))
     torch.cuda.synchronize()
     assert (a.float() - b.float()).abs().max().item() < 2e-2
 

@@ -68,20 +68,24 @@ def test_set_enabled_round_trip():
     assert c["attention_enabled"] and c["norms_enabled"]
 
 
-def test_varlen_kernel_registered_for_gpu():
-    assert katt.install_varlen_kernel()
+def test_varlen_kernels_and_autograd_registered():
+    has = torch._C._dispatch_has_kernel_for_dispatch_key
+    assert has("torch_attn::_varlen_attn", "CUDA")
+    assert has("torch_attn::_varlen_attn_backward", "CUDA")
+    for op in ("ktt::_sdpa_lengths", "ktt::_sdpa_varlen", "ktt::_sdpa_varlen_offsets"):
+        assert "Autograd[alias]" in torch._C._dispatch_dump(op), op
 
 
 def test_key_lengths_validation_follows_the_reference():
     """Host key lengths must lie in [1, Sk] with one per batch (``lengths.py:10-29``); a
     GPU tensor is not checked on the host (the kernels clamp it)."""
-    from kohakutt_amd.attention import device_lengths
+    from kohakutt_amd.attention import _as_counts
 
-    assert device_lengths([1, 5], 2, 5, "cpu").tolist() == [1, 5]
-    assert device_lengths(torch.tensor([3, 4]), 2, 5, "cpu").dtype == torch.int32
+    assert _as_counts([1, 5], 2, 5, "cpu").tolist() == [1, 5]
+    assert _as_counts(torch.tensor([3, 4]), 2, 5, "cpu").dtype == torch.int32
     with pytest.raises(ValueError, match="must lie in"):
-        device_lengths([0, 5], 2, 5, "cpu")
+        _as_counts([0, 5], 2, 5, "cpu")
     with pytest.raises(ValueError, match="must lie in"):
-        device_lengths([1, 6], 2, 5, "cpu")
+        _as_counts([1, 6], 2, 5, "cpu")
     with pytest.raises(ValueError, match="one length per batch"):
-        device_lengths([1, 2, 3], 2, 5, "cpu")
+        _as_counts([1, 2, 3], 2, 5, "cpu")
