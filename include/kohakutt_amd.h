@@ -224,7 +224,9 @@ int kmi_rms_norm_fwd(const void* x, const void* weight, const void* bias, void* 
  *   dweight = sum over rows of dy * x * rstd                          (per column).
  * dy / dx have x's dtype (BF16, F16 or F32); weight / dweight w_dtype; weight may be NULL
  * (then dweight must be NULL).  dweight needs kmi_rms_norm_bwd_workspace_bytes of fp32
- * workspace (per-chunk column sums, added in a fixed order: deterministic).
+ * workspace (per-block column sums, added in a fixed order: deterministic).  Rows of
+ * whole 16-byte vectors take one pass over dy and x (as kmi_layer_norm_bwd); others an
+ * element path.
  * Replaces the reference's RMSNorm training backward (RmsNormFunction, aten_norm.cpp:
  * 548-599; ktt_norm backward and column-sum programs, layernorm.md:90-102).
  */
@@ -233,6 +235,27 @@ int kmi_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t width, size_t* bytes)
 int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weight, const float* rstd,
                      void* dx, void* dweight, int64_t rows, int64_t width, int32_t x_dtype,
                      int32_t w_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * LayerNorm backward over rows of `width` contiguous elements, from the forward's fp32
+ * mean and rstd:
+ *   xh = (x - mean) * rstd, g = dy * weight (dy without a weight),
+ *   dx = rstd * (g - mean_row(g) - xh * mean_row(g * xh))            (per row),
+ *   dweight = sum over rows of dy * xh, dbias = sum over rows of dy   (per column).
+ * dy / dx have x's dtype (BF16, F16 or F32); weight / dweight w_dtype (x's or F32);
+ * dbias b_dtype; weight, dweight and dbias may be NULL (dweight needs weight).  Rows must
+ * be whole 16-byte vectors, 16-byte aligned, at most 256 vectors (else KMI_EUNSUPPORTED).
+ * dx in one pass over dy and x; dweight / dbias from per-block partial sums added in a
+ * fixed order (deterministic), in kmi_layer_norm_bwd_workspace_bytes of fp32 workspace.
+ * Replaces the reference's native_layer_norm_backward on its own programs
+ * (aten_norm.cpp:130-224,811; ktt_norm bwd_* and colsum_* programs, layernorm.md:90-102).
+ */
+int kmi_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t width, size_t* bytes);
+
+int kmi_layer_norm_bwd(const void* dy, const void* x, const float* mean, const float* rstd,
+                       const void* weight, void* dx, void* dweight, void* dbias, int64_t rows,
+                       int64_t width, int32_t x_dtype, int32_t w_dtype, int32_t b_dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* The message of the last failed call on this thread ("" if none). */
 const char* kmi_last_error(void);

@@ -243,7 +243,7 @@ extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t work
     p.total_k = static_cast<int>(a->total_k);
     if (pl.splits > 1) {
         p.part_o = static_cast<float*>(workspace);
-        p.part_lse = p.part_o + static_cast<size_t>(pl.splits) * p.rows_total * p.hq * a->head_dim;
+        p.part_lse = p.part_o + static_cast<size_t>(pl.splits) * p.rows_total * p.hq * padded_head_dim(a->head_dim);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     const hipError_t err = a->dtype == KMI_BF16 ? launch_dim<bf16>(p, pl, s) : launch_dim<f16>(p, pl, s);

@@ -473,6 +473,228 @@ int64_t rms_bwd_chunks(int64_t rows) {
     return std::min<int64_t>(kRmsBwdMaxChunks, std::max<int64_t>(1, ceil_div(rows, kRmsBwdRowsPerChunk)));
 }
 
+// Norm backward in one pass over dy and x (LayerNorm y = (x - m) r w + b; RMSNorm m = 0):
+//   xh = (x - m) r, g = dy w, dx = r (g - mean(g) [LayerNorm only] - xh mean(g xh)),
+//   dw = sum over rows of dy xh, db = sum over rows of dy
+// (the reference's ktt_norm backward and column-sum programs, layernorm.md:90-102; torch's
+// native_layer_norm_backward computes the same).  A 256-thread block takes a run of
+// consecutive rows; wavefront w takes rows w, w + 4, ... of it, holds a row in registers as
+// VPL 16-byte vectors per lane, reduces mean(g) and mean(g xh) across its lanes, writes dx
+// and adds dy xh (and dy) into per-lane column sums.  The four wavefronts' column sums
+// meet in LDS in wavefront order and the block writes one partial row pair;
+// norm_bwd_colsum adds the blocks' partials in block order (deterministic, no atomics).
+template <typename T, typename W, bool LAYER, int VPL, bool HW, bool HB>
+__global__ __launch_bounds__(256) void norm_bwd_rows(const T* dy, const T* x, const float* mean, const float* rstd,
+                                                     const W* weight, T* __restrict__ dx, float* __restrict__ part,
+                                                     int64_t rows, int width, int64_t rows_per_block) {
+    constexpr int E = 16 / sizeof(T);
+    extern __shared__ float colsum[];  // [2][width]: dw, db
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int nvec = width / E;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+    Param<W, E> gw[HW ? VPL : 1];
+    if constexpr (HW) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) gw[i].load(weight, min(lane + kWave * i, nvec - 1));
+    }
+    float aw[VPL][E], ab[HB ? VPL : 1][E];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            aw[i][j] = 0.f;
+            if constexpr (HB) ab[i][j] = 0.f;
+        }
+    const float inv_w = 1.f / static_cast<float>(width);
+    for (int64_t row = r0 + wave; row < r1; row += 4) {
+        const T* xr = x + row * width;
+        const T* gr = dy + row * width;
+        u32x4 rx[VPL], rg[VPL];
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int vc = min(lane + kWave * i, nvec - 1);
+            rx[i] = *reinterpret_cast<const u32x4*>(xr + vc * E);
+            rg[i] = *reinterpret_cast<const u32x4*>(gr + vc * E);
+        }
+#pragma unroll
+        for (int i = 0; i < VPL; ++i)
+            if (lane + kWave * i >= nvec) rx[i] = rg[i] = u32x4{0u, 0u, 0u, 0u};
+        const float m = LAYER ? mean[row] : 0.f, r = rstd[row];
+        float sg = 0.f, sgx = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            float xv[E], gv[E];
+            unpack<T>(rx[i], xv);
+            unpack<T>(rg[i], gv);
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                const float xh = (xv[j] - m) * r;
+                const float g = HW ? gv[j] * gw[i].at(j) : gv[j];
+                sg += g;
+                sgx += g * xh;
+                aw[i][j] += gv[j] * xh;
+                if constexpr (HB) ab[i][j] += gv[j];
+            }
+        }
+        sgx = wave_sum(sgx);
+        const float b = sgx * inv_w;
+        const float a = LAYER ? wave_sum(sg) * inv_w : 0.f;
+        T* dr = dx + row * width;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int vi = lane + kWave * i;
+            if (vi < nvec) {
+                float xv[E], gv[E], o[E];
+                unpack<T>(rx[i], xv);
+                unpack<T>(rg[i], gv);
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const float xh = (xv[j] - m) * r;
+                    const float g = HW ? gv[j] * gw[i].at(j) : gv[j];
+                    o[j] = r * (g - a - xh * b);
+                }
+                store_pack<T, E>(dr + vi * E, o);
+            }
+        }
+    }
+    // The wavefronts' column sums, added in wavefront order; wavefront 3 writes the block's
+    // partial rows [blockIdx.x][2][width].
+    float* pw = part + static_cast<int64_t>(blockIdx.x) * 2 * width;
+    for (int w = 0; w < 4; ++w) {
+        if (wave == w) {
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                const int vi = lane + kWave * i;
+                if (vi >= nvec) continue;
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const int col = vi * E + j;
+                    const float vw = aw[i][j] + (w > 0 ? colsum[col] : 0.f);
+                    const float vb = HB ? ab[i][j] + (w > 0 ? colsum[width + col] : 0.f) : 0.f;
+                    if (w < 3) {
+                        colsum[col] = vw;
+                        if (HB) colsum[width + col] = vb;
+                    } else {
+                        pw[col] = vw;
+                        if (HB) pw[width + col] = vb;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// dw (and db) from the blocks' partial rows: 64 columns per block, 16 lanes over the
+// partial rows (lane l takes rows l, l + 16, ...), their sums added in lane order.
+__global__ __launch_bounds__(1024) void norm_bwd_colsum(const float* part, void* dw, void* db, int w_dtype,
+                                                        int b_dtype, int nblocks, int width) {
+    __shared__ float red[2][16][64];
+    const int c = blockIdx.x * 64 + (threadIdx.x & 63), l = threadIdx.x >> 6;
+    float sw = 0.f, sb = 0.f;
+    if (c < width) {
+#pragma unroll 4
+        for (int b = l; b < nblocks; b += 16) {
+            sw += part[static_cast<int64_t>(b) * 2 * width + c];
+            if (db) sb += part[static_cast<int64_t>(b) * 2 * width + width + c];
+        }
+    }
+    red[0][l][threadIdx.x & 63] = sw;
+    red[1][l][threadIdx.x & 63] = sb;
+    __syncthreads();
+    if (l == 0 && c < width) {
+        float tw = 0.f, tb = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            tw += red[0][i][threadIdx.x];
+            tb += red[1][i][threadIdx.x];
+        }
+        if (dw) store_any(dw, w_dtype, c, tw);
+        if (db) store_any(db, b_dtype, c, tb);
+    }
+}
+
+// Blocks of the one-pass backward: about two per CU, whole wavefront rows each.
+int64_t norm_bwd_blocks(int64_t rows) { return std::max<int64_t>(1, std::min<int64_t>(512, ceil_div(rows, 4))); }
+int64_t norm_bwd_rows_per_block(int64_t rows) { return ceil_div(ceil_div(rows, norm_bwd_blocks(rows)), 4) * 4; }
+
+// The vector lanes the one-pass backward needs for a row (0 when it does not apply: the
+// row must be whole 16-byte vectors, 16-byte aligned, at most 4 vectors per lane: more
+// would take the column sums past the register file).
+int norm_bwd_vpl(const void* dy, const void* x, const void* dx, const void* w, int64_t width, int x_dtype, int w_dtype,
+                 int rows_align) {
+    const int xs = dtype_size(x_dtype);
+    if (xs == 0 || width % (16 / xs) != 0 || !aligned(dy, 16) || !aligned(x, 16) || !aligned(dx, 16)) return 0;
+    if (w && !(w_dtype == x_dtype || w_dtype == KMI_F32)) return 0;
+    if (w && !aligned(w, 16 / xs * dtype_size(w_dtype))) return 0;
+    (void)rows_align;
+    const int64_t nvec = width / (16 / xs);
+    const int64_t need = ceil_div(nvec, kWave);
+    if (need > 4) return 0;
+    int n = 1;
+    while (n < need) n <<= 1;
+    return n;
+}
+
+template <typename T, typename W, bool LAYER>
+hipError_t launch_norm_bwd(const void* dy, const void* x, const float* mean, const float* rstd, const void* w,
+                           void* dx, void* dw, void* db, int64_t rows, int width, int vpl, int w_dtype, int b_dtype,
+                           float* part, hipStream_t s) {
+    const int64_t nb = norm_bwd_blocks(rows), rpb = norm_bwd_rows_per_block(rows);
+    const size_t lds = static_cast<size_t>(2) * width * sizeof(float);
+    const bool hb = db != nullptr;
+    auto* dyp = static_cast<const T*>(dy);
+    auto* xp = static_cast<const T*>(x);
+    auto* wp = static_cast<const W*>(w);
+    auto* dxp = static_cast<T*>(dx);
+#define KMI_BWD_LAUNCH(N, HWV, HBV)                                                                        \
+    hipLaunchKernelGGL((norm_bwd_rows<T, W, LAYER, N, HWV, HBV>), dim3(static_cast<unsigned>(nb)), dim3(256), \
+                       lds, s, dyp, xp, mean, rstd, wp, dxp, part, rows, width, rpb)
+#define KMI_BWD_CASE(N)                                  \
+    case N:                                              \
+        if (w && hb) KMI_BWD_LAUNCH(N, true, true);      \
+        else if (w) KMI_BWD_LAUNCH(N, true, false);      \
+        else if (hb) KMI_BWD_LAUNCH(N, false, true);     \
+        else KMI_BWD_LAUNCH(N, false, false);            \
+        break;
+    switch (vpl) {
+        KMI_BWD_CASE(1)
+        KMI_BWD_CASE(2)
+        KMI_BWD_CASE(4)
+        default: return hipErrorInvalidValue;
+    }
+#undef KMI_BWD_CASE
+#undef KMI_BWD_LAUNCH
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || (!dw && !db)) return err;
+    hipLaunchKernelGGL(norm_bwd_colsum, dim3(static_cast<unsigned>(ceil_div(width, 64))), dim3(1024), 0, s, part, dw,
+                       db, w_dtype, b_dtype, static_cast<int>(nb), width);
+    return hipGetLastError();
+}
+
+template <bool LAYER>
+hipError_t norm_bwd_dispatch(const void* dy, const void* x, const float* mean, const float* rstd, const void* w,
+                             void* dx, void* dw, void* db, int64_t rows, int width, int vpl, int x_dtype, int w_dtype,
+                             int b_dtype, float* part, hipStream_t s) {
+    const bool pf32 = w && w_dtype == KMI_F32;
+    switch (x_dtype) {
+        case KMI_BF16:
+            return pf32 ? launch_norm_bwd<bf16, float, LAYER>(dy, x, mean, rstd, w, dx, dw, db, rows, width, vpl,
+                                                              w_dtype, b_dtype, part, s)
+                        : launch_norm_bwd<bf16, bf16, LAYER>(dy, x, mean, rstd, w, dx, dw, db, rows, width, vpl,
+                                                             w_dtype, b_dtype, part, s);
+        case KMI_F16:
+            return pf32 ? launch_norm_bwd<f16, float, LAYER>(dy, x, mean, rstd, w, dx, dw, db, rows, width, vpl,
+                                                             w_dtype, b_dtype, part, s)
+                        : launch_norm_bwd<f16, f16, LAYER>(dy, x, mean, rstd, w, dx, dw, db, rows, width, vpl,
+                                                           w_dtype, b_dtype, part, s);
+        default:
+            return launch_norm_bwd<float, float, LAYER>(dy, x, mean, rstd, w, dx, dw, db, rows, width, vpl, w_dtype,
+                                                        b_dtype, part, s);
+    }
+}
+
 template <bool LAYER>
 int norm_fwd(const char* name, const void* x, const void* w, const void* b, void* y,
              float* mean, float* rstd, int64_t rows, int64_t width, int x_dtype,
@@ -556,8 +778,52 @@ extern "C" int kmi_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t width, siz
     using namespace kmi;
     if (!bytes) return fail(KMI_EINVAL, "kmi_rms_norm_bwd_workspace_bytes: null bytes");
     if (rows < 0 || width < 0) return fail(KMI_EINVAL, "kmi_rms_norm_bwd_workspace_bytes: negative size");
-    *bytes = rows == 0 ? 0 : static_cast<size_t>(rms_bwd_chunks(rows) * width) * sizeof(float);
+    // Enough for either path: the one-pass kernel's per-block partial rows or the
+    // row-chunk column sums of the element path.
+    const int64_t n = std::max(rms_bwd_chunks(rows), 2 * norm_bwd_blocks(rows)) * width;
+    *bytes = rows == 0 ? 0 : static_cast<size_t>(n) * sizeof(float);
     return KMI_OK;
+}
+
+extern "C" int kmi_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t width, size_t* bytes) {
+    using namespace kmi;
+    if (!bytes) return fail(KMI_EINVAL, "kmi_layer_norm_bwd_workspace_bytes: null bytes");
+    if (rows < 0 || width < 0) return fail(KMI_EINVAL, "kmi_layer_norm_bwd_workspace_bytes: negative size");
+    *bytes = rows == 0 ? 0 : static_cast<size_t>(2 * norm_bwd_blocks(rows) * width) * sizeof(float);
+    return KMI_OK;
+}
+
+extern "C" int kmi_layer_norm_bwd(const void* dy, const void* x, const float* mean, const float* rstd,
+                                  const void* weight, void* dx, void* dweight, void* dbias, int64_t rows,
+                                  int64_t width, int32_t x_dtype, int32_t w_dtype, int32_t b_dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    using namespace kmi;
+    const char* name = "kmi_layer_norm_bwd";
+    if (dtype_size(x_dtype) == 0) return fail(KMI_EINVAL, std::string(name) + ": x dtype must be BF16, F16 or F32");
+    if ((weight || dweight) && dtype_size(w_dtype) == 0)
+        return fail(KMI_EINVAL, std::string(name) + ": weight dtype must be BF16, F16 or F32");
+    if (dbias && dtype_size(b_dtype) == 0)
+        return fail(KMI_EINVAL, std::string(name) + ": bias dtype must be BF16, F16 or F32");
+    if (rows < 0 || width < 0) return fail(KMI_EINVAL, std::string(name) + ": negative size");
+    if (rows == 0) return KMI_OK;
+    if (width == 0) return fail(KMI_EINVAL, std::string(name) + ": empty rows");
+    if (!dy || !x || !mean || !rstd || !dx) return fail(KMI_EINVAL, std::string(name) + ": null dy, x, mean, rstd or dx");
+    if (dweight && !weight) return fail(KMI_EINVAL, std::string(name) + ": dweight needs weight");
+    if (rows > (int64_t{1} << 40) || width > (int64_t{1} << 30))
+        return fail(KMI_EUNSUPPORTED, std::string(name) + ": too many rows or too wide");
+    const int vpl = norm_bwd_vpl(dy, x, dx, weight, width, x_dtype, w_dtype, 0);
+    if (vpl == 0)
+        return fail(KMI_EUNSUPPORTED, std::string(name) + ": rows must be whole 16-byte vectors (16-byte aligned, "
+                                                          "at most 256 vectors) with weight in x's dtype or fp32");
+    const size_t need = static_cast<size_t>(2 * norm_bwd_blocks(rows) * width) * sizeof(float);
+    if ((dweight || dbias) && (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 4))
+        return fail(KMI_EWORKSPACE, std::string(name) + ": workspace missing or smaller than "
+                                                        "kmi_layer_norm_bwd_workspace_bytes");
+    const hipError_t err =
+        norm_bwd_dispatch<true>(dy, x, mean, rstd, weight, dx, dweight, dbias, rows, static_cast<int>(width), vpl,
+                                x_dtype, w_dtype, b_dtype, static_cast<float*>(workspace),
+                                static_cast<hipStream_t>(stream));
+    return hip_status(err, name);
 }
 
 extern "C" int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weight, const float* rstd, void* dx,
@@ -576,12 +842,20 @@ extern "C" int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weigh
     if (rows > (int64_t{1} << 31) || width > (int64_t{1} << 30))
         return fail(KMI_EUNSUPPORTED, std::string(name) + ": too many rows or too wide");
     const int64_t chunks = rms_bwd_chunks(rows);
-    if (dweight && (!workspace || workspace_bytes < static_cast<size_t>(chunks * width) * sizeof(float) ||
-                    reinterpret_cast<uintptr_t>(workspace) % 4))
+    const size_t need = static_cast<size_t>(std::max(chunks, 2 * norm_bwd_blocks(rows)) * width) * sizeof(float);
+    if (dweight && (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 4))
         return fail(KMI_EWORKSPACE, std::string(name) + ": workspace missing or smaller than "
                                                         "kmi_rms_norm_bwd_workspace_bytes");
     hipStream_t s = static_cast<hipStream_t>(stream);
     float* part = static_cast<float*>(workspace);
+    // Whole-vector rows: the one-pass kernel (dy and x read once); otherwise the element
+    // path (a dx pass and a column-sum pass).
+    const int vpl = norm_bwd_vpl(dy, x, dx, weight, width, x_dtype, w_dtype, 0);
+    if (vpl > 0) {
+        const hipError_t e1 = norm_bwd_dispatch<false>(dy, x, nullptr, rstd, weight, dx, dweight, nullptr, rows,
+                                                       static_cast<int>(width), vpl, x_dtype, w_dtype, 0, part, s);
+        return hip_status(e1, name);
+    }
     const int wd = static_cast<int>(w_dtype);
     hipError_t err;
     switch (x_dtype) {

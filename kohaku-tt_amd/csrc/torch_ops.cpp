@@ -16,6 +16,7 @@
 #include <ATen/ATen.h>
 #include <ATen/native/transformers/attention.h>
 #include <ATen/ops/_fused_sdp_choice_cuda_dispatch.h>
+#include <ATen/ops/native_layer_norm_backward_cuda_dispatch.h>
 #include <ATen/ops/native_layer_norm_cuda_dispatch.h>
 #include <ATen/ops/rms_norm_compositeimplicitautograd_dispatch.h>
 #include <ATen/ops/scaled_dot_product_attention_compositeimplicitautograd_dispatch.h>
@@ -1053,6 +1054,52 @@ std::tuple<Tensor, Tensor, Tensor> native_layer_norm(const Tensor& input, at::In
     return {y, mean, rstd};
 }
 
+// aten::native_layer_norm_backward on CUDA (the reference's own backward programs,
+// aten_norm.cpp:130-224,811): the one-pass kernel (kmi_layer_norm_bwd) when the forward's
+// statistics are this build's fp32 ones and the rows are whole 16-byte vectors of at most
+// 256 vectors; torch's CUDA kernel otherwise.
+std::tuple<Tensor, Tensor, Tensor> native_layer_norm_backward(const Tensor& grad_out, const Tensor& input,
+                                                              at::IntArrayRef normalized_shape, const Tensor& mean,
+                                                              const Tensor& rstd, const optional<Tensor>& weight,
+                                                              const optional<Tensor>& bias,
+                                                              std::array<bool, 3> output_mask) {
+    const int64_t nd = static_cast<int64_t>(normalized_shape.size());
+    int64_t width = 1;
+    for (auto s : normalized_shape) width *= s;
+    const bool hw = weight && weight->defined(), hb = bias && bias->defined();
+    const auto wt = hw ? weight->scalar_type() : input.scalar_type();
+    const int xs = input.element_size();
+    bool take = g_norms.load() && input.is_cuda() && norm_dtype(input.scalar_type()) && input.numel() > 0 &&
+                grad_out.scalar_type() == input.scalar_type() && grad_out.sizes() == input.sizes() && nd >= 1 &&
+                nd <= input.dim() && mean.scalar_type() == at::kFloat && rstd.scalar_type() == at::kFloat &&
+                mean.numel() * width == input.numel() && rstd.numel() == mean.numel() && width % (16 / xs) == 0 &&
+                width / (16 / xs) <= 4 * 64 && (!hw || wt == input.scalar_type() || wt == at::kFloat) &&
+                (!hb || bias->scalar_type() == wt) && real_data(input) && real_data(grad_out);
+    if (!take)
+        return at::cuda::native_layer_norm_backward(grad_out, input, normalized_shape, mean, rstd, weight, bias,
+                                                    output_mask);
+    c10::DeviceGuard guard(input.device());
+    const Tensor x = input.contiguous(), gy = grad_out.contiguous();
+    const Tensor m = mean.contiguous(), r = rstd.contiguous();
+    const Tensor w = hw ? weight->contiguous() : Tensor();
+    const int64_t rows = x.numel() / width;
+    Tensor dx = at::empty_like(x);
+    Tensor dw = (output_mask[1] && hw) ? at::empty_like(w) : Tensor();
+    Tensor db = (output_mask[2] && hb) ? at::empty({width}, x.options().dtype(wt)).view(bias->sizes()) : Tensor();
+    size_t ws = 0;
+    check(kmi_layer_norm_bwd_workspace_bytes(rows, width, &ws), "kmi_layer_norm_bwd_workspace_bytes");
+    Tensor work;
+    if ((dw.defined() || db.defined()) && ws) work = at::empty({static_cast<int64_t>(ws)}, x.options().dtype(at::kByte));
+    check(kmi_layer_norm_bwd(gy.data_ptr(), x.data_ptr(), m.data_ptr<float>(), r.data_ptr<float>(),
+                             hw ? w.data_ptr() : nullptr, dx.data_ptr(), dw.defined() ? dw.data_ptr() : nullptr,
+                             db.defined() ? db.data_ptr() : nullptr, rows, width, code_of(x.scalar_type()),
+                             hw ? code_of(wt) : 0, db.defined() ? code_of(wt) : 0,
+                             work.defined() ? work.data_ptr() : nullptr, ws, stream_of(x)),
+          "kmi_layer_norm_bwd");
+    g_norm_bwd_calls.fetch_add(1);
+    return {output_mask[0] ? dx.view(input.sizes()) : Tensor(), dw, db};
+}
+
 // y, rstd of RMSNorm over the trailing dims (width elements per row), optional bias.
 std::tuple<Tensor, Tensor> rms_forward(const Tensor& input, int64_t width, optional<Tensor> w, optional<Tensor> b,
                                        double eps, int64_t nd) {
@@ -1268,6 +1315,7 @@ TORCH_LIBRARY_IMPL(aten, CUDA, m) {
     m.impl("_scaled_dot_product_fused_attention_overrideable", TORCH_FN(kta::sdpa_overrideable));
     m.impl("_scaled_dot_product_fused_attention_overrideable_backward", TORCH_FN(kta::sdpa_overrideable_backward));
     m.impl("native_layer_norm", TORCH_FN(kta::native_layer_norm));
+    m.impl("native_layer_norm_backward", TORCH_FN(kta::native_layer_norm_backward));
 }
 
 TORCH_LIBRARY_IMPL(aten, AutogradCUDA, m) {

@@ -26,6 +26,8 @@ EXPORTS = (
     "kmi_rms_norm_fwd",
     "kmi_rms_norm_bwd_workspace_bytes",
     "kmi_rms_norm_bwd",
+    "kmi_layer_norm_bwd_workspace_bytes",
+    "kmi_layer_norm_bwd",
     "kmi_last_error",
     "kmi_abi_version",
 )
@@ -143,6 +145,9 @@ def lib():
         h.kmi_rms_norm_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, ctypes.c_double, vp]
         h.kmi_rms_norm_bwd_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(ctypes.c_size_t)]
         h.kmi_rms_norm_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i32, i32, vp, ctypes.c_size_t, vp]
+        h.kmi_layer_norm_bwd_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(ctypes.c_size_t)]
+        h.kmi_layer_norm_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, vp,
+                                         ctypes.c_size_t, vp]
         h.kmi_last_error.restype = ctypes.c_char_p
         h.kmi_last_error.argtypes = []
         h.kmi_abi_version.argtypes = []

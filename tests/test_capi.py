@@ -146,7 +146,9 @@ def test_rms_norm_backward_rejects_malformed_calls_before_launch():
     lib = capi.lib()
     n = ctypes.c_size_t()
     assert lib.kmi_rms_norm_bwd_workspace_bytes(2048, 896, ctypes.byref(n)) == capi.KMI_OK
-    assert n.value == 128 * 896 * 4  # 16-row chunks of fp32 column sums
+    # the larger of the one-pass kernel's partial rows (2 x 512 blocks) and the element
+    # path's 16-row chunks (128) of fp32 column sums
+    assert n.value == max(2 * 512, 128) * 896 * 4
     assert lib.kmi_rms_norm_bwd_workspace_bytes(-1, 896, ctypes.byref(n)) == capi.KMI_EINVAL
     p = 0x1000
     # Unknown dtype, null operands, dweight without weight, missing workspace.
@@ -157,3 +159,24 @@ def test_rms_norm_backward_rejects_malformed_calls_before_launch():
     assert lib.kmi_rms_norm_bwd(p, p, p, p, p, p, 4, 64, capi.KMI_BF16, capi.KMI_BF16, None, 0, None) == capi.KMI_EWORKSPACE
     # No rows: nothing to do.
     assert lib.kmi_rms_norm_bwd(p, p, p, p, p, p, 0, 64, capi.KMI_BF16, capi.KMI_BF16, None, 0, None) == capi.KMI_OK
+
+
+def test_layer_norm_backward_rejects_malformed_calls_before_launch():
+    lib = capi.lib()
+    n = ctypes.c_size_t()
+    assert lib.kmi_layer_norm_bwd_workspace_bytes(8192, 640, ctypes.byref(n)) == capi.KMI_OK
+    assert n.value == 2 * 512 * 640 * 4  # dweight and dbias partial rows of 512 blocks
+    assert lib.kmi_layer_norm_bwd_workspace_bytes(3, 640, ctypes.byref(n)) == capi.KMI_OK
+    assert n.value == 2 * 1 * 640 * 4
+    p = 0x1000
+    bf = capi.KMI_BF16
+    call = lib.kmi_layer_norm_bwd
+    assert call(p, p, p, p, p, p, p, p, 4, 64, 9, bf, bf, None, 0, None) == capi.KMI_EINVAL
+    assert call(p, p, None, p, p, p, p, p, 4, 64, bf, bf, bf, None, 0, None) == capi.KMI_EINVAL
+    assert call(p, p, p, p, None, p, p, None, 4, 64, bf, bf, bf, None, 0, None) == capi.KMI_EINVAL
+    assert "dweight needs weight" in lib.kmi_last_error().decode()
+    assert call(p, p, p, p, p, p, p, p, 4, 64, bf, bf, bf, None, 0, None) == capi.KMI_EWORKSPACE
+    # rows that are not whole 16-byte vectors, or too wide for the one-pass kernel
+    assert call(p, p, p, p, p, p, None, None, 4, 60, bf, bf, bf, None, 0, None) == capi.KMI_EUNSUPPORTED
+    assert call(p, p, p, p, p, p, None, None, 4, 4096, bf, bf, bf, None, 0, None) == capi.KMI_EUNSUPPORTED
+    assert call(p, p, p, p, p, p, p, p, 0, 64, bf, bf, bf, None, 0, None) == capi.KMI_OK

@@ -298,8 +298,11 @@ def test_varlen_packed_mask_backward(native, dev):
         n = b - a
         m = pm[off:off + n * n].reshape(n, n).double().clamp_min(-5e5)
         off += n * n
-        dead = (m <= -5e5).all(-1, keepdim=True)
-        m = m.masked_fill(dead.expand_as(m), 0.0)
+        # causal visibility stays; a row whose visible keys are all masked attends over
+        # their raw scores (the forward's rule)
+        vis = torch.ones(n, n, dtype=torch.bool).tril()
+        dead = ((m <= -5e5) | ~vis).all(-1, keepdim=True)
+        m = m.masked_fill(dead & vis, 0.0).masked_fill(~vis, float("-inf"))
         qs, ks, vs = (t.double().transpose(0, 1)[None].requires_grad_() for t in (q[a:b], k[a:b], v[a:b]))
         o = F.scaled_dot_product_attention(qs, ks.repeat_interleave(2, 1), vs.repeat_interleave(2, 1), attn_mask=m)
         o.backward(go[a:b].double().transpose(0, 1)[None])

@@ -66,8 +66,8 @@ def test_rms_norm(native, dev, shape, dtype):
     torch.cuda.synchronize()
     assert native.counters()["norms"] == 1
     yr, _ = onorm.rms_norm(C.f64(x), C.f64(w), eps=1e-6)
-    # the CPU same-dtype reference: fp32 math, one rounding (as the kernels)
-    cpu = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()).to(dtype)
+    # the reference's CPU path at the same dtype (tests/hardware/ops/test_norm.py:25-38)
+    cpu = F.rms_norm(x, [shape[-1]], w, 1e-6)
     _check(f"RMS {shape} {dtype}", y.cpu(), cpu, torch.from_numpy(yr), dtype)
 
 
@@ -78,7 +78,8 @@ def test_ktt_rms_norm_bias_and_stats(native, dev):
     b = C.randn(g, 896)
     y = torch.ops.ktt.rms_norm(x.to(dev), w.to(dev), b.to(dev), 1e-6).cpu()
     yr, _ = onorm.rms_norm(C.f64(x), C.f64(w), C.f64(b), eps=1e-6)
-    cpu = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float() + b.float()).bfloat16()
+    # ktt::rms_norm's CPU path: the fp32 composite (aten_fused.cpp:13-28) rounded once
+    cpu = torch.ops.ktt.rms_norm(x, w, b, 1e-6)
     _check("ktt.rms_norm bias", y, cpu, torch.from_numpy(yr), torch.bfloat16)
 
 
@@ -124,7 +125,7 @@ def test_norm_configs_and_repeat_bit_identical(native, dev):
             y = F.rms_norm(xd, [W], wd, eps)
             y2 = F.rms_norm(xd, [W], wd, eps)
             yr, _ = onorm.rms_norm(C.f64(x), C.f64(w), eps=eps)
-            cpu = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps) * w.float()).bfloat16()
+            cpu = F.rms_norm(x, [W], w, eps)
         else:
             y = F.layer_norm(xd, [W], wd, b.to(dev), eps)
             y2 = F.layer_norm(xd, [W], wd, b.to(dev), eps)
@@ -175,3 +176,104 @@ def test_rms_norm_backward_kernels_match_float64(native, dev, shape, x_dtype, w_
     torch.cuda.synchronize()
     again = [xd.grad] + ([] if wd is None else [wd.grad])
     assert all(torch.equal(a, b) for a, b in zip(first, again))
+
+
+LN_BWD = [
+    # shape, x dtype, weight dtype (None: no affine), bias
+    ((1, 197, 768), torch.bfloat16, torch.bfloat16, True),
+    ((2, 4096, 640), torch.bfloat16, torch.bfloat16, True),
+    ((33, 64), torch.float16, torch.float32, True),
+    ((5, 7, 1000), torch.float32, torch.float32, False),
+    ((3, 2048), torch.bfloat16, None, False),
+    ((1025, 128), torch.bfloat16, torch.bfloat16, False),
+]
+
+
+@pytest.mark.parametrize("shape,x_dtype,w_dtype,has_bias", LN_BWD)
+def test_layer_norm_backward_kernel(native, dev, shape, x_dtype, w_dtype, has_bias):
+    """aten::native_layer_norm_backward on the one-pass kernel: dx, dweight, dbias against
+    float64 autograd; median relative error at most 1.5x torch CPU autograd at the same
+    dtype; repeat calls bit-identical."""
+    from oracle.ruler import diff_stats
+
+    print(f"LN backward {shape} {x_dtype} {w_dtype} bias={has_bias}", flush=True)
+    g = torch.Generator().manual_seed(41 + shape[-1])
+    width = shape[-1]
+    x = (torch.randn(*shape, generator=g) * 2 + 0.3).to(x_dtype)
+    gy = torch.randn(*shape, generator=g).to(x_dtype)
+    w = None if w_dtype is None else (1 + 0.1 * torch.randn(width, generator=g)).to(w_dtype)
+    b = None if not has_bias else (0.1 * torch.randn(width, generator=g)).to(w_dtype)
+
+    def run(device, dtype=None):
+        cast = (lambda t: t.to(dtype)) if dtype is not None else (lambda t: t)
+        xx = cast(x).to(device).requires_grad_()
+        ww = None if w is None else cast(w).to(device).requires_grad_()
+        bb = None if b is None else cast(b).to(device).requires_grad_()
+        F.layer_norm(xx, (width,), ww, bb, 1e-5).backward(cast(gy).to(device))
+        return [t.grad for t in (xx, ww, bb) if t is not None]
+
+    native.reset_counters()
+    got = run(dev)
+    torch.cuda.synchronize()
+    assert native.counters()["norms_backward"] == 1, native.counters()
+    ref = run("cpu", torch.float64)
+    cpu = run("cpu")
+    for name, a, c, r in zip(("dx", "dw", "db"), got, cpu, ref):
+        sg, sc = diff_stats(a.cpu(), r), diff_stats(c, r)
+        print(f"  {name}: gpu rel_median {sg['rel_median']:.2e} cpu {sc['rel_median']:.2e}", flush=True)
+        assert sg["nonfinite"] == 0 and sg["rel_median"] <= 1.5 * sc["rel_median"] + 1e-7, (name, sg, sc)
+    again = run(dev)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b2) for a, b2 in zip(got, again))
+
+
+def test_layer_norm_backward_wide_rows_keep_torch_kernel(native, dev):
+    """Rows past 256 vectors take torch's own CUDA backward (fed this build's statistics)."""
+    x = torch.randn(4, 4096, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    native.reset_counters()
+    F.layer_norm(x, (4096,)).sum().backward()
+    torch.cuda.synchronize()
+    c = native.counters()
+    assert c["norms"] == 1 and c["norms_backward"] == 0, c
+    assert torch.isfinite(x.grad).all()
+
+
+def test_rms_norm_forward_and_backward_capture_in_a_graph(native, dev):
+    """RMSNorm forward and backward captured in one HIP graph after a side-stream warm-up
+    (the autograd engine runs each backward node on its forward's stream, so the forward
+    is captured on the capture stream too); every replay matches the eager result."""
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(2048, 896, generator=g).bfloat16().to(dev).requires_grad_()
+    w = (1 + 0.02 * torch.randn(896, generator=g)).bfloat16().to(dev).requires_grad_()
+    gy = torch.randn(2048, 896, generator=g).bfloat16().to(dev)
+
+    def step():
+        x.grad = None
+        w.grad = None
+        y = F.rms_norm(x, (896,), w, 1e-6)
+        y.backward(gy)
+        return y
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    y_eager = step().detach().clone()
+    dx_eager, dw_eager = x.grad.clone(), w.grad.clone()
+    graph = torch.cuda.CUDAGraph()
+    x.grad = None
+    w.grad = None
+    with torch.cuda.graph(graph):
+        y_static = F.rms_norm(x, (896,), w, 1e-6)
+        y_static.backward(gy)
+    dx_static, dw_static = x.grad, w.grad
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_static, y_eager)
+        assert torch.equal(dx_static, dx_eager) and torch.equal(dw_static, dw_eager)
+        step()  # eager work between replays
+        torch.cuda.synchronize()
