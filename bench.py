@@ -66,12 +66,14 @@ def parse():
 class Row:
     """One benchmark row: ``make(n)`` returns n call closures over distinct input sets
     on the GPU and the CPU reference closure; ``work`` is FLOPs (mfma) or bytes (hbm)
-    per call; ``flops`` / ``bytes`` both when known."""
+    per call; ``flops`` / ``bytes`` both when known.  ``counter`` names the
+    ``kohakutt_amd.counters()`` entry each call adds one to when the kernels take it
+    (None for rows that call the C ABI directly: no routing decision to check)."""
 
-    def __init__(self, name, label, bound, flops, nbytes, make, kernel):
+    def __init__(self, name, label, bound, flops, nbytes, make, kernel, counter):
         self.name, self.label, self.bound = name, label, bound
         self.flops, self.bytes = flops, nbytes
-        self.make, self.kernel = make, kernel
+        self.make, self.kernel, self.counter = make, kernel, counter
 
 
 def _rotate(dev, tensors, n):
@@ -116,7 +118,7 @@ def build_rows():
                 kk, vv = k.repeat_interleave(hq // k.size(1), 1), v.repeat_interleave(hq // k.size(1), 1)
             return lambda: F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask, is_causal=causal)
 
-        rows[name] = Row(name, label, bound, flops, nbytes, (make, cpu), "attn_fwd_kernel")
+        rows[name] = Row(name, label, bound, flops, nbytes, (make, cpu), "attn_fwd_kernel", "attention")
 
     def norm_row(name, label, x, w, b, eps, kind):
         rows_, width = x.numel() // x.size(-1), x.size(-1)
@@ -134,7 +136,7 @@ def build_rows():
                 return lambda: F.layer_norm(x, [width], w, b, eps)
             return lambda: F.rms_norm(x, [width], w, eps)
 
-        rows[name] = Row(name, label, "hbm", None, nbytes, (make, cpu), "norm_rows_wave")
+        rows[name] = Row(name, label, "hbm", None, nbytes, (make, cpu), "norm_rows_wave", "norms")
 
     c1 = C.config1()
     sdpa_row("c1_attn", "C1 causal GQA prefill 1x14/2x2048x64", "mfma", c1["q"], c1["k"], c1["v"], causal=True)
@@ -157,7 +159,8 @@ def build_rows():
     # Backward FLOPs: S, dP, dV, dK, dQ = 2.5x the forward's two products.
     rows["c1_attn_bwd"] = Row(
         "c1_attn_bwd", "extra: C1 attention backward (flash dQ/dK/dV from the forward's lse)", "mfma",
-        2.5 * C.attn_flops(64, 14, C.causal_pairs(1, 2048)), None, (bwd_make, bwd_cpu), "attn_bwd_dkdv")
+        2.5 * C.attn_flops(64, 14, C.causal_pairs(1, 2048)), None, (bwd_make, bwd_cpu), "attn_bwd_dkdv",
+        "attention_backward")
     norm_row("c1_rms", "C1 rms_norm [1,2048,896]", c1["x"], c1["w"], None, 1e-6, "rms")
 
     def rms_bwd_make(dev, n):
@@ -192,7 +195,7 @@ def build_rows():
     # Bytes: dy and x read, dx written (M W 2 each), weight read and dweight written, rstd read.
     rows["c1_rms_bwd"] = Row(
         "c1_rms_bwd", "extra: C1 rms_norm backward [1,2048,896] (dx, dweight)", "hbm", None,
-        3 * 2048 * 896 * 2 + 2 * 896 * 2 + 2048 * 4, (rms_bwd_make, rms_bwd_cpu), "rms_bwd_rows")
+        3 * 2048 * 896 * 2 + 2 * 896 * 2 + 2048 * 4, (rms_bwd_make, rms_bwd_cpu), "norm_bwd_rows", None)
 
     c2 = C.config2(1)
     norm_row("c2_ln", "C2 layer_norm [1,197,768]", c2["x"], c2["w"], c2["b"], 1e-6, "ln")
@@ -215,7 +218,7 @@ def build_rows():
     rows["c3_decode_lengths"] = Row(
         "c3_decode_lengths", "extra: C3 decode through key lengths (ktt::_sdpa_lengths, no mask)", "hbm",
         C.attn_flops(d3, 16, int(lens.sum())), dec_bytes - 8 * 4096 + 8 * 4,
-        (lengths_make, rows["c3_decode"].make[1]), "attn_decode_kernel")
+        (lengths_make, rows["c3_decode"].make[1]), "attn_decode_kernel", "attention")
     norm_row("c3_rms", "C3 rms_norm [8,1,2048]", c3["x"], c3["w"], None, 1e-6, "rms")
 
     c4 = C.config4()
@@ -258,13 +261,63 @@ def build_rows():
 
         extra = 4 * sum(n * n for n in L) if masked else 0
         rows[name] = Row(name, label, "mfma", C.attn_flops(128, 16, pairs), v4_bytes + extra, (make, cpu),
-                         "attn_fwd_kernel")
+                         "attn_fwd_kernel", "attention")
 
     varlen_row("c4_varlen", f"C4 varlen causal GQA 8 seqs T={t} 16/8x128", False)
     varlen_row("c4_varlen_masked", "C4 varlen causal + packed additive mask", True)
 
+    def varlen_bwd_make(dev, n):
+        cu_t = torch.tensor(cu, dtype=torch.int32)
+        sets = _rotate(dev, [c4["q"], c4["k"], c4["v"], cu_t, c4["q"]], n)
+        mx = max(L)
+        calls = []
+        for q, k, v, cu_d, go in sets:
+            out, lse = torch.ops.ktt._sdpa_varlen_offsets(q, k, v, cu_d, cu_d, mx, mx, True)
+            calls.append(lambda q=q, k=k, v=v, cu_d=cu_d, go=go, out=out, lse=lse:
+                         torch.ops.ktt._sdpa_varlen_offsets_backward(go, q, k, v, out, lse, cu_d, cu_d, mx, mx,
+                                                                     True))
+        return calls
+
+    def varlen_bwd_cpu():
+        q, k, v = (t.detach().clone().requires_grad_() for t in (c4["q"], c4["k"], c4["v"]))
+        outs = []
+        for a, b in zip(cu[:-1], cu[1:]):
+            qs = q[a:b].transpose(0, 1)[None]
+            ks = k[a:b].transpose(0, 1)[None].repeat_interleave(2, 1)
+            vs = v[a:b].transpose(0, 1)[None].repeat_interleave(2, 1)
+            outs.append(F.scaled_dot_product_attention(qs, ks, vs, is_causal=True))
+        return lambda: torch.autograd.grad(outs, (q, k, v), [o.detach().clone() for o in outs],
+                                           retain_graph=True)
+
+    rows["c4_varlen_bwd"] = Row(
+        "c4_varlen_bwd", "extra: C4 varlen causal backward (one launch set over the packed batch)", "mfma",
+        2.5 * C.attn_flops(128, 16, pairs), None, (varlen_bwd_make, varlen_bwd_cpu), "attn_bwd_dkdv",
+        "attention_backward")
+
     c5 = C.config5()
     norm_row("c5_ln", "C5 layer_norm [2,4096,640]", c5["x"], c5["w"], c5["b"], 1e-5, "ln")
+
+    def ln_bwd_make(dev, n):
+        sets = _rotate(dev, [c5["x"], c5["w"], c5["b"], c5["x"]], n)
+        calls = []
+        for x, w, b, gy in sets:
+            _, mean, rstd = torch.ops.aten.native_layer_norm(x, [640], w, b, 1e-5)
+            calls.append(lambda x=x, w=w, b=b, gy=gy, mean=mean, rstd=rstd:
+                         torch.ops.aten.native_layer_norm_backward(gy, x, [640], mean, rstd, w, b,
+                                                                   [True, True, True]))
+        return calls
+
+    def ln_bwd_cpu():
+        x, w, b = (t.detach().clone().requires_grad_() for t in (c5["x"], c5["w"], c5["b"]))
+        y = F.layer_norm(x, [640], w, b, 1e-5)
+        return lambda: torch.autograd.grad(y, (x, w, b), c5["x"], retain_graph=True)
+
+    # Bytes: dy and x read, dx written (M W 2 each), mean and rstd read, weight read,
+    # dweight and dbias written.
+    rows["c5_ln_bwd"] = Row(
+        "c5_ln_bwd", "extra: C5 layer_norm backward [2,4096,640] (dx, dweight, dbias)", "hbm", None,
+        3 * 8192 * 640 * 2 + 2 * 8192 * 4 + 3 * 640 * 2, (ln_bwd_make, ln_bwd_cpu), "norm_bwd_rows",
+        "norms_backward")
     sdpa_row("c5_self", "C5 SDXL self 2x10x4096x64", "mfma", c5["q"], c5["k"], c5["v"])
     sdpa_row("c5_cross", "C5 SDXL cross 2x10x4096q/77kv x64", "hbm", c5["q"], c5["ck"], c5["cv"])
 
@@ -370,6 +423,17 @@ def cpu_time(fn, seconds, min_calls=5):
     return statistics.median(times), len(times)
 
 
+def cpu_model_name():
+    """The host CPU's model name (from /proc/cpuinfo), or None."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def traffic_for(row_name):
     """HBM bytes per launch of the row's dominant kernel from the committed rocprofv3
     counter summary (profiles/traffic.json), or None."""
@@ -420,14 +484,21 @@ def main():
     results = {}
     for name in names:
         row = rows[name]
+        before = kohakutt_amd.counters()
         km, gm, em = measure(row, dev, args.steps, args.warmup, flush_buf)
+        after = kohakutt_amd.counters()
+        # Every timed call went to the kernels: the row's counter grew by at least the
+        # eager calls (the event-timed and the wall-timed loops), and none was declined.
+        if row.counter is not None:
+            grew = after[row.counter] - before[row.counter]
+            assert grew >= 2 * args.steps, (name, row.counter, grew)
+        assert after["attention_declined"] == before["attention_declined"], (name, after)
         results[name] = summarize(row, km, gm, em)
         log(json.dumps(results[name]))
-    counters = kohakutt_amd.counters()
-    assert counters["attention_declined"] == 0, counters
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    cpu_model = cpu_model_name()
     cpu_rows = {}
     if not args.no_cpu:
         for name in names:
@@ -487,7 +558,7 @@ def main():
     if "c1_attn" in cpu_rows:
         c = cpu_rows["c1_attn"]
         line["cpu_baseline"] = {
-            "value": c["tflops"], "unit": "TFLOP/s", "cores": cores, "kind": "reference",
+            "value": c["tflops"], "unit": "TFLOP/s", "cores": cores, "kind": "reference", "cpu_model": cpu_model,
             "sample": f"torch CPU bf16 F.scaled_dot_product_attention (the reference's CPU path) on the "
                       f"C1 shape, {c['calls']} calls over ~{args.cpu_seconds:.0f} s, median "
                       f"{c['ms_per_call']} ms/call, {cores} threads",

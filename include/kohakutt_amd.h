@@ -1,12 +1,16 @@
 /*
  * kohakutt_amd -- C ABI of the MI355X (gfx950) attention + norm hot path.
  *
- * Plain C: device pointers, int64 sizes and element strides, dtype codes and an opaque
- * stream (a hipStream_t passed as void*).  No torch or HIP types cross this boundary.
+ * This is the build's own thin layer under its torch ops (the ktt:: operators and the
+ * aten overrides that make it a drop-in): plain C, device pointers, int64 sizes and
+ * element strides, dtype codes and an opaque stream (a hipStream_t passed as void*).  No
+ * torch or HIP types cross it.  It does not stand in for the reference's C API
+ * (py_bridge/ktt_capi.h, a handle API of ktt_h tensors freed with ktt_release): each
+ * entry point below does the device work of one of the reference's bridge functions,
+ * named at the entry point, on caller-owned device memory.
  *
- * Conventions (the reference's C ABI, src/kohakutt_native/csrc/py_bridge/ktt_capi.h:1-3,
- * 96-124, and capi.cpp:19,58-79, returns NULL / -1 and keeps the message in a
- * thread_local string read by ktt_last_error(); this ABI keeps that error model):
+ * Conventions (the error model follows the reference's C API, ktt_capi.h:1-3 and
+ * capi.cpp:19,58-79: a failure code plus a thread_local message):
  *   - every entry point returns KMI_OK (0) or a negative kmi_status; the message of the
  *     last failure on the calling thread is kmi_last_error();
  *   - arguments are validated on the host before anything is enqueued: a rejected call
@@ -60,9 +64,9 @@ enum kmi_mask_mode {
  * Attention forward: out = softmax(scale * q k^T + mask) v per (batch, query head),
  * query head h reading K/V head h / (heads_q / heads_kv).
  *
- * Replaces the reference's bridge::sdpa / ktt_sdpa (ktt_capi.h:96-124,
- * device_attention.cpp:265-497) for the dense route and bridge::sdpa_varlen
- * (device_attention.cpp:681-761) for packed sequences.
+ * Does the device work of the reference's bridge::sdpa (device_attention.cpp:265-497)
+ * for the dense route and of bridge::sdpa_varlen (device_attention.cpp:681-761) for
+ * packed sequences.
  *
  * Dense: q [B, Hq, Sq, D], k/v [B, Hkv, Sk, D], out [B, Hq, Sq, D]; *_stride give the
  *   element strides of the batch, head and sequence dims (the head-dim stride is 1).
@@ -114,8 +118,8 @@ typedef struct kmi_attn_args {
     /* Dense calls only (ABI 2; NULL: every key).  Device int32 [batch]: sequence b's
      * queries see keys [0, L_b), L_b = key_lengths[b] clamped to [1, seq_k]; no mask is
      * built or read and key tiles past L_b are not loaded.  Query rows past L_b still see
-     * the first L_b keys.  Composes with causal (top-left).  Replaces the
-     * reference's bridge::sdpa_lengths behind ktt::_sdpa_lengths (aten_lengths.cpp:69-101,
+     * the first L_b keys.  Composes with causal (top-left).  Does the
+     * work of the reference's bridge::sdpa_lengths behind ktt::_sdpa_lengths (aten_lengths.cpp:69-101,
      * 175-197; docs/reference/kernels/flash.md, Key lengths). */
     const int32_t* key_lengths;
     /* ABI 3, varlen with KMI_MASK_PACKED (NULL: the kernels add up the block sizes): device
@@ -143,7 +147,7 @@ int kmi_attn_fwd(const kmi_attn_args* args, void* workspace, size_t workspace_by
  * forward's modes and strides and get no gradient.  Workspace:
  * kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row dot products; with GQA or split
  * query / key ranges also fp32 dK / dV and dQ partials, added in a fixed order).
- * Replaces the reference's flash backward behind tt_sdpa_overrideable_backward's stats
+ * Does the work of the reference's flash backward behind tt_sdpa_overrideable_backward's stats
  * route (aten_attention.cpp:716-812; bridge in device_attention.cpp:1208-1281;
  * docs/reference/kernels/flash.md:151-206) and its packed backward behind
  * ktt::_sdpa_varlen_backward (aten_varlen.cpp:237-319).  Supported: BF16 / F16, head
@@ -199,8 +203,8 @@ int kmi_attn_bwd(const kmi_attn_bwd_args* args, void* workspace, size_t workspac
  *   y = (x - mean) * rstd * weight + bias, rstd = 1 / sqrt(max(var, 0) + eps),
  * mean / rstd written as fp32 [rows] (either may be NULL).  weight / bias may be NULL;
  * x / y dtype BF16, F16 or F32; weight / bias BF16, F16 or F32.
- * Replaces the reference's ktt_layer_norm (ktt_capi.h:96-124; bridge::layer_norm,
- * device_norm.cpp:235-300; ktt_norm::forward, ktt_norm/program.cpp:436).
+ * Does the work of the reference's bridge::layer_norm (device_norm.cpp:235-300;
+ * ktt_norm::forward, ktt_norm/program.cpp:436).
  */
 int kmi_layer_norm_fwd(const void* x, const void* weight, const void* bias, void* y,
                        float* mean, float* rstd, int64_t rows, int64_t width,
@@ -210,9 +214,8 @@ int kmi_layer_norm_fwd(const void* x, const void* weight, const void* bias, void
 /*
  * RMSNorm forward: y = x * rstd * weight (+ bias), rstd = 1 / sqrt(mean(x^2) + eps),
  * rstd written as fp32 [rows] (may be NULL).
- * Replaces the reference's ktt_rms_norm / ktt_rms_norm_train (ktt_capi.h:96-124;
- * bridge::rms_norm, device_norm.cpp:203-233; ktt::rms_norm with bias,
- * aten_fused.cpp:60-85).
+ * Does the work of the reference's bridge::rms_norm (device_norm.cpp:203-233) and of
+ * ktt::rms_norm with bias (aten_fused.cpp:60-85).
  */
 int kmi_rms_norm_fwd(const void* x, const void* weight, const void* bias, void* y,
                      float* rstd, int64_t rows, int64_t width, int32_t x_dtype,
@@ -227,7 +230,7 @@ int kmi_rms_norm_fwd(const void* x, const void* weight, const void* bias, void* 
  * workspace (per-block column sums, added in a fixed order: deterministic).  Rows of
  * whole 16-byte vectors take one pass over dy and x (as kmi_layer_norm_bwd); others an
  * element path.
- * Replaces the reference's RMSNorm training backward (RmsNormFunction, aten_norm.cpp:
+ * Does the work of the reference's RMSNorm training backward (RmsNormFunction, aten_norm.cpp:
  * 548-599; ktt_norm backward and column-sum programs, layernorm.md:90-102).
  */
 int kmi_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t width, size_t* bytes);
@@ -247,7 +250,7 @@ int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weight, const fl
  * be whole 16-byte vectors, 16-byte aligned, at most 256 vectors (else KMI_EUNSUPPORTED).
  * dx in one pass over dy and x; dweight / dbias from per-block partial sums added in a
  * fixed order (deterministic), in kmi_layer_norm_bwd_workspace_bytes of fp32 workspace.
- * Replaces the reference's native_layer_norm_backward on its own programs
+ * Does the work of the reference's native_layer_norm_backward on its own programs
  * (aten_norm.cpp:130-224,811; ktt_norm bwd_* and colsum_* programs, layernorm.md:90-102).
  */
 int kmi_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t width, size_t* bytes);

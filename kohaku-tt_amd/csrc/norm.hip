@@ -559,7 +559,9 @@ __global__ __launch_bounds__(256) void norm_bwd_rows(const T* dy, const T* x, co
         }
     }
     // The wavefronts' column sums, added in wavefront order; wavefront 3 writes the block's
-    // partial rows [blockIdx.x][2][width].
+    // partial rows [blockIdx.x][2][width].  part is null when neither dw nor db is asked for
+    // (the same for the whole grid, so every wavefront leaves here together).
+    if (part == nullptr) return;
     float* pw = part + static_cast<int64_t>(blockIdx.x) * 2 * width;
     for (int w = 0; w < 4; ++w) {
         if (wave == w) {
@@ -644,6 +646,8 @@ hipError_t launch_norm_bwd(const void* dy, const void* x, const float* mean, con
     const int64_t nb = norm_bwd_blocks(rows), rpb = norm_bwd_rows_per_block(rows);
     const size_t lds = static_cast<size_t>(2) * width * sizeof(float);
     const bool hb = db != nullptr;
+    // Column sums only when dw or db is asked for: the caller's workspace may be absent.
+    if (!dw && !db) part = nullptr;
     auto* dyp = static_cast<const T*>(dy);
     auto* xp = static_cast<const T*>(x);
     auto* wp = static_cast<const W*>(w);

@@ -205,10 +205,11 @@ def test_layer_norm_backward_kernel(native, dev, shape, x_dtype, w_dtype, has_bi
     b = None if not has_bias else (0.1 * torch.randn(width, generator=g)).to(w_dtype)
 
     def run(device, dtype=None):
+        # Fresh leaves every run (x.to("cpu") would be x itself).
         cast = (lambda t: t.to(dtype)) if dtype is not None else (lambda t: t)
-        xx = cast(x).to(device).requires_grad_()
-        ww = None if w is None else cast(w).to(device).requires_grad_()
-        bb = None if b is None else cast(b).to(device).requires_grad_()
+        xx = cast(x).to(device).detach().clone().requires_grad_()
+        ww = None if w is None else cast(w).to(device).detach().clone().requires_grad_()
+        bb = None if b is None else cast(b).to(device).detach().clone().requires_grad_()
         F.layer_norm(xx, (width,), ww, bb, 1e-5).backward(cast(gy).to(device))
         return [t.grad for t in (xx, ww, bb) if t is not None]
 
