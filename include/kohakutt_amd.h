@@ -15,10 +15,11 @@
  *     last failure on the calling thread is kmi_last_error();
  *   - arguments are validated on the host before anything is enqueued: a rejected call
  *     launches nothing;
- *   - work is enqueued on `stream` and never synchronised; nothing is allocated, except
- *     that kmi_attn_fwd uses the caller's workspace (kmi_attn_workspace_bytes) for
- *     split-KV partials;
- *   - calls are thread-safe (no mutable global state besides the thread_local error).
+ *   - work is enqueued on `stream` and never synchronised; nothing is allocated: split-KV
+ *     partials and backward partial sums go to the caller's workspace (the *_bytes
+ *     queries), or, for kmi_attn_fwd_noalloc, to a device array of the library;
+ *   - calls are thread-safe (no mutable global state besides the thread_local error and
+ *     kmi_attn_fwd_noalloc's device array, which calls overlapping on one device share).
  */
 #ifndef KOHAKUTT_AMD_H
 #define KOHAKUTT_AMD_H
@@ -133,6 +134,17 @@ int kmi_attn_workspace_bytes(const kmi_attn_args* args, size_t* bytes);
 /* Enqueues the attention forward of `args` on `stream` (hipStream_t). */
 int kmi_attn_fwd(const kmi_attn_args* args, void* workspace, size_t workspace_bytes,
                  void* stream);
+
+/*
+ * kmi_attn_fwd without a workspace argument and without any allocation: for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, hosts that forbid
+ * hipMalloc).  No counterpart in the reference.  Split-KV partials go to a file-scope
+ * device array of the library (16 MiB per device, held for the life of the process); a
+ * call whose kmi_attn_workspace_bytes exceed it returns KMI_EUNSUPPORTED and launches
+ * nothing.  Calls that overlap on one device share that array and race; calls in one
+ * stream order do not.
+ */
+int kmi_attn_fwd_noalloc(const kmi_attn_args* args, void* stream);
 
 /*
  * Attention backward of a kmi_attn_fwd call (dense or varlen, causal or not, masked or

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 #include "attention_params.hpp"
 
@@ -178,28 +179,9 @@ int cu_count() {
     return n;
 }
 
-}  // namespace fwd
-}  // namespace kmi
-
-extern "C" int kmi_attn_workspace_bytes(const kmi_attn_args* args, size_t* bytes) {
-    using namespace kmi;
-    using namespace kmi::fwd;
-    if (!bytes) return fail(KMI_EINVAL, "kmi_attn_workspace_bytes: null bytes");
-    if (const char* why = check_args(args)) return fail(KMI_EINVAL, std::string("kmi_attn_workspace_bytes: ") + why);
-    *bytes = ws_bytes_for(args, make_plan(args));
-    return KMI_OK;
-}
-
-extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t workspace_bytes, void* stream) {
-    using namespace kmi;
-    using namespace kmi::fwd;
-    if (const char* why = check_args(a)) return fail(KMI_EINVAL, std::string("kmi_attn_fwd: ") + why);
-    if (a->seq_q == 0) return KMI_OK;
-    const Plan pl = make_plan(a);
-    const size_t need = ws_bytes_for(a, pl);
-    if (need > 0 && (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16))
-        return fail(KMI_EWORKSPACE, "kmi_attn_fwd: workspace missing, misaligned or smaller than "
-                                    "kmi_attn_workspace_bytes");
+// Enqueues a checked, planned call; `workspace` holds the plan's split partials (when it
+// splits).
+int enqueue(const kmi_attn_args* a, const Plan& pl, void* workspace, void* stream, const char* name) {
     AttnParams p{};
     p.q = a->q;
     p.k = a->k;
@@ -247,5 +229,73 @@ extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t work
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     const hipError_t err = a->dtype == KMI_BF16 ? launch_dim<bf16>(p, pl, s) : launch_dim<f16>(p, pl, s);
-    return hip_status(err, "kmi_attn_fwd");
+    return hip_status(err, name);
+}
+
+// Scratch of kmi_attn_fwd_noalloc: split-KV partials in a file-scope device array (each
+// device holds its own copy for the life of the process), so that entry point allocates
+// nothing.  Calls that overlap on one device share it and race; every partial a call's
+// merge reads is written by that call first, so nothing needs clearing between calls.
+constexpr size_t kScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The scratch's device address on the current device, looked up once per device (with
+// that device current); nullptr when the lookup fails.
+void* scratch_on_current_device() {
+    static std::mutex mu;
+    static void* addr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        addr[dev] = ptr;
+    }
+    return addr[dev];
+}
+
+}  // namespace fwd
+}  // namespace kmi
+
+extern "C" int kmi_attn_workspace_bytes(const kmi_attn_args* args, size_t* bytes) {
+    using namespace kmi;
+    using namespace kmi::fwd;
+    if (!bytes) return fail(KMI_EINVAL, "kmi_attn_workspace_bytes: null bytes");
+    if (const char* why = check_args(args)) return fail(KMI_EINVAL, std::string("kmi_attn_workspace_bytes: ") + why);
+    *bytes = ws_bytes_for(args, make_plan(args));
+    return KMI_OK;
+}
+
+extern "C" int kmi_attn_fwd(const kmi_attn_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+    using namespace kmi;
+    using namespace kmi::fwd;
+    if (const char* why = check_args(a)) return fail(KMI_EINVAL, std::string("kmi_attn_fwd: ") + why);
+    if (a->seq_q == 0) return KMI_OK;
+    const Plan pl = make_plan(a);
+    const size_t need = ws_bytes_for(a, pl);
+    if (need > 0 && (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16))
+        return fail(KMI_EWORKSPACE, "kmi_attn_fwd: workspace missing, misaligned or smaller than "
+                                    "kmi_attn_workspace_bytes");
+    return enqueue(a, pl, workspace, stream, "kmi_attn_fwd");
+}
+
+extern "C" int kmi_attn_fwd_noalloc(const kmi_attn_args* a, void* stream) {
+    using namespace kmi;
+    using namespace kmi::fwd;
+    if (const char* why = check_args(a)) return fail(KMI_EINVAL, std::string("kmi_attn_fwd_noalloc: ") + why);
+    if (a->seq_q == 0) return KMI_OK;
+    const Plan pl = make_plan(a);
+    const size_t need = ws_bytes_for(a, pl);
+    if (need > kScratchBytes)
+        return fail(KMI_EUNSUPPORTED, "kmi_attn_fwd_noalloc: the call needs " + std::to_string(need) +
+                                          " bytes of split-KV scratch, beyond the library's " +
+                                          std::to_string(kScratchBytes) +
+                                          "; call kmi_attn_fwd with a workspace of kmi_attn_workspace_bytes");
+    void* ws = nullptr;
+    if (need > 0) {
+        ws = scratch_on_current_device();
+        if (!ws) return fail(KMI_EHIP, "kmi_attn_fwd_noalloc: the scratch address of the current device is unknown");
+    }
+    return enqueue(a, pl, ws, stream, "kmi_attn_fwd_noalloc");
 }

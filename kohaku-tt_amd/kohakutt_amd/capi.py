@@ -20,6 +20,7 @@ KMI_MASK_NONE, KMI_MASK_STRIDED, KMI_MASK_PACKED = 0, 1, 2
 EXPORTS = (
     "kmi_attn_workspace_bytes",
     "kmi_attn_fwd",
+    "kmi_attn_fwd_noalloc",
     "kmi_attn_bwd_workspace_bytes",
     "kmi_attn_bwd",
     "kmi_layer_norm_fwd",
@@ -139,6 +140,7 @@ def lib():
         vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
         h.kmi_attn_workspace_bytes.argtypes = [ctypes.POINTER(AttnArgs), ctypes.POINTER(ctypes.c_size_t)]
         h.kmi_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), vp, ctypes.c_size_t, vp]
+        h.kmi_attn_fwd_noalloc.argtypes = [ctypes.POINTER(AttnArgs), vp]
         h.kmi_attn_bwd_workspace_bytes.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.POINTER(ctypes.c_size_t)]
         h.kmi_attn_bwd.argtypes = [ctypes.POINTER(AttnBwdArgs), vp, ctypes.c_size_t, vp]
         h.kmi_layer_norm_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, ctypes.c_double, vp]
@@ -171,6 +173,10 @@ def workspace_bytes(args: AttnArgs) -> int:
 
 def attn_fwd(args: AttnArgs, workspace: int, workspace_bytes_: int, stream: int) -> None:
     check(lib().kmi_attn_fwd(ctypes.byref(args), workspace, workspace_bytes_, stream))
+
+
+def attn_fwd_noalloc(args: AttnArgs, stream: int) -> None:
+    check(lib().kmi_attn_fwd_noalloc(ctypes.byref(args), stream))
 
 
 def layer_norm_fwd(x, w, b, y, mean, rstd, rows, width, x_dtype, w_dtype, b_dtype, eps, stream) -> None:
