@@ -118,7 +118,7 @@ __device__ __forceinline__ int64_t packed_block_offset(const AttnParams& p, int 
 
 // D: the padded head dim (a multiple of 32; the call's own head dim, a multiple of 8, is
 // AttnParams::d and the columns past it are zeros in registers and LDS).
-template <int D, int NQB, int TWIDTH = WN>
+template <int D, int NQB, int TWIDTH = WN, int NW = NWAVES>
 struct Shape {
     static constexpr int TW = TWIDTH;    // keys per wavefront tile
     static constexpr int BM = 16 * NQB;  // rows of a workgroup (shared by its wavefronts)
@@ -142,16 +142,16 @@ struct Shape {
     // (the buffer must not set the workgroup's LDS size, which bounds workgroups per CU).
     template <typename T>
     static constexpr int merge_blocks() {
-        const size_t tiles = static_cast<size_t>(NWAVES) * TILE * sizeof(T);
-        const size_t per = static_cast<size_t>(NWAVES) * 16 * CP * sizeof(float);
+        const size_t tiles = static_cast<size_t>(NW) * TILE * sizeof(T);
+        const size_t per = static_cast<size_t>(NW) * 16 * CP * sizeof(float);
         const int mb = static_cast<int>(tiles / per);
         return mb < 1 ? 1 : (mb > NQB ? NQB : mb);
     }
     template <typename T>
     static constexpr size_t lds_bytes() {
-        const size_t tiles = static_cast<size_t>(NWAVES) * TILE * sizeof(T);
-        const size_t comb = static_cast<size_t>(NWAVES) * 16 * merge_blocks<T>() * CP * sizeof(float);
-        return (tiles > comb ? tiles : comb) + static_cast<size_t>(NWAVES) * BM * 4 * sizeof(float);
+        const size_t tiles = static_cast<size_t>(NW) * TILE * sizeof(T);
+        const size_t comb = static_cast<size_t>(NW) * 16 * merge_blocks<T>() * CP * sizeof(float);
+        return (tiles > comb ? tiles : comb) + static_cast<size_t>(NW) * BM * 4 * sizeof(float);
     }
 };
 
@@ -208,11 +208,12 @@ __device__ __forceinline__ MRaw mask_load(const MRaw* mp, int64_t mrow, int key,
 
 // RS (row split, short key ranges): each wavefront owns its own 16 NQB rows and runs every
 // key tile itself -- no key split, no merge, no barrier; the workgroup holds 4 row blocks.
-template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
+template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH, int NW>
 __device__ __forceinline__ void attn_block(const AttnParams& p, const int split, const int bh, const int xt) {
     static_assert(!RS || MK == MK_NONE, "row split is for unmasked calls (no block barriers)");
+    static_assert(!RS || NW == NWAVES, "row split plans four wavefronts");
     typedef typename Mfma<T>::v8 v8;
-    typedef Shape<D, NQB, TWIDTH> S;
+    typedef Shape<D, NQB, TWIDTH, NW> S;
     constexpr int TW = S::TW;   // keys per tile
     constexpr int KH = TW / 32;  // 32-key chunks per tile (one PV MFMA each)
     constexpr int BM = S::BM, VP = S::VP, KP = S::KP, CP = S::CP;
@@ -257,7 +258,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     }
     if (p.klen) lk = min(max(p.klen[seq], 1), p.seq_k);
     const int vrows = lq * G;
-    const int r_begin = RS ? (xt * NWAVES + wave) * BM : xt * BM;
+    const int r_begin = RS ? (xt * NW + wave) * BM : xt * BM;
     if (lk <= 0) return;
     if constexpr (RS) {
         if (p.rs_shared) {
@@ -273,11 +274,11 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             const T* vg = static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] + static_cast<int64_t>(k0) * p.vs[2];
             constexpr int VPR_ = D / 8;
             const int nvec = nt * S::TW * VPR_;
-            constexpr int MAXV = (kRsTiles * 32 * VPR_ + NTHREADS - 1) / NTHREADS;  // up to kRsTiles tiles (host bound)
+            constexpr int MAXV = (kRsTiles * 32 * VPR_ + (NW * kWave) - 1) / (NW * kWave);  // up to kRsTiles tiles (host bound)
             u32x4 kv[MAXV], vv[MAXV];
 #pragma unroll
             for (int j = 0; j < MAXV; ++j) {
-                const int v = min(tid + NTHREADS * j, nvec - 1);
+                const int v = min(tid + (NW * kWave) * j, nvec - 1);
                 const int row = min(v / VPR_, lk - 1), ch = v % VPR_;
                 // Columns past the head dim read in range and are zeroed.
                 const int col = min(8 * ch, p.d - 8);
@@ -288,7 +289,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             }
 #pragma unroll
             for (int j = 0; j < MAXV; ++j) {
-                const int v = min(tid + NTHREADS * j, nvec - 1);
+                const int v = min(tid + (NW * kWave) * j, nvec - 1);
                 const int row = v / VPR_, ch = v % VPR_;
                 *reinterpret_cast<u32x4*>(kls + row * S::KP + 8 * ch) = kv[j];
                 *reinterpret_cast<u32x4*>(vls + row * S::VP + 8 * ch) = vv[j];
@@ -297,7 +298,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         }
     }
     if (r_begin >= vrows) return;
-    constexpr int TS = RS ? 1 : NWAVES;  // tile stride of one wavefront
+    constexpr int TS = RS ? 1 : NW;  // tile stride of one wavefront
     const int r_end = min(vrows, r_begin + BM);
     const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys <= i + coff
     int kend = lk;
@@ -369,6 +370,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     const bool stage_lane = dg < NCH;
     const bool stage_live = 8 * dg < p.d;
     const int dgc = min(dg, (p.d - 1) / 8);
+    // Padded head dims: K's columns past d must be zeros (they meet Q's zero columns in
+    // S, and a finite value of another row there could still be inf); V's need not be
+    // (they only reach output columns past d, which are never written).  Uniform.
+    const bool kpad = p.d < D;
     const int64_t kstride = p.ks[2] * static_cast<int64_t>(sizeof(T)), vstride = p.vs[2] * static_cast<int64_t>(sizeof(T));
     const char* kunit = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + kb_off + kvh * p.ks[1] +
                                                       static_cast<int64_t>(k0) * p.ks[2]);
@@ -404,15 +409,22 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
                 for (int c = 0; c < DC; ++c) {
-                    const u32x4 x = buffer_load16(rs, k_lane + 16 * kb * step + 64 * c);
-                    kr[kb][c] = __builtin_bit_cast(v8, 32 * c + 8 * g4 < p.d ? x : u32x4{0u, 0u, 0u, 0u});
+                    kr[kb][c] = __builtin_bit_cast(v8, buffer_load16(rs, k_lane + 16 * kb * step + 64 * c));
                 }
+            }
+            if (kpad) {
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int c = 0; c < DC; ++c)
+                        if (32 * c + 8 * g4 >= p.d) kr[kb][c] = v8{};
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < KIT; ++i) {
-                const u32x4 x = buffer_load16(rs, k_lane + i * RPP * step);
-                kst[i] = stage_live ? x : u32x4{0u, 0u, 0u, 0u};
+            for (int i = 0; i < KIT; ++i) kst[i] = buffer_load16(rs, k_lane + i * RPP * step);
+            if (kpad && !stage_live) {
+#pragma unroll
+                for (int i = 0; i < KIT; ++i) kst[i] = u32x4{0u, 0u, 0u, 0u};
             }
         }
     };
@@ -423,10 +435,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         uint32_t step = static_cast<uint32_t>(vstride);
         __asm__ volatile("" : "+s"(step));
 #pragma unroll
-        for (int i = 0; i < KIT; ++i) {
-            const u32x4 x = buffer_load16(rs, v_lane + i * RPP * step);
-            vreg[i] = stage_live ? x : u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int i = 0; i < KIT; ++i) vreg[i] = buffer_load16(rs, v_lane + i * RPP * step);
         if constexpr (MASKED) {
             const MRaw* mp = static_cast<const MRaw*>(mptr);
             if (mvec && key0 + TW <= lk) {
@@ -516,7 +525,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // tiles whose every key is masked contribute exactly nothing once the row is known to
     // keep a key somewhere, so they are neither loaded nor computed.  A scan of the whole
     // mask row establishes that first (a row with no kept key needs every raw score).
-    constexpr int FLAG_CAP = NWAVES * BM * 4 * static_cast<int>(sizeof(float));
+    constexpr int FLAG_CAP = NW * BM * 4 * static_cast<int>(sizeof(float));
     uint8_t* tflag = smem + S::template lds_bytes<T>() - FLAG_CAP;
     bool skip = false;
     if constexpr (MASKED) {
@@ -529,21 +538,21 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                               m_key == 1 && ntl > 0 && ntl <= FLAG_CAP && lk % EPV == 0 &&
                               (reinterpret_cast<uintptr_t>(mrow0) & 15) == 0;
         if (eligible) {
-            for (int i = tid; i < ntl; i += NTHREADS) tflag[i] = 0;
+            for (int i = tid; i < ntl; i += (NW * kWave)) tflag[i] = 0;
             __syncthreads();
             bool keeps = false;
             const int nv = lk / EPV;
-            for (int v0 = tid; v0 < nv; v0 += 2 * NTHREADS) {
+            for (int v0 = tid; v0 < nv; v0 += 2 * (NW * kWave)) {
                 u32x4 raw2[2];
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    const int v = v0 + u * NTHREADS;
+                    const int v = v0 + u * (NW * kWave);
                     raw2[u] = v < nv ? *reinterpret_cast<const u32x4*>(mrow0 + static_cast<int64_t>(v) * EPV)
                                      : u32x4{0u, 0u, 0u, 0u};
                 }
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    const int v = v0 + u * NTHREADS;
+                    const int v = v0 + u * (NW * kWave);
                     if (v >= nv) continue;
                     const MRaw* e = reinterpret_cast<const MRaw*>(&raw2[u]);
 #pragma unroll
@@ -837,26 +846,26 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // accumulators.  Wavefronts in masked mode (they met a kept key) win; a row none of
     // them kept a key for merges every wavefront's raw-score state.  The sums run in a
     // fixed wavefront order.
-    f32x4* stats = reinterpret_cast<f32x4*>(smem + S::template lds_bytes<T>() - NWAVES * BM * sizeof(f32x4));
+    f32x4* stats = reinterpret_cast<f32x4*>(smem + S::template lds_bytes<T>() - NW * BM * sizeof(f32x4));
     float l_run[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; ++b) {
         l_run[b] = lacc[b][0];
     }
-    auto combine = [&](const f32x4 (&sw)[NWAVES], float (&wt)[NWAVES], float& m, float& lt, bool& any_masked) {
+    auto combine = [&](const f32x4 (&sw)[NW], float (&wt)[NW], float& m, float& lt, bool& any_masked) {
         any_masked = false;
 #pragma unroll
-        for (int w = 0; w < NWAVES; ++w) any_masked = any_masked || (sw[w][2] == 0.f && sw[w][1] > 0.f);
+        for (int w = 0; w < NW; ++w) any_masked = any_masked || (sw[w][2] == 0.f && sw[w][1] > 0.f);
         m = -INFINITY;
-        bool sel[NWAVES];
+        bool sel[NW];
 #pragma unroll
-        for (int w = 0; w < NWAVES; ++w) {
+        for (int w = 0; w < NW; ++w) {
             sel[w] = (!any_masked || sw[w][2] == 0.f) && sw[w][1] > 0.f;
             m = fmaxf(m, sel[w] ? sw[w][0] : -INFINITY);
         }
         lt = 0.f;
 #pragma unroll
-        for (int w = 0; w < NWAVES; ++w) {
+        for (int w = 0; w < NW; ++w) {
             wt[w] = sel[w] ? __builtin_amdgcn_exp2f(sw[w][0] - m) : 0.f;
             lt += wt[w] * sw[w][1];
         }
@@ -911,24 +920,24 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         __syncthreads();
         // thread -> (row, 4 consecutive head-dim columns): weights of the wavefronts, their
         // O sum, the normalised row.
-        for (int idx = tid; idx < BM * VPRO; idx += NTHREADS) {
+        for (int idx = tid; idx < BM * VPRO; idx += (NW * kWave)) {
             const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
             const int r = r_begin + row;
             if (r >= r_end) continue;
-            f32x4 sw[NWAVES];
-            f32x4 ov[NWAVES];
+            f32x4 sw[NW];
+            f32x4 ov[NW];
 #pragma unroll
-            for (int w = 0; w < NWAVES; ++w) {
+            for (int w = 0; w < NW; ++w) {
                 sw[w] = stats[w * BM + row];
                 ov[w] = *reinterpret_cast<const f32x4*>(
                     reinterpret_cast<const float*>(smem + static_cast<size_t>(w) * S::TILE * sizeof(T)) + row * CP + col);
             }
-            float wt[NWAVES], m, lt;
+            float wt[NW], m, lt;
             bool any_masked;
             combine(sw, wt, m, lt, any_masked);
             f32x4 acc = ov[0] * wt[0];
 #pragma unroll
-            for (int w = 1; w < NWAVES; ++w) acc += ov[w] * wt[w];
+            for (int w = 1; w < NW; ++w) acc += ov[w] * wt[w];
             acc *= lt > 0.f ? 1.f / lt : 0.f;
             write_row(r, col, acc);
             if (col == 0) write_lse(r, lt > 0.f ? m + log2f(lt) : -INFINITY, !any_masked && MASKED);
@@ -946,10 +955,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         float fscale[NQB];
 #pragma unroll
         for (int b = 0; b < NQB; ++b) {
-            f32x4 sw[NWAVES];
+            f32x4 sw[NW];
 #pragma unroll
-            for (int w = 0; w < NWAVES; ++w) sw[w] = stats[w * BM + 16 * b + l16];
-            float wt[NWAVES], m, lt;
+            for (int w = 0; w < NW; ++w) sw[w] = stats[w * BM + 16 * b + l16];
+            float wt[NW], m, lt;
             bool any_masked;
             combine(sw, wt, m, lt, any_masked);
             fscale[b] = lt > 0.f ? wt[wave] / lt : 0.f;
@@ -971,13 +980,13 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                         o[d][b] * fscale[b];
             }
             __syncthreads();
-            for (int idx = tid; idx < MROWS * VPRO; idx += NTHREADS) {
+            for (int idx = tid; idx < MROWS * VPRO; idx += (NW * kWave)) {
                 const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
                 const int r = r_begin + 16 * b0 + row;
                 if (16 * b0 + row >= BM || r >= r_end) continue;
                 f32x4 acc = *reinterpret_cast<const f32x4*>(comb + row * CP + col);
 #pragma unroll
-                for (int w = 1; w < NWAVES; ++w) acc += *reinterpret_cast<const f32x4*>(comb + (w * MROWS + row) * CP + col);
+                for (int w = 1; w < NW; ++w) acc += *reinterpret_cast<const f32x4*>(comb + (w * MROWS + row) * CP + col);
                 write_row(r, col, acc);
             }
         }
@@ -996,8 +1005,8 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 // 2 npair shortest causal query tiles of each unit run two to a workgroup (shortest with
 // longest of that set, so no pair outlasts the heaviest tile), which keeps the grid within
 // one round of resident workgroups.
-template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
-__global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) {
+template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH, int NW>
+__global__ __launch_bounds__(NW * kWave) void attn_fwd_kernel(const AttnParams p) {
     int lin = blockIdx.x;
     const int split = lin % p.splits;
     lin /= p.splits;
@@ -1010,18 +1019,18 @@ __global__ __launch_bounds__(NTHREADS) void attn_fwd_kernel(const AttnParams p) 
     // idles.  Equal-length batches keep each XCD on few units (their K/V stay in its L2).
     const int bh = (lin - xi * units + (p.cu_q ? xi * 9 : 0)) % units;
     if (!p.causal) {
-        attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, xi);
+        attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, split, bh, xi);
         return;
     }
     const int singles = p.nx - 2 * p.npair;
     if (xi < singles) {
-        attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, p.nx - 1 - xi);
+        attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, split, bh, p.nx - 1 - xi);
         return;
     }
     const int j = xi - singles;
-    attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, 2 * p.npair - 1 - j);
+    attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, split, bh, 2 * p.npair - 1 - j);
     __syncthreads();  // the second tile reuses the LDS
-    attn_block<T, D, NQB, MK, RS, TWIDTH>(p, split, bh, j);
+    attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, split, bh, j);
 }
 
 // Decode: at most 16 "virtual rows" (Sq x G) per (sequence, K/V head).  The key tiles of a
@@ -1174,8 +1183,10 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
                                                       static_cast<int64_t>(k0) * p.vs[2]);
     const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
     const bool stage_lane = dg < NCH;  // staging lanes past the padded row idle
-    const bool stage_live = 8 * dg < p.d;
     const int dgc = min(dg, (p.d - 1) / 8);
+    // Padded head dims: K's columns past d are zeroed (as in the prefill kernel); V's
+    // reach only output columns past d, which are never written.  Uniform.
+    const bool kpad = p.d < D;
     const uint32_t k_lane = static_cast<uint32_t>(l16 * kstride + 16 * g4);
     const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dgc);
     const uint32_t kspan = static_cast<uint32_t>(kstride > 0 ? kstride : p.d * static_cast<int64_t>(sizeof(T)));
@@ -1195,15 +1206,17 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                const u32x4 x = buffer_load16(rk, k_lane + 16 * kb * kst + 64 * c);
-                kreg[kb][c] = __builtin_bit_cast(v8, 32 * c + 8 * g4 < p.d ? x : u32x4{0u, 0u, 0u, 0u});
-            }
+            for (int c = 0; c < DC; ++c)
+                kreg[kb][c] = __builtin_bit_cast(v8, buffer_load16(rk, k_lane + 16 * kb * kst + 64 * c));
+        if (kpad) {
 #pragma unroll
-        for (int i2 = 0; i2 < KIT; ++i2) {
-            const u32x4 x = buffer_load16(rv, v_lane + i2 * RPP * vst);
-            vreg[i2] = stage_live ? x : u32x4{0u, 0u, 0u, 0u};
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int c = 0; c < DC; ++c)
+                    if (32 * c + 8 * g4 >= p.d) kreg[kb][c] = v8{};
         }
+#pragma unroll
+        for (int i2 = 0; i2 < KIT; ++i2) vreg[i2] = buffer_load16(rv, v_lane + i2 * RPP * vst);
         if constexpr (MASKED) {
             const MRaw* mp = static_cast<const MRaw*>(p.mask);
             if (mvec && key0 + WN <= lk) {
@@ -1553,24 +1566,24 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
             wsum > 0.f ? (m + log2f(wsum)) * kLn2 + (any_masked ? 0.f : kMaskedLogit) : -INFINITY;
 }
 
-template <typename T, int D, int NQB, int MK, bool RS = false, int TWIDTH = WN>
+template <typename T, int D, int NQB, int MK, bool RS = false, int TWIDTH = WN, int NW = NWAVES>
 hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     static int per_cu = 0;  // resident workgroups per CU
-    typedef Shape<D, NQB, TWIDTH> S;
+    typedef Shape<D, NQB, TWIDTH, NW> S;
     // Shared row split: every key tile of a unit (at most four) in LDS, K then V.
     constexpr size_t rs_max = RS ? kRsTiles * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T) : 0;
     const size_t lds_tiles = S::template lds_bytes<T>();
     const size_t lds = RS && p_in.rs_shared
                            ? ceil_div(p_in.seq_k, TWIDTH) * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T)
                            : lds_tiles;
-    const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH>);
+    const void* fn = reinterpret_cast<const void*>(&attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH, NW>);
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(std::max(lds_tiles, rs_max)));
         if (attr_err == hipSuccess &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NTHREADS, lds_tiles) != hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, (NW * kWave), lds_tiles) != hipSuccess)
             per_cu = 0;
     });
     if (attr_err != hipSuccess) return attr_err;
@@ -1585,7 +1598,7 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
         p.npair = static_cast<int>(std::min<int64_t>(ceil_div(extra, units), p.nx / 2));
         grid -= static_cast<int64_t>(p.npair) * units;
     }
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH>), dim3(static_cast<unsigned>(grid)), dim3(NTHREADS), lds,
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH, NW>), dim3(static_cast<unsigned>(grid)), dim3((NW * kWave)), lds,
                        stream, p);
     return hipGetLastError();
 }
