@@ -387,6 +387,82 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
     T* vl = kl + (KD ? 0 : TW * KP);
 
+    // DMA2 (32-row tiles at D = 64, unmasked): K and V tiles go from global memory
+    // straight into the wavefront's LDS tile (buffer loads with the lds modifier: no
+    // staging registers, no LDS store instructions).  A step reads all of its tile's K and
+    // V fragments first, then requests the next tile into the same buffer, so the wait
+    // before the next step's reads is for loads issued a whole step earlier.  Rows sit at
+    // pitch D with 16-byte chunks XOR-swizzled (K: chunk c of row r at c ^ kswz(r); V at
+    // c ^ vswz(r)) so that K's row reads and V's transposed reads hit distinct banks.  DMA
+    // instruction i fills rows 8 i .. 8 i + 7; lane q the slot of row 8 i + q / 8,
+    // physical chunk q % 8.
+    constexpr bool DMA2 = !KD && !RS && MK == MK_NONE && D == 64 && NQB == 2 && TW == 32 && sizeof(T) == 2;
+    auto kswz = [](int r) { return (r ^ (r >> 3)) & 7; };
+    auto vswz = [](int r) { return 2 * ((r ^ (r >> 2)) & 3); };
+    T* const kd2 = kl;
+    T* const vd2 = kl + TW * D;
+    uint32_t dk_off[DMA2 ? TW / 8 : 1], dv_off[DMA2 ? TW / 8 : 1];
+    int kfo[DMA2 ? KB : 1][DMA2 ? DC : 1];  // K fragment element offsets in the tile
+    int vtro[DMA2 ? DB : 1];                 // V transposed-read element offsets (first 16 keys)
+    if constexpr (DMA2) {
+        const int cmax = (p.d - 1) / 8;  // padded head dims: chunks past d repeat the last
+#pragma unroll
+        for (int i = 0; i < TW / 8; ++i) {
+            const int r = 8 * i + (lane >> 3);
+            dk_off[i] = static_cast<uint32_t>(r) * static_cast<uint32_t>(kstride) +
+                        16u * static_cast<uint32_t>(min((lane & 7) ^ kswz(r), cmax));
+            dv_off[i] = static_cast<uint32_t>(r) * static_cast<uint32_t>(vstride) +
+                        16u * static_cast<uint32_t>(min((lane & 7) ^ vswz(r), cmax));
+        }
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                const int r = 16 * kb + l16;
+                kfo[kb][c] = r * D + 8 * ((4 * c + g4) ^ kswz(r));
+            }
+        const int r = 4 * g4 + (l16 >> 2);
+#pragma unroll
+        for (int d = 0; d < DB; ++d) vtro[d] = r * D + 8 * (((2 * d) ^ vswz(r)) | ((l16 >> 1) & 1)) + 4 * (l16 & 1);
+    }
+    auto dma_tile = [&](int tt) {
+        if constexpr (DMA2) {
+            const int key0 = tt * TW;
+            const int rows_here = min(lk - key0, TW);
+            const auto rk = buffer_rsrc(kunit + key0 * kstride, static_cast<uint32_t>(rows_here) * kspan);
+            const auto rv = buffer_rsrc(vunit + key0 * vstride, static_cast<uint32_t>(rows_here) * vspan);
+            if (rows_here == TW) {
+#pragma unroll
+                for (int i = 0; i < TW / 8; ++i) {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rk, (__attribute__((address_space(3))) void*)(kd2 + i * 512), 16, dk_off[i], 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rv, (__attribute__((address_space(3))) void*)(vd2 + i * 512), 16, dv_off[i], 0, 0, 0);
+                }
+            } else {
+                // Last tile: rows past the unit's last key repeat it (finite; their scores
+                // are masked), so every lane reads in range and every slot is written.
+                const int cmax = (p.d - 1) / 8;
+#pragma unroll
+                for (int i = 0; i < TW / 8; ++i) {
+                    const int r = 8 * i + (lane >> 3);
+                    const uint32_t rr = static_cast<uint32_t>(min(r, rows_here - 1));
+                    const uint32_t ok = rr * static_cast<uint32_t>(kstride) +
+                                        16u * static_cast<uint32_t>(min((lane & 7) ^ kswz(r), cmax));
+                    const uint32_t ov = rr * static_cast<uint32_t>(vstride) +
+                                        16u * static_cast<uint32_t>(min((lane & 7) ^ vswz(r), cmax));
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rk, (__attribute__((address_space(3))) void*)(kd2 + i * 512), 16, ok, 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rv, (__attribute__((address_space(3))) void*)(vd2 + i * 512), 16, ov, 0, 0, 0);
+                }
+            }
+        } else {
+            (void)tt;
+        }
+    };
+    v8 vpre[DMA2 ? DB : 1];  // DMA2: this tile's V fragments, read at the top of its step
+
     // Mask values of the staged tile, loaded with its K / V (raw element type; converted
     // when the tile is computed, so the loads stay in flight meanwhile).
     typedef typename std::conditional<MK == MK_BOOL, uint8_t,
@@ -510,7 +586,11 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // loads share one round trip with the Q fragments and the mask-row scan below).
     const int t_spec = t_begin + (RS ? 0 : wave);
     const bool rs_shared = RS && p.rs_shared;
-    if (S::PREFETCH && t_spec < t_end && !rs_shared) load_tile(t_spec);
+    if constexpr (DMA2) {
+        if (t_spec < t_end) dma_tile(t_spec);
+    } else if (S::PREFETCH && t_spec < t_end && !rs_shared) {
+        load_tile(t_spec);
+    }
     float c2 = p.scale_log2;
     if (c2 < 0.f) {
         c2 = -c2;
@@ -674,6 +754,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         // The V fragments are requested first; the MFMAs of row block b then interleave
         // with the exponentials of row block b + 1 (scheduling groups below).
         v8 vf[KH][DB];
+        if constexpr (DMA2) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d) vf[0][d] = vpre[d];
+        } else
 #pragma unroll
         for (int h = 0; h < KH; ++h) {
             const T* vsrc = vl + (32 * h + 4 * g4 + (l16 >> 2)) * VP + 4 * (l16 & 3);
@@ -716,8 +800,49 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     };
 
     int t = next_tile(t_spec);
-    if (S::PREFETCH && t != t_spec && t < t_end && !rs_shared) load_tile(t);
-    if (rs_shared) {
+    if (!DMA2 && S::PREFETCH && t != t_spec && t < t_end && !rs_shared) load_tile(t);
+    if constexpr (DMA2) {
+        while (t < t_end) {
+            // This tile's K and V fragments, once its DMA has landed: an explicit wait, as the
+            // compiler's own wait covers the transposed reads but not the plain ones.
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            v8 kf[KB][DC];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int c = 0; c < DC; ++c) kf[kb][c] = *reinterpret_cast<const v8*>(kd2 + kfo[kb][c]);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                const u32x2 lo = lds_read_tr(vd2 + vtro[d]);           // keys 4 g + s
+                const u32x2 hi = lds_read_tr(vd2 + 16 * D + vtro[d]);  // keys 16 + 4 g + s (same swizzle)
+                vpre[d] = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            }
+            if (kpad) {
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int c = 0; c < DC; ++c)
+                        if (32 * c + 8 * g4 >= p.d) kf[kb][c] = v8{};
+            }
+            // The reads are done before the next tile's DMA lands in the same buffer.
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            const int t_next = next_tile(t + TS);
+            if (t_next < t_end) dma_tile(t_next);
+            f32x4 s[KB][NQB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+                for (int b = 0; b < NQB; ++b) {
+                    s[kb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
+                }
+            }
+            const MCur mnone{};
+            consume(t, s, mnone);
+            t = t_next;
+        }
+    } else if (rs_shared) {
         // Every key tile is in LDS: S, softmax and PV per tile, nothing else.
         T* const kls = reinterpret_cast<T*>(smem);
         T* const vls = kls + ((lk + TW - 1) / TW) * TW * KP;
