@@ -397,30 +397,29 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // instruction i fills rows 8 i .. 8 i + 7; lane q the slot of row 8 i + q / 8,
     // physical chunk q % 8.
     constexpr bool DMA2 = !KD && !RS && MK == MK_NONE && D == 64 && NQB == 2 && TW == 32 && sizeof(T) == 2;
-    auto kswz = [](int r) { return (r ^ (r >> 3)) & 7; };
+    // Swizzles chosen so that rows r and r + 16 share one (the fragment reads of the second
+    // 16-key block are an immediate offset away) and, within a DMA instruction's eight rows
+    // 8 i + a, depend on a and the parity of i only (the row term 8 i * stride goes to the
+    // scalar offset; two lane offsets per operand).
+    auto kswz = [](int r) { return (r & 7) ^ ((r >> 3) & 1); };
     auto vswz = [](int r) { return 2 * ((r ^ (r >> 2)) & 3); };
     T* const kd2 = kl;
     T* const vd2 = kl + TW * D;
-    uint32_t dk_off[DMA2 ? TW / 8 : 1], dv_off[DMA2 ? TW / 8 : 1];
-    int kfo[DMA2 ? KB : 1][DMA2 ? DC : 1];  // K fragment element offsets in the tile
-    int vtro[DMA2 ? DB : 1];                 // V transposed-read element offsets (first 16 keys)
+    uint32_t dk_b[DMA2 ? 2 : 1], dv_b[DMA2 ? 2 : 1];  // DMA lane offsets for even / odd i
+    int kfo[DMA2 ? DC : 1];                          // K fragment element offsets (keys 0..15)
+    int vtro[DMA2 ? DB : 1];                         // V transposed-read element offsets (first 16 keys)
     if constexpr (DMA2) {
         const int cmax = (p.d - 1) / 8;  // padded head dims: chunks past d repeat the last
+        const int a = lane >> 3, q7 = lane & 7;
 #pragma unroll
-        for (int i = 0; i < TW / 8; ++i) {
-            const int r = 8 * i + (lane >> 3);
-            dk_off[i] = static_cast<uint32_t>(r) * static_cast<uint32_t>(kstride) +
-                        16u * static_cast<uint32_t>(min((lane & 7) ^ kswz(r), cmax));
-            dv_off[i] = static_cast<uint32_t>(r) * static_cast<uint32_t>(vstride) +
-                        16u * static_cast<uint32_t>(min((lane & 7) ^ vswz(r), cmax));
+        for (int par = 0; par < 2; ++par) {
+            dk_b[par] = static_cast<uint32_t>(a) * static_cast<uint32_t>(kstride) +
+                        16u * static_cast<uint32_t>(min(q7 ^ kswz(8 * par + a), cmax));
+            dv_b[par] = static_cast<uint32_t>(a) * static_cast<uint32_t>(vstride) +
+                        16u * static_cast<uint32_t>(min(q7 ^ vswz(8 * par + a), cmax));
         }
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                const int r = 16 * kb + l16;
-                kfo[kb][c] = r * D + 8 * ((4 * c + g4) ^ kswz(r));
-            }
+        for (int c = 0; c < DC; ++c) kfo[c] = l16 * D + 8 * ((4 * c + g4) ^ kswz(l16));
         const int r = 4 * g4 + (l16 >> 2);
 #pragma unroll
         for (int d = 0; d < DB; ++d) vtro[d] = r * D + 8 * (((2 * d) ^ vswz(r)) | ((l16 >> 1) & 1)) + 4 * (l16 & 1);
@@ -434,10 +433,12 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             if (rows_here == TW) {
 #pragma unroll
                 for (int i = 0; i < TW / 8; ++i) {
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rk, (__attribute__((address_space(3))) void*)(kd2 + i * 512), 16, dk_off[i], 0, 0, 0);
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rv, (__attribute__((address_space(3))) void*)(vd2 + i * 512), 16, dv_off[i], 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(kd2 + i * 512),
+                                                             16, dk_b[i & 1],
+                                                             static_cast<int>(8 * i * static_cast<uint32_t>(kstride)), 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vd2 + i * 512),
+                                                             16, dv_b[i & 1],
+                                                             static_cast<int>(8 * i * static_cast<uint32_t>(vstride)), 0, 0);
                 }
             } else {
                 // Last tile: rows past the unit's last key repeat it (finite; their scores
@@ -810,7 +811,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-                for (int c = 0; c < DC; ++c) kf[kb][c] = *reinterpret_cast<const v8*>(kd2 + kfo[kb][c]);
+                for (int c = 0; c < DC; ++c) kf[kb][c] = *reinterpret_cast<const v8*>(kd2 + 16 * kb * D + kfo[c]);
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
                 const u32x2 lo = lds_read_tr(vd2 + vtro[d]);           // keys 4 g + s
@@ -1130,8 +1131,11 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 // 2 npair shortest causal query tiles of each unit run two to a workgroup (shortest with
 // longest of that set, so no pair outlasts the heaviest tile), which keeps the grid within
 // one round of resident workgroups.
+// The 32-row D = 64 unmasked variant (K and V by DMA, no staging registers) is held to
+// four wavefronts per SIMD.
 template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH, int NW>
-__global__ __launch_bounds__(NW * kWave) void attn_fwd_kernel(const AttnParams p) {
+__global__ __launch_bounds__(NW * kWave, (D == 64 && NQB == 2 && MK == MK_NONE && !RS && TWIDTH == 32) ? 4 : 1)
+void attn_fwd_kernel(const AttnParams p) {
     int lin = blockIdx.x;
     const int split = lin % p.splits;
     lin /= p.splits;
