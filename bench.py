@@ -423,6 +423,18 @@ def cpu_time(fn, seconds, min_calls=5):
     return statistics.median(times), len(times)
 
 
+def counters_for(row_name):
+    """Derived SQ counter figures of the row's kernel from the committed rocprofv3 summary
+    (profiles/sq_counters.json), or None."""
+    p = REPO / "profiles" / "sq_counters.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(row_name)
+    except (ValueError, OSError):
+        return None
+
+
 def cpu_model_name():
     """The host CPU's model name (from /proc/cpuinfo), or None."""
     try:
@@ -548,6 +560,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
             "traffic": traffic_for("c1_attn"),
+            "mfma_busy_profiled": (counters_for("c1_attn") or {}).get("mfma_busy_frac"),
             "kernel": "attn_fwd_kernel<bf16,64,*>",
             "kernel_ms": head["ms_per_call"],
             "kernel_ms_eager_event_pairs": head["kernel_ms"],
