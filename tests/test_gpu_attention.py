@@ -162,6 +162,28 @@ def test_large_logits_masked_keys_contribute_nothing(native, dev):
     assert np.abs(out.double().numpy() - ref).max() < 2e-2
 
 
+def test_nan_mask_entries_act_as_masked_keys(native, dev):
+    """Decision D6: a NaN in an additive mask is a masked key here (the -5e5 clamp keeps
+    max(NaN, -5e5) = -5e5), so the row stays finite; the reference's raw-mask path keeps
+    the NaN (flash_dm.hpp:93-94) and that row comes out NaN.  Pinned so that a change is
+    deliberate: the output equals the oracle's with the NaN entries set to -inf."""
+    g = C.gen(14)
+    q = C.randn(g, 1, 2, 32, 64)
+    k = C.randn(g, 1, 2, 64, 64)
+    v = C.randn(g, 1, 2, 64, 64)
+    mask = torch.zeros(1, 1, 32, 64)
+    mask[..., 5, 10] = float("nan")
+    mask[..., 7, ::3] = float("nan")
+    mask[..., 9, :] = float("nan")  # every key: the fully-masked rule (D1)
+    native.reset_counters()
+    out = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev), attn_mask=mask.to(dev)).cpu()
+    _ran(native)
+    assert torch.isfinite(out).all()
+    as_masked = mask.masked_fill(mask.isnan(), float("-inf"))
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), as_masked.numpy())
+    assert np.abs(out.double().numpy() - ref).max() < 2e-2
+
+
 def test_split_kv_matches_single_pass(native, dev):
     """Decode shapes split the keys across workgroups; the merged result matches the
     oracle and the per-(batch, head) rows stay isolated."""
