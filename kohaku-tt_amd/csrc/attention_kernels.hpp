@@ -1137,9 +1137,35 @@ template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH, int NW>
 __global__ __launch_bounds__(NW * kWave, (D == 64 && NQB == 2 && MK == MK_NONE && !RS && TWIDTH == 32) ? 4 : 1)
 void attn_fwd_kernel(const AttnParams p) {
     int lin = blockIdx.x;
+    const int units = p.batch * p.hkv;
+    if (p.xcd_map != 0) {
+        // XCD-aware order (one split, no pairs): the dispatcher deals workgroups to the
+        // eight XCDs in turn, so block b runs on XCD b % 8; each XCD takes its own units,
+        // whose K/V then stay in its L2 instead of every XCD streaming every unit.
+        const int x = lin & 7, s = lin >> 3;
+        int bh, xi;
+        if (p.xcd_map == 1) {
+            // Unit u on XCD u % 8; within an XCD the query tile rows go heaviest first.
+            const int nxu = (units - x + 7) >> 3;
+            if (nxu <= 0) return;
+            const int rank = s / nxu;
+            if (rank >= p.nx) return;
+            bh = x + 8 * (s - rank * nxu);
+            xi = p.causal ? p.nx - 1 - rank : rank;
+        } else {
+            // The unit-major query tiles, one contiguous chunk per XCD.
+            const int total = p.nx * units, per = (total + 7) >> 3;
+            const int item = x * per + s;
+            if (s >= per || item >= total) return;
+            bh = item / p.nx;
+            const int r = item - bh * p.nx;
+            xi = p.causal ? p.nx - 1 - r : r;
+        }
+        attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, 0, bh, xi);
+        return;
+    }
     const int split = lin % p.splits;
     lin /= p.splits;
-    const int units = p.batch * p.hkv;
     const int xi = lin / units;
     // Varlen: the units of a query tile row are rotated by 9 per row.  Workgroups are dealt
     // to XCDs and then shader engines in fixed rotation, so without it the units that have
@@ -1695,6 +1721,16 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
             wsum > 0.f ? (m + log2f(wsum)) * kLn2 + (any_masked ? 0.f : kMaskedLogit) : -INFINITY;
 }
 
+// KMI_ATTN_XCD_MAP (read once): 0 keeps the plain workgroup order everywhere, 1 also
+// orders causal / varlen grids by XCD; unset: non-causal dense grids only.
+inline int xcd_map_mode() {
+    static const int v = [] {
+        const char* e = std::getenv("KMI_ATTN_XCD_MAP");
+        return e ? std::atoi(e) : 2;
+    }();
+    return v;
+}
+
 template <typename T, int D, int NQB, int MK, bool RS = false, int TWIDTH = WN, int NW = NWAVES>
 hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) {
     static std::once_flag once;
@@ -1726,6 +1762,25 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
         const int64_t extra = grid - slots;
         p.npair = static_cast<int>(std::min<int64_t>(ceil_div(extra, units), p.nx / 2));
         grid -= static_cast<int64_t>(p.npair) * units;
+    }
+    // XCD-aware order for non-causal dense grids whose units' K/V exceed an XCD's 4 MB L2:
+    // each XCD takes a contiguous chunk of the unit-major query tiles (C5 self: 149 -> 47
+    // MB of L2 misses for 42 MB of data, 140 -> 136 us).  Causal and varlen grids keep the
+    // plain order: unit u on XCD u % 8 cut C4's misses 352 -> 54 MB but ran 63 -> 73 us
+    // (its misses were served by the MALL, not what bounded it); KMI_ATTN_XCD_MAP=1 asks
+    // for it.
+    p.xcd_map = 0;
+    const int64_t kv_bytes = units * static_cast<int64_t>(p.seq_k) * p.d * 2 * static_cast<int64_t>(sizeof(T));
+    if (!RS && p.splits == 1 && p.npair == 0 && kv_bytes > (int64_t{4} << 20) && xcd_map_mode() != 0) {
+        if (p.cu_q || p.causal) {
+            if (units >= 8 && xcd_map_mode() == 1) {
+                p.xcd_map = 1;
+                grid = 8 * ceil_div(units, 8) * static_cast<int64_t>(p.nx);
+            }
+        } else {
+            p.xcd_map = 2;
+            grid = 8 * ceil_div(static_cast<int64_t>(p.nx) * units, 8);
+        }
     }
     hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH, NW>), dim3(static_cast<unsigned>(grid)), dim3((NW * kWave)), lds,
                        stream, p);

@@ -47,6 +47,10 @@ struct AttnParams {
     int splits, tiles_per_split;
     int nx;  // query tiles per (sequence, K/V head)
     int npair;  // causal: the 2 npair shortest query tiles of a unit run two per workgroup
+    // Workgroup order across the XCDs (block b runs on XCD b % 8): 0 the plain order; 1
+    // unit u on XCD u % 8, query tiles heaviest first; 2 the unit-major query tiles in one
+    // contiguous chunk per XCD.  Either keeps a unit's K/V in the L2 of one or two XCDs.
+    int xcd_map;
     int total_q, total_k;  // varlen packed token counts
     int64_t rows_total;
 };
