@@ -477,14 +477,19 @@ int64_t rms_bwd_chunks(int64_t rows) {
 //   xh = (x - m) r, g = dy w, dx = r (g - mean(g) [LayerNorm only] - xh mean(g xh)),
 //   dw = sum over rows of dy xh, db = sum over rows of dy
 // (the reference's ktt_norm backward and column-sum programs, layernorm.md:90-102; torch's
-// native_layer_norm_backward computes the same).  A 256-thread block takes a run of
-// consecutive rows; wavefront w takes rows w, w + 4, ... of it, holds a row in registers as
+// native_layer_norm_backward computes the same).  A block of four wavefronts takes a run of
+// consecutive rows; wavefront w takes rows w, w + 4, ... of it (the next one's loads
+// issued before the current one is worked on), holds a row in registers as
 // VPL 16-byte vectors per lane, reduces mean(g) and mean(g xh) across its lanes, writes dx
-// and adds dy xh (and dy) into per-lane column sums.  The four wavefronts' column sums
+// and adds dy xh (and dy) into per-lane column sums.  The wavefronts' column sums
 // meet in LDS in wavefront order and the block writes one partial row pair;
 // norm_bwd_colsum adds the blocks' partials in block order (deterministic, no atomics).
+// Wavefronts per block of the one-pass backward (eight measured slower: C5 LayerNorm's
+// row pass 14.9 -> 23 us).
+constexpr int kNormBwdWaves = 4;
+
 template <typename T, typename W, bool LAYER, int VPL, bool HW, bool HB>
-__global__ __launch_bounds__(256) void norm_bwd_rows(const T* dy, const T* x, const float* mean, const float* rstd,
+__global__ __launch_bounds__(kNormBwdWaves * kWave) void norm_bwd_rows(const T* dy, const T* x, const float* mean, const float* rstd,
                                                      const W* weight, T* __restrict__ dx, float* __restrict__ part,
                                                      int64_t rows, int width, int64_t rows_per_block) {
     constexpr int E = 16 / sizeof(T);
@@ -507,15 +512,31 @@ __global__ __launch_bounds__(256) void norm_bwd_rows(const T* dy, const T* x, co
             if constexpr (HB) ab[i][j] = 0.f;
         }
     const float inv_w = 1.f / static_cast<float>(width);
-    for (int64_t row = r0 + wave; row < r1; row += 4) {
-        const T* xr = x + row * width;
-        const T* gr = dy + row * width;
-        u32x4 rx[VPL], rg[VPL];
+    // This wavefront's rows r0 + wave, r0 + wave + kNormBwdWaves, ...: the next row's dy and x are
+    // requested before the current row is worked on.
+    int voff[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) voff[i] = min(lane + kWave * i, nvec - 1) * E;
+    u32x4 nx_x[VPL], nx_g[VPL];
+    if (r0 + wave < r1) {
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
-            const int vc = min(lane + kWave * i, nvec - 1);
-            rx[i] = *reinterpret_cast<const u32x4*>(xr + vc * E);
-            rg[i] = *reinterpret_cast<const u32x4*>(gr + vc * E);
+            nx_x[i] = *reinterpret_cast<const u32x4*>(x + (r0 + wave) * width + voff[i]);
+            nx_g[i] = *reinterpret_cast<const u32x4*>(dy + (r0 + wave) * width + voff[i]);
+        }
+    }
+    for (int64_t row = r0 + wave; row < r1; row += kNormBwdWaves) {
+        u32x4 rx[VPL], rg[VPL];
+        for (int i = 0; i < VPL; ++i) {
+            rx[i] = nx_x[i];
+            rg[i] = nx_g[i];
+        }
+        if (row + kNormBwdWaves < r1) {
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                nx_x[i] = *reinterpret_cast<const u32x4*>(x + (row + kNormBwdWaves) * width + voff[i]);
+                nx_g[i] = *reinterpret_cast<const u32x4*>(dy + (row + kNormBwdWaves) * width + voff[i]);
+            }
         }
 #pragma unroll
         for (int i = 0; i < VPL; ++i)
@@ -558,12 +579,12 @@ __global__ __launch_bounds__(256) void norm_bwd_rows(const T* dy, const T* x, co
             }
         }
     }
-    // The wavefronts' column sums, added in wavefront order; wavefront 3 writes the block's
+    // The wavefronts' column sums, added in wavefront order; the last wavefront writes the block's
     // partial rows [blockIdx.x][2][width].  part is null when neither dw nor db is asked for
     // (the same for the whole grid, so every wavefront leaves here together).
     if (part == nullptr) return;
     float* pw = part + static_cast<int64_t>(blockIdx.x) * 2 * width;
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kNormBwdWaves; ++w) {
         if (wave == w) {
 #pragma unroll
             for (int i = 0; i < VPL; ++i) {
@@ -574,7 +595,7 @@ __global__ __launch_bounds__(256) void norm_bwd_rows(const T* dy, const T* x, co
                     const int col = vi * E + j;
                     const float vw = aw[i][j] + (w > 0 ? colsum[col] : 0.f);
                     const float vb = HB ? ab[i][j] + (w > 0 ? colsum[width + col] : 0.f) : 0.f;
-                    if (w < 3) {
+                    if (w < kNormBwdWaves - 1) {
                         colsum[col] = vw;
                         if (HB) colsum[width + col] = vb;
                     } else {
@@ -589,17 +610,29 @@ __global__ __launch_bounds__(256) void norm_bwd_rows(const T* dy, const T* x, co
 }
 
 // dw (and db) from the blocks' partial rows: 64 columns per block, 16 lanes over the
-// partial rows (lane l takes rows l, l + 16, ...), their sums added in lane order.
+// partial rows (lane l takes rows l, l + 16, ... -- at most 32 of them, all loaded in one
+// round: a loop of dependent rounds made this pass as long as the row pass), their sums
+// added in lane order.
+constexpr int kColsumRowsPerLane = 32;  // norm_bwd_blocks() <= 16 * this
 __global__ __launch_bounds__(1024) void norm_bwd_colsum(const float* part, void* dw, void* db, int w_dtype,
                                                         int b_dtype, int nblocks, int width) {
     __shared__ float red[2][16][64];
     const int c = blockIdx.x * 64 + (threadIdx.x & 63), l = threadIdx.x >> 6;
     float sw = 0.f, sb = 0.f;
     if (c < width) {
-#pragma unroll 4
-        for (int b = l; b < nblocks; b += 16) {
-            sw += part[static_cast<int64_t>(b) * 2 * width + c];
-            if (db) sb += part[static_cast<int64_t>(b) * 2 * width + width + c];
+        float vw[kColsumRowsPerLane], vb[kColsumRowsPerLane];
+#pragma unroll
+        for (int i = 0; i < kColsumRowsPerLane; ++i) {
+            const int b = min(l + 16 * i, nblocks - 1);
+            vw[i] = part[static_cast<int64_t>(b) * 2 * width + c];
+            vb[i] = db ? part[static_cast<int64_t>(b) * 2 * width + width + c] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < kColsumRowsPerLane; ++i) {
+            if (l + 16 * i < nblocks) {
+                sw += vw[i];
+                sb += vb[i];
+            }
         }
     }
     red[0][l][threadIdx.x & 63] = sw;
@@ -618,8 +651,12 @@ __global__ __launch_bounds__(1024) void norm_bwd_colsum(const float* part, void*
 }
 
 // Blocks of the one-pass backward: about two per CU, whole wavefront rows each.
-int64_t norm_bwd_blocks(int64_t rows) { return std::max<int64_t>(1, std::min<int64_t>(512, ceil_div(rows, 4))); }
-int64_t norm_bwd_rows_per_block(int64_t rows) { return ceil_div(ceil_div(rows, norm_bwd_blocks(rows)), 4) * 4; }
+int64_t norm_bwd_blocks(int64_t rows) {
+    return std::max<int64_t>(1, std::min<int64_t>(512, ceil_div(rows, kNormBwdWaves)));
+}
+int64_t norm_bwd_rows_per_block(int64_t rows) {
+    return ceil_div(ceil_div(rows, norm_bwd_blocks(rows)), kNormBwdWaves) * kNormBwdWaves;
+}
 
 // The vector lanes the one-pass backward needs for a row (0 when it does not apply: the
 // row must be whole 16-byte vectors, 16-byte aligned, at most 4 vectors per lane: more
@@ -653,7 +690,7 @@ hipError_t launch_norm_bwd(const void* dy, const void* x, const float* mean, con
     auto* wp = static_cast<const W*>(w);
     auto* dxp = static_cast<T*>(dx);
 #define KMI_BWD_LAUNCH(N, HWV, HBV)                                                                        \
-    hipLaunchKernelGGL((norm_bwd_rows<T, W, LAYER, N, HWV, HBV>), dim3(static_cast<unsigned>(nb)), dim3(256), \
+    hipLaunchKernelGGL((norm_bwd_rows<T, W, LAYER, N, HWV, HBV>), dim3(static_cast<unsigned>(nb)), dim3(kNormBwdWaves * kWave), \
                        lds, s, dyp, xp, mean, rstd, wp, dxp, part, rows, width, rpb)
 #define KMI_BWD_CASE(N)                                  \
     case N:                                              \

@@ -146,8 +146,8 @@ def test_rms_norm_backward_rejects_malformed_calls_before_launch():
     lib = capi.lib()
     n = ctypes.c_size_t()
     assert lib.kmi_rms_norm_bwd_workspace_bytes(2048, 896, ctypes.byref(n)) == capi.KMI_OK
-    # the larger of the one-pass kernel's partial rows (2 x 512 blocks) and the element
-    # path's 16-row chunks (128) of fp32 column sums
+    # the larger of the one-pass kernel's partial rows (2 x 512 blocks of four rows) and
+    # the element path's 16-row chunks (128) of fp32 column sums
     assert n.value == max(2 * 512, 128) * 896 * 4
     assert lib.kmi_rms_norm_bwd_workspace_bytes(-1, 896, ctypes.byref(n)) == capi.KMI_EINVAL
     p = 0x1000
