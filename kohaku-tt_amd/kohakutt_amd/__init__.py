@@ -46,6 +46,7 @@ def _load():
 _load()
 
 from . import attention  # noqa: E402
+from . import chains  # noqa: E402,F401
 from .attention import sdpa, sdpa_varlen  # noqa: E402,F401
 
 attention.install()

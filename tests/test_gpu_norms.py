@@ -278,3 +278,27 @@ def test_rms_norm_forward_and_backward_capture_in_a_graph(native, dev):
         assert torch.equal(dx_static, dx_eager) and torch.equal(dw_static, dw_eager)
         step()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_compiled_rms_norm_chain_runs_the_kernel(native, dev):
+    """torch.compile with kohakutt_amd.chains.backend turns a Hugging Face RMSNorm chain
+    into ktt::rms_norm, which runs the norm kernel on the GPU (one call, counted)."""
+    from kohakutt_amd import chains
+
+    g = torch.Generator().manual_seed(91)
+    x = torch.randn(2, 37, 896, generator=g).bfloat16()
+    w = (1 + 0.02 * torch.randn(896, generator=g)).bfloat16()
+
+    def hf(x, w):
+        h = x.to(torch.float32)
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)
+        return w * h.to(x.dtype)
+
+    torch._dynamo.reset()
+    f = torch.compile(hf, backend=chains.backend, fullgraph=True)
+    native.reset_counters()
+    y = f(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert native.counters()["norms"] == 1, native.counters()
+    ref = F.rms_norm(x.double(), [896], w.double(), 1e-6)
+    _check("compiled rms chain", y.cpu(), hf(x, w), ref, torch.bfloat16)
