@@ -20,6 +20,21 @@
 namespace kmi {
 namespace {
 
+// Row-block grids.  HIP bounds each grid dimension at 2^32 - 1 work-items, which one
+// 256-thread block per row passes at 2^24 rows (and one wavefront per row at 2^26): a
+// launch of more blocks than kGridX spreads them over y, and a block finds its index as
+// y * gridDim.x + x (blocks past the last row return before any barrier).
+constexpr int64_t kGridX = int64_t{1} << 20;
+
+dim3 block_grid(int64_t blocks) {
+    if (blocks <= kGridX) return dim3(static_cast<unsigned>(blocks));
+    return dim3(static_cast<unsigned>(kGridX), static_cast<unsigned>(ceil_div(blocks, kGridX)));
+}
+
+__device__ __forceinline__ int64_t block_index() {
+    return static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+}
+
 template <typename T, int E>
 struct alignas(E * sizeof(T)) Pack {
     T e[E];
@@ -77,7 +92,7 @@ __global__ __launch_bounds__(1024) void norm_rows_wave(
     int64_t rows, int width, float eps) {
     constexpr int E = 16 / sizeof(T);
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x >> 6);
+    const int64_t row = block_index() * (blockDim.x / kWave) + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int nvec = width / E;
     const T* xr = x + row * width;
@@ -160,13 +175,14 @@ template <typename T, typename W, int VPT, bool LAYER, int PRM>
 __global__ __launch_bounds__(256) void norm_rows_block(
     const T* x, const W* weight, const W* bias,
     T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
-    int width, float eps) {
+    int64_t rows, int width, float eps) {
     constexpr int E = 16 / sizeof(T);
     constexpr int NW = 4;
     __shared__ float red[2][NW];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1), wave = tid >> 6;
-    const int64_t row = blockIdx.x;
+    const int64_t row = block_index();
+    if (row >= rows) return;
     const int nvec = width / E;
     const T* xr = x + row * width;
     constexpr bool HW = PRM & 1, HB = PRM & 2;  // weight, bias (see norm_rows_wave)
@@ -276,9 +292,10 @@ __device__ float block_sum(float v, float* scratch) {
 template <bool LAYER>
 __global__ __launch_bounds__(256) void norm_rows_generic(
     const void* x, const void* weight, const void* bias, void* y, float* mean_out,
-    float* rstd_out, int64_t width, int x_dtype, int w_dtype, int b_dtype, float eps) {
+    float* rstd_out, int64_t rows, int64_t width, int x_dtype, int w_dtype, int b_dtype, float eps) {
     __shared__ float scratch[4];
-    const int64_t row = blockIdx.x;
+    const int64_t row = block_index();
+    if (row >= rows) return;
     const int64_t base = row * width;
     float s = 0.f;
     for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
@@ -319,7 +336,7 @@ hipError_t launch_wave(const void* x, const void* w, const void* b, void* y, flo
     // 16 rows per block once there are enough rows to fill the chip that way (fewer
     // workgroups to dispatch), 4 rows per block otherwise.
     const int rpb = rows >= 16 * 512 ? 16 : 4;
-    const dim3 grid(static_cast<unsigned>(ceil_div(rows, rpb))), block(kWave * rpb);
+    const dim3 grid = block_grid(ceil_div(rows, rpb)), block(kWave * rpb);
     auto* xp = static_cast<const T*>(x);
     auto* wp = static_cast<const W*>(w);
     auto* bp = static_cast<const W*>(b);
@@ -352,7 +369,7 @@ template <typename T, typename W, bool LAYER>
 hipError_t launch_block(const void* x, const void* w, const void* b, void* y, float* mean,
                         float* rstd, int64_t rows, int width, float eps, int vpt,
                         hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(rows)), block(256);
+    const dim3 grid = block_grid(rows), block(256);
     auto* xp = static_cast<const T*>(x);
     auto* wp = static_cast<const W*>(w);
     auto* bp = static_cast<const W*>(b);
@@ -362,13 +379,13 @@ hipError_t launch_block(const void* x, const void* w, const void* b, void* y, fl
     case N:                                                                                         \
         switch (prm) {                                                                              \
             case 0: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 0>), grid, block, 0, stream, \
-                                       xp, wp, bp, yp, mean, rstd, width, eps); break;              \
+                                       xp, wp, bp, yp, mean, rstd, rows, width, eps); break;        \
             case 1: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 1>), grid, block, 0, stream, \
-                                       xp, wp, bp, yp, mean, rstd, width, eps); break;              \
+                                       xp, wp, bp, yp, mean, rstd, rows, width, eps); break;        \
             case 2: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 2>), grid, block, 0, stream, \
-                                       xp, wp, bp, yp, mean, rstd, width, eps); break;              \
+                                       xp, wp, bp, yp, mean, rstd, rows, width, eps); break;        \
             default: hipLaunchKernelGGL((norm_rows_block<T, W, N, LAYER, 3>), grid, block, 0, stream, \
-                                        xp, wp, bp, yp, mean, rstd, width, eps);                    \
+                                        xp, wp, bp, yp, mean, rstd, rows, width, eps);              \
         }                                                                                           \
         break;
     switch (vpt) {
@@ -401,9 +418,10 @@ bool aligned(const void* p, int64_t bytes) {
 // dx: one 256-thread block per row, fp32 sums; any width and alignment.
 template <typename T>
 __global__ __launch_bounds__(256) void rms_bwd_rows(const T* dy, const T* x, const void* weight, const float* rstd,
-                                                    T* dx, int64_t width, int w_dtype) {
+                                                    T* dx, int64_t rows, int64_t width, int w_dtype) {
     __shared__ float scratch[4];
-    const int64_t row = blockIdx.x;
+    const int64_t row = block_index();
+    if (row >= rows) return;
     const int64_t base = row * width;
     float s = 0.f;
 #pragma unroll 4
@@ -456,9 +474,9 @@ template <typename T>
 hipError_t launch_rms_bwd(const void* dy, const void* x, const void* weight, const float* rstd, void* dx,
                           void* dweight, int64_t rows, int64_t width, int w_dtype, float* part, int64_t chunks,
                           hipStream_t s) {
-    hipLaunchKernelGGL((rms_bwd_rows<T>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
-                       static_cast<const T*>(dy), static_cast<const T*>(x), weight, rstd, static_cast<T*>(dx), width,
-                       w_dtype);
+    hipLaunchKernelGGL((rms_bwd_rows<T>), block_grid(rows), dim3(256), 0, s,
+                       static_cast<const T*>(dy), static_cast<const T*>(x), weight, rstd, static_cast<T*>(dx), rows,
+                       width, w_dtype);
     if (dweight) {
         const unsigned gx = static_cast<unsigned>(ceil_div(width, 256));
         hipLaunchKernelGGL((rms_bwd_dw_partial<T>), dim3(gx, static_cast<unsigned>(chunks)), dim3(256), 0, s,
@@ -786,8 +804,8 @@ int norm_fwd(const char* name, const void* x, const void* w, const void* b, void
             default: err = go(float{}, float{});
         }
     } else {
-        hipLaunchKernelGGL((norm_rows_generic<LAYER>), dim3(static_cast<unsigned>(rows)),
-                           dim3(256), 0, stream, x, w, b, y, mean, rstd, width, x_dtype,
+        hipLaunchKernelGGL((norm_rows_generic<LAYER>), block_grid(rows),
+                           dim3(256), 0, stream, x, w, b, y, mean, rstd, rows, width, x_dtype,
                            w_dtype, b_dtype, e);
         err = hipGetLastError();
     }

@@ -239,6 +239,59 @@ def test_layer_norm_backward_wide_rows_keep_torch_kernel(native, dev):
     assert torch.isfinite(x.grad).all()
 
 
+def _rows_close(got, want, tol):
+    err = (got.double() - want).abs().max().item()
+    assert err <= tol * max(want.abs().max().item(), 1.0), (err, tol)
+
+
+def test_row_counts_past_one_grid_dimension(native, dev):
+    """Row counts whose one-block-per-row (2^24 rows) or one-wavefront-per-row (2^26 rows)
+    grids pass HIP's 2^32 work-items per grid dimension: forward element path, forward
+    wavefront path and the RMSNorm backward element path, checked on the first and last
+    rows against float64 (rows are independent) and dweight against its float64 sum."""
+    g = torch.Generator(device=dev).manual_seed(61)
+    sample = lambda t: torch.cat([t[:2048], t[-2048:]]).cpu()  # noqa: E731
+
+    rows = (1 << 24) + 3  # width 3: the element path, one block per row
+    x = torch.randn(rows, 3, device=dev, generator=g).bfloat16()
+    w = (1 + 0.05 * torch.randn(3, device=dev, generator=g)).bfloat16()
+    native.reset_counters()
+    y = F.rms_norm(x, (3,), w, 1e-6)
+    torch.cuda.synchronize()
+    assert native.counters()["norms"] == 1
+    want, _ = onorm.rms_norm(sample(x).double().numpy(), w.cpu().double().numpy(), eps=1e-6)
+    _rows_close(sample(y), torch.from_numpy(want), 2e-2)
+
+    xg = x.clone().requires_grad_()
+    wg = w.clone().requires_grad_()
+    dy = torch.randn(rows, 3, device=dev, generator=g).bfloat16()
+    F.rms_norm(xg, (3,), wg, 1e-6).backward(dy)
+    torch.cuda.synchronize()
+    assert native.counters()["norms_backward"] == 1
+    xs = sample(x).double().requires_grad_()
+    F.rms_norm(xs, (3,), w.cpu().double(), 1e-6).backward(sample(dy).double())
+    _rows_close(sample(xg.grad), xs.grad, 2e-2)
+    x64, dy64 = x.double(), dy.double()
+    r64 = torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6)
+    terms = dy64 * x64 * r64
+    dw = terms.sum(0).cpu()
+    spread = terms.pow(2).sum(0).sqrt().cpu()
+    assert ((wg.grad.cpu().double() - dw).abs() <= 1e-2 * spread + 1e-3 * dw.abs()).all(), (wg.grad, dw)
+    del xg, wg, dy, x64, dy64, r64, terms
+
+    rows = (1 << 26) + 5  # width 8: one 16-byte vector, one wavefront per row
+    x = torch.randn(rows, 8, device=dev, generator=g).bfloat16()
+    wl = (1 + 0.05 * torch.randn(8, device=dev, generator=g)).bfloat16()
+    bl = (0.1 * torch.randn(8, device=dev, generator=g)).bfloat16()
+    y, mean, rstd = torch.native_layer_norm(x, (8,), wl, bl, 1e-5)
+    torch.cuda.synchronize()
+    want, m64, r64 = onorm.layer_norm(sample(x).double().numpy(), wl.cpu().double().numpy(),
+                                      bl.cpu().double().numpy(), eps=1e-5)
+    _rows_close(sample(y), torch.from_numpy(want), 2e-2)
+    _rows_close(sample(rstd), torch.from_numpy(r64), 1e-5)
+    _rows_close(sample(mean), torch.from_numpy(m64), 1e-5)
+
+
 def test_rms_norm_forward_and_backward_capture_in_a_graph(native, dev):
     """RMSNorm forward and backward captured in one HIP graph after a side-stream warm-up
     (the autograd engine runs each backward node on its forward's stream, so the forward
