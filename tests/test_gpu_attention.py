@@ -332,6 +332,18 @@ def test_varlen_key_mask_and_neighbour_independence(native, dev):
     assert torch.equal(out[40:41], out2[40:41])
 
 
+def test_varlen_op_refuses_undersized_longest_lengths(native, dev):
+    """The packed op checks max_q / max_k against host offsets itself (callers may reach
+    it without the Python front)."""
+    q = torch.randn(8, 2, 64, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(9, 2, 64, device=dev, dtype=torch.bfloat16)
+    cu_q, cu_k = torch.tensor([0, 3, 8]), torch.tensor([0, 4, 9])
+    with pytest.raises(ValueError, match="below the longest sequence"):
+        torch.ops.ktt._sdpa_varlen_offsets(q, k, k, cu_q, cu_k, 4, 5, False, None, None, None)
+    out, _ = torch.ops.ktt._sdpa_varlen_offsets(q, k, k, cu_q, cu_k, 5, 5, False, None, None, None)
+    assert torch.isfinite(out).all()
+
+
 def test_varlen_cross_lengths_bottom_right(native, dev):
     g = C.gen(22)
     cu_q = [0, 10, 30, 31]

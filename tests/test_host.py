@@ -89,3 +89,13 @@ def test_key_lengths_validation_follows_the_reference():
         _as_counts([1, 6], 2, 5, "cpu")
     with pytest.raises(ValueError, match="one length per batch"):
         _as_counts([1, 2, 3], 2, 5, "cpu")
+
+
+@pytest.mark.parametrize("max_q,max_k", [(2, None), (None, 3), (4, 4)])
+def test_varlen_undersized_longest_lengths_are_refused(max_q, max_k):
+    """max_q / max_k size the kernels' grid and LDS; values below the longest sequence of
+    host offsets are refused before any tensor is read (here on CPU tensors)."""
+    q = torch.zeros(8, 2, 64, dtype=torch.bfloat16)
+    k = torch.zeros(9, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="below the longest sequence"):
+        kohakutt_amd.sdpa_varlen(q, k, k, [0, 3, 8], [0, 4, 9], max_q=max_q, max_k=max_k)
