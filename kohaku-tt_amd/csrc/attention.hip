@@ -70,8 +70,12 @@ int splits_override() {
     return v;
 }
 
-// The row-block counts a padded head dim is instantiated for: 1, 2 up to 128, 4 at 64.
-bool nqb_allowed(int dp, int nqb) { return nqb == 1 || (nqb == 2 && dp <= 128) || (nqb == 4 && dp == 64); }
+// The row-block counts a padded head dim is instantiated for: 1, 2 up to 128, 4 at 64
+// (masked: 2 at 64, 1 above).
+bool nqb_allowed(int dp, int nqb, bool masked) {
+    if (masked) return nqb == 1 || (nqb == 2 && dp == 64);
+    return nqb == 1 || (nqb == 2 && dp <= 128) || (nqb == 4 && dp == 64);
+}
 
 Plan make_plan(const kmi_attn_args* a) {
     Plan pl{};
@@ -91,7 +95,7 @@ Plan make_plan(const kmi_attn_args* a) {
     // at two wavefronts per SIMD.
     if (a->mask_mode != KMI_MASK_NONE) nqb = std::min(nqb, dp == 64 ? 2 : 1);
     const int forced = nqb_override();
-    if (nqb_allowed(dp, forced)) nqb = forced;
+    if (nqb_allowed(dp, forced, a->mask_mode != KMI_MASK_NONE)) nqb = forced;
     pl.nqb = nqb;
     const int64_t bm = 16 * pl.nqb;
     pl.nx = static_cast<int>(ceil_div(vrows, bm));
@@ -130,7 +134,7 @@ Plan make_plan(const kmi_attn_args* a) {
     // gives every CU a workgroup.
     if (!pl.decode && pl.splits == 1 && !a->causal && a->mask_mode == KMI_MASK_NONE && nk <= 8 && dp <= 128) {
         int q = dp == 64 ? (ceil_div(vrows, 256) * units >= 512 ? 4 : 2) : 1;
-        if (nqb_allowed(dp, forced)) q = forced;
+        if (nqb_allowed(dp, forced, false)) q = forced;
         const int64_t nx_rs = ceil_div(vrows, NWAVES * 16 * q);
         if (nx_rs * units >= 256) {
             pl.rs = true;

@@ -118,7 +118,14 @@ __device__ __forceinline__ int64_t packed_block_offset(const AttnParams& p, int 
 
 // D: the padded head dim (a multiple of 32; the call's own head dim, a multiple of 8, is
 // AttnParams::d and the columns past it are zeros in registers and LDS).
-template <int D, int NQB, int TWIDTH = WN, int NW = NWAVES>
+// Unmasked, head-dim-64 tiles of 32 keys and 32 or 64 rows take K and V from global memory
+// straight into LDS (buffer loads with the lds modifier).
+template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
+constexpr bool fwd_dma() {
+    return !RS && MK == MK_NONE && D == 64 && (NQB == 2 || NQB == 4) && TWIDTH == 32 && sizeof(T) == 2;
+}
+
+template <int D, int NQB, int TWIDTH = WN, int NW = NWAVES, bool DMA = false>
 struct Shape {
     static constexpr int TW = TWIDTH;    // keys per wavefront tile
     static constexpr int BM = 16 * NQB;  // rows of a workgroup (shared by its wavefronts)
@@ -135,7 +142,7 @@ struct Shape {
     static constexpr bool PREFETCH = D <= 128;
     // K fragments straight from memory into registers (KD) where the wavefront's 64 rows
     // give each loaded fragment the most use; otherwise K is staged in LDS too.
-    static constexpr bool KD = D == 64 && NQB == 4;
+    static constexpr bool KD = D == 64 && NQB == 4 && !DMA;
     static constexpr int TILE = (KD ? 0 : TW * KP) + TW * VP;  // elements of one wavefront's tile
     static constexpr int CP = D + 4;     // merge buffer row pitch (floats)
     // The merge runs over groups of MB row blocks whose buffer fits in the tile area
@@ -213,7 +220,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     static_assert(!RS || MK == MK_NONE, "row split is for unmasked calls (no block barriers)");
     static_assert(!RS || NW == NWAVES, "row split plans four wavefronts");
     typedef typename Mfma<T>::v8 v8;
-    typedef Shape<D, NQB, TWIDTH, NW> S;
+    typedef Shape<D, NQB, TWIDTH, NW, fwd_dma<T, D, NQB, MK, RS, TWIDTH>()> S;
     constexpr int TW = S::TW;   // keys per tile
     constexpr int KH = TW / 32;  // 32-key chunks per tile (one PV MFMA each)
     constexpr int BM = S::BM, VP = S::VP, KP = S::KP, CP = S::CP;
@@ -341,9 +348,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         lim[b] = p.causal ? min(lk, pos + coff + 1) : lk;  // keys [0, lim) are visible
         const T* src = qp + qb_off + head * p.qs[1] + static_cast<int64_t>(q0 + pos) * p.qs[2];
         // Rows past the end read row r_begin (in range) and are never written; columns past
-        // the head dim read in range and are zeroed.
+        // the head dim read in range and are zeroed below (a uniform fix-up, so that the
+        // common case waits for these loads only where the loop first uses them).
 #pragma unroll
-        for (int c = 0; c < DC; ++c) qf[b][c] = head_frag<v8>(src, 32 * c + 8 * g4, p.d);
+        for (int c = 0; c < DC; ++c) qf[b][c] = *reinterpret_cast<const v8*>(src + min(32 * c + 8 * g4, p.d - 8));
         if constexpr (MASKED) {
             if (p.mask_mode == KMI_MASK_PACKED) {
                 mrow[b] = m_seq_packed + static_cast<int64_t>(pos) * lk;
@@ -387,7 +395,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
     T* vl = kl + (KD ? 0 : TW * KP);
 
-    // DMA2 (32-row tiles at D = 64, unmasked): K and V tiles go from global memory
+    // DMA2 (32- and 64-row tiles at D = 64, unmasked): K and V tiles go from global memory
     // straight into the wavefront's LDS tile (buffer loads with the lds modifier: no
     // staging registers, no LDS store instructions).  A step reads all of its tile's K and
     // V fragments first, then requests the next tile into the same buffer, so the wait
@@ -396,7 +404,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // c ^ vswz(r)) so that K's row reads and V's transposed reads hit distinct banks.  DMA
     // instruction i fills rows 8 i .. 8 i + 7; lane q the slot of row 8 i + q / 8,
     // physical chunk q % 8.
-    constexpr bool DMA2 = !KD && !RS && MK == MK_NONE && D == 64 && NQB == 2 && TW == 32 && sizeof(T) == 2;
+    constexpr bool DMA2 = fwd_dma<T, D, NQB, MK, RS, TWIDTH>();
     // Swizzles chosen so that rows r and r + 16 share one (the fragment reads of the second
     // 16-key block are an immediate offset away) and, within a DMA instruction's eight rows
     // 8 i + a, depend on a and the parity of i only (the row term 8 i * stride goes to the
@@ -592,14 +600,20 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     } else if (S::PREFETCH && t_spec < t_end && !rs_shared) {
         load_tile(t_spec);
     }
+    // Padded head dims zero Q's columns past d; a negative scale flips Q's sign.  Both are
+    // uniform, and only they wait for the Q loads here.
     float c2 = p.scale_log2;
-    if (c2 < 0.f) {
-        c2 = -c2;
+    const bool qneg = c2 < 0.f;
+    if (qneg) c2 = -c2;
+    if (kpad || qneg) {
+        const uint32_t flip = qneg ? 0x80008000u : 0u;
 #pragma unroll
         for (int b = 0; b < NQB; ++b)
 #pragma unroll
-            for (int c = 0; c < DC; ++c)
-                qf[b][c] = __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, qf[b][c]) ^ 0x80008000u);
+            for (int c = 0; c < DC; ++c) {
+                const u32x4 x = __builtin_bit_cast(u32x4, qf[b][c]) ^ flip;
+                qf[b][c] = __builtin_bit_cast(v8, 32 * c + 8 * g4 < p.d ? x : u32x4{0u, 0u, 0u, 0u});
+            }
     }
 
     // Key-mask tile skipping: with a mask that depends only on the key (a padding mask),
@@ -1044,28 +1058,30 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             if (g4 == 0) stats[wave * BM + 16 * b + l16] = f32x4{m_run[b], l_run[b], raw[b] ? 1.f : 0.f, 0.f};
         }
         __syncthreads();
-        // thread -> (row, 4 consecutive head-dim columns): weights of the wavefronts, their
-        // O sum, the normalised row.
-        for (int idx = tid; idx < BM * VPRO; idx += (NW * kWave)) {
-            const int row = idx / VPRO, col = 4 * (idx - (idx / VPRO) * VPRO);
+        // thread -> (row, 8 consecutive head-dim columns): weights of the wavefronts, their
+        // O sum, the normalised row (one combine per thread at 32 rows).
+        constexpr int CG = D / 8;  // 8-column groups of a row
+        for (int idx = tid; idx < BM * CG; idx += (NW * kWave)) {
+            const int row = idx / CG, col = 8 * (idx % CG);
             const int r = r_begin + row;
             if (r >= r_end) continue;
             f32x4 sw[NW];
-            f32x4 ov[NW];
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                sw[w] = stats[w * BM + row];
-                ov[w] = *reinterpret_cast<const f32x4*>(
-                    reinterpret_cast<const float*>(smem + static_cast<size_t>(w) * S::TILE * sizeof(T)) + row * CP + col);
-            }
+            for (int w = 0; w < NW; ++w) sw[w] = stats[w * BM + row];
             float wt[NW], m, lt;
             bool any_masked;
             combine(sw, wt, m, lt, any_masked);
-            f32x4 acc = ov[0] * wt[0];
+            f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int w = 1; w < NW; ++w) acc += ov[w] * wt[w];
-            acc *= lt > 0.f ? 1.f / lt : 0.f;
-            write_row(r, col, acc);
+            for (int w = 0; w < NW; ++w) {
+                const float* ow =
+                    reinterpret_cast<const float*>(smem + static_cast<size_t>(w) * S::TILE * sizeof(T)) + row * CP + col;
+                lo += *reinterpret_cast<const f32x4*>(ow) * wt[w];
+                hi += *reinterpret_cast<const f32x4*>(ow + 4) * wt[w];
+            }
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;
+            write_row(r, col, lo * inv);
+            write_row(r, col + 4, hi * inv);
             if (col == 0) write_lse(r, lt > 0.f ? m + log2f(lt) : -INFINITY, !any_masked && MASKED);
         }
     } else {
@@ -1134,7 +1150,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 // The 32-row D = 64 unmasked variant (K and V by DMA, no staging registers) is held to
 // four wavefronts per SIMD.
 template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH, int NW>
-__global__ __launch_bounds__(NW * kWave, (D == 64 && NQB == 2 && MK == MK_NONE && !RS && TWIDTH == 32) ? 4 : 1)
+__global__ __launch_bounds__(NW * kWave, (fwd_dma<T, D, NQB, MK, RS, TWIDTH>() ? (NQB == 2 ? 4 : 2) : 1))
 void attn_fwd_kernel(const AttnParams p) {
     int lin = blockIdx.x;
     const int units = p.batch * p.hkv;
@@ -1736,7 +1752,7 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     static int per_cu = 0;  // resident workgroups per CU
-    typedef Shape<D, NQB, TWIDTH, NW> S;
+    typedef Shape<D, NQB, TWIDTH, NW, fwd_dma<T, D, NQB, MK, RS, TWIDTH>()> S;
     // Shared row split: every key tile of a unit (at most four) in LDS, K then V.
     constexpr size_t rs_max = RS ? kRsTiles * TWIDTH * static_cast<size_t>(S::KP + S::VP) * sizeof(T) : 0;
     const size_t lds_tiles = S::template lds_bytes<T>();
