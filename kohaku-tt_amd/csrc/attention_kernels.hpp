@@ -1182,6 +1182,13 @@ void attn_fwd_kernel(const AttnParams p) {
     }
     const int split = lin % p.splits;
     lin /= p.splits;
+    if (p.snake > 0) {
+        // One resident round: the rank order alternates direction per round of CU count
+        // blocks (C1: the most key tiles on one CU 148 -> 121, mean 114).
+        const int round = lin / p.snake, pos = lin - round * p.snake;
+        const int in_round = min(p.snake, p.nx * units - round * p.snake);
+        if (round & 1) lin = round * p.snake + (in_round - 1 - pos);
+    }
     const int xi = lin / units;
     // Varlen: the units of a query tile row are rotated by 9 per row.  Workgroups are dealt
     // to XCDs and then shader engines in fixed rotation, so without it the units that have
@@ -1786,11 +1793,14 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
     // (its misses were served by the MALL, not what bounded it); KMI_ATTN_XCD_MAP=1 asks
     // for it.
     p.xcd_map = 0;
+    p.snake = 0;
+    if (p.causal && !p.cu_q && p.splits == 1 && p.npair == 0 && slots > 0 && grid <= slots) p.snake = cu_count();
     const int64_t kv_bytes = units * static_cast<int64_t>(p.seq_k) * p.d * 2 * static_cast<int64_t>(sizeof(T));
     if (!RS && p.splits == 1 && p.npair == 0 && kv_bytes > (int64_t{4} << 20) && xcd_map_mode() != 0) {
         if (p.cu_q || p.causal) {
             if (units >= 8 && xcd_map_mode() == 1) {
                 p.xcd_map = 1;
+                p.snake = 0;
                 grid = 8 * ceil_div(units, 8) * static_cast<int64_t>(p.nx);
             }
         } else {

@@ -51,6 +51,10 @@ struct AttnParams {
     // unit u on XCD u % 8, query tiles heaviest first; 2 the unit-major query tiles in one
     // contiguous chunk per XCD.  Either keeps a unit's K/V in the L2 of one or two XCDs.
     int xcd_map;
+    // Causal grids resident in one round: the CU count n (0: off).  Blocks b, b + n, b + 2n
+    // ... run on one CU, so the heaviest-first rank order runs forward in even rounds of n
+    // blocks and backward in odd ones, which evens out the work each CU gets.
+    int snake;
     int total_q, total_k;  // varlen packed token counts
     int64_t rows_total;
 };
