@@ -841,8 +841,6 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             }
             // The reads are done before the next tile's DMA lands in the same buffer.
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            const int t_next = next_tile(t + TS);
-            if (t_next < t_end) dma_tile(t_next);
             f32x4 s[KB][NQB];
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
@@ -853,6 +851,9 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                     for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
                 }
             }
+            // The next tile's request issues while the S MFMAs run.
+            const int t_next = next_tile(t + TS);
+            if (t_next < t_end) dma_tile(t_next);
             const MCur mnone{};
             consume(t, s, mnone);
             t = t_next;
