@@ -122,7 +122,7 @@ __device__ __forceinline__ int64_t packed_block_offset(const AttnParams& p, int 
 // straight into LDS (buffer loads with the lds modifier).
 template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
 constexpr bool fwd_dma() {
-    return !RS && MK == MK_NONE && D == 64 && (NQB == 2 || NQB == 4) && TWIDTH == 32 && sizeof(T) == 2;
+    return MK == MK_NONE && D == 64 && (NQB == 2 || (NQB == 4 && !RS)) && TWIDTH == 32 && sizeof(T) == 2;
 }
 
 template <int D, int NQB, int TWIDTH = WN, int NW = NWAVES, bool DMA = false>
@@ -596,7 +596,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     const int t_spec = t_begin + (RS ? 0 : wave);
     const bool rs_shared = RS && p.rs_shared;
     if constexpr (DMA2) {
-        if (t_spec < t_end) dma_tile(t_spec);
+        if (t_spec < t_end && !rs_shared) dma_tile(t_spec);
     } else if (S::PREFETCH && t_spec < t_end && !rs_shared) {
         load_tile(t_spec);
     }
@@ -769,7 +769,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         // The V fragments are requested first; the MFMAs of row block b then interleave
         // with the exponentials of row block b + 1 (scheduling groups below).
         v8 vf[KH][DB];
-        if constexpr (DMA2) {
+        if (DMA2 && !rs_shared) {
 #pragma unroll
             for (int d = 0; d < DB; ++d) vf[0][d] = vpre[d];
         } else
@@ -816,7 +816,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 
     int t = next_tile(t_spec);
     if (!DMA2 && S::PREFETCH && t != t_spec && t < t_end && !rs_shared) load_tile(t);
-    if constexpr (DMA2) {
+    if (DMA2 && !rs_shared) {
         while (t < t_end) {
             // This tile's K and V fragments, once its DMA has landed: an explicit wait, as the
             // compiler's own wait covers the transposed reads but not the plain ones.
