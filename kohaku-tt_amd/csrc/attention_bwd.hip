@@ -297,11 +297,22 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         return static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
     };
     TileRegs<DP> qr, dor;
+    // Row statistics of an item's rows (threads < BT hold one row each), loaded with its
+    // Q and dO a whole item ahead.
+    float lv_n = 0.f, dr_n = 0.f;
+    auto load_stats = [&](int h, int r0) {
+        if (threadIdx.x < BT) {
+            const int ic = min(r0 + static_cast<int>(threadIdx.x), g.lq - 1);
+            lv_n = p.lse[g.lb + h * p.ls[1] + static_cast<int64_t>(g.q0 + ic) * p.ls[2]];
+            dr_n = p.dr[h * p.rows_total + g.row_base + ic];
+        }
+    };
     if (split < items) {
         int h, r0;
         item_at(split, h, r0);
         load_regs<T, DP>(q_of(h), p.qs[2], r0, g.lq, p.d, qr);
         load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, p.d, dor);
+        load_stats(h, r0);
     }
     for (int it = split; it < items; it += p.splits) {
         int h, r0;
@@ -310,16 +321,13 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         store_regs<T, DP>(qr, qs, qt);
         store_regs<T, DP>(dor, dos, dot);
         if (threadIdx.x < BT) {
-            const int i = r0 + threadIdx.x;
-            const bool ok = i < g.lq;
-            const int ic = min(i, g.lq - 1);
-            const float lv = p.lse[g.lb + h * p.ls[1] + static_cast<int64_t>(g.q0 + ic) * p.ls[2]];
+            const bool ok = r0 + static_cast<int>(threadIdx.x) < g.lq;
             float l2;
             bool raw;
-            row_stats(lv, ok, l2, raw);
+            row_stats(lv_n, ok, l2, raw);
             lse2[threadIdx.x] = l2;
             raws[threadIdx.x] = raw ? 1 : 0;
-            drs[threadIdx.x] = ok ? p.dr[h * p.rows_total + g.row_base + ic] : 0.f;
+            drs[threadIdx.x] = ok ? dr_n : 0.f;
         }
         __syncthreads();
         if (it + p.splits < items) {  // the next item's loads overlap this item's products
@@ -327,6 +335,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
             item_at(it + p.splits, h2, r2);
             load_regs<T, DP>(q_of(h2), p.qs[2], r2, g.lq, p.d, qr);
             load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, p.d, dor);
+            load_stats(h2, r2);
         }
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
