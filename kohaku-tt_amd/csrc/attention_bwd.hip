@@ -27,6 +27,7 @@
 // index (16 contiguous bytes per lane), so tiles needed with either index contiguous are
 // staged twice, row-major and transposed.  lse is the forward's natural-log row LSE.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -56,6 +57,37 @@ struct BwdMfma<f16> {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
 };
+
+// gfx950's transposed LDS read: within each 16-lane group, output lane j, slot s receives
+// element j % 4 of the 4-element chunk that source lane 4 s + j / 4 addressed.  Source lane
+// k of group g pointing at M[row(g, k / 4)][col0 + 4 (k % 4)] so delivers M[row(g, s)][col0
+// + j] to lane j, slot s.  tr_frag reads the B operand of a product contracted over the
+// 32 rows of a row-major tile: lane (g, l) gets column col0 + l of rows 4 g + s (slots
+// 0..3) and 16 + 4 g + s (slots 4..7).  The A operand pairs with it when its row k-slots
+// follow the same order (P^T / dS^T rows stored at perm_row()).
+template <typename T>
+__device__ __forceinline__ typename BwdMfma<T>::v8 tr_frag(const T* tile, int pitch, int col0, int g4, int l16) {
+    const T* src = tile + (4 * g4 + (l16 >> 2)) * pitch + col0 + 4 * (l16 & 3);
+    u32x2 lo, hi;
+    if constexpr (std::is_same<T, bf16>::value) {
+        typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 x4;
+        lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                           (__attribute__((address_space(3))) x4*)(const_cast<T*>(src))));
+        hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                           (__attribute__((address_space(3))) x4*)(const_cast<T*>(src + 16 * pitch))));
+    } else {
+        typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 x4;
+        lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                           (__attribute__((address_space(3))) x4*)(const_cast<T*>(src))));
+        hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                           (__attribute__((address_space(3))) x4*)(const_cast<T*>(src + 16 * pitch))));
+    }
+    return __builtin_bit_cast(typename BwdMfma<T>::v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+}
+
+// Position of row r (0..31) in the k order tr_frag delivers: rows 4 g + s, 16 + 4 g + s
+// at 8 g + s, 8 g + 4 + s.
+__device__ __forceinline__ int perm_row(int r) { return 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3); }
 
 struct BwdParams {
     const void *q, *k, *v, *o, *dout;
@@ -240,9 +272,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T qs[BT * RP];
     __shared__ __align__(16) T dos[BT * RP];
-    __shared__ __align__(16) T qt[DP * TP];
-    __shared__ __align__(16) T dot[DP * TP];
-    __shared__ __align__(16) T pt[4 * 16 * TP];   // per wavefront: P^T [16 keys][32 rows]
+    __shared__ __align__(16) T pt[4 * 16 * TP];   // per wavefront: P^T [16 keys][32 rows, perm_row order]
     __shared__ __align__(16) T dst[4 * 16 * TP];  // per wavefront: dS^T
     __shared__ float lse2[BT], drs[BT];
     __shared__ int raws[BT];
@@ -318,8 +348,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         int h, r0;
         item_at(it, h, r0);
         __syncthreads();  // the previous item's LDS reads are done
-        store_regs<T, DP>(qr, qs, qt);
-        store_regs<T, DP>(dor, dos, dot);
+        store_regs<T, DP>(qr, qs, nullptr);
+        store_regs<T, DP>(dor, dos, nullptr);
         if (threadIdx.x < BT) {
             const bool ok = r0 + static_cast<int>(threadIdx.x) < g.lq;
             float l2;
@@ -351,6 +381,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
             }
             const int rl = rb * 16 + l16;
             const int row = r0 + rl;
+            const int pr = perm_row(rl);
             const float l2 = lse2[rl], dr = drs[rl];
             const bool raw = raws[rl] != 0;
 #pragma unroll
@@ -365,8 +396,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
                 }
                 // Rows past the end carry lse2 = +inf: their P is exactly 0.
                 const float e = keep ? __builtin_amdgcn_exp2f(st[j] * p.c2 + add - l2) : 0.f;
-                ptw[(4 * g4 + j) * TP + rl] = from_f32<T>(e);
-                dsw[(4 * g4 + j) * TP + rl] = from_f32<T>(e * (dpt[j] - dr));
+                ptw[(4 * g4 + j) * TP + pr] = from_f32<T>(e);
+                dsw[(4 * g4 + j) * TP + pr] = from_f32<T>(e * (dpt[j] - dr));
             }
         }
         // The compiler keeps these LDS reads after the stores above (same arrays); the
@@ -376,8 +407,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         const v8 sa = *reinterpret_cast<const v8*>(dsw + l16 * TP + 8 * g4);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-            const v8 ob = *reinterpret_cast<const v8*>(dot + (db * 16 + l16) * TP + 8 * g4);
-            const v8 qb = *reinterpret_cast<const v8*>(qt + (db * 16 + l16) * TP + 8 * g4);
+            // dO^T and Q^T straight from the row-major tiles (transposed reads).
+            const v8 ob = tr_frag<T>(dos, RP, 16 * db, g4, l16);
+            const v8 qb = tr_frag<T>(qs, RP, 16 * db, g4, l16);
             dv[db] = BwdMfma<T>::run(pa, ob, dv[db]);
             dk[db] = BwdMfma<T>::run(sa, qb, dk[db]);
         }
