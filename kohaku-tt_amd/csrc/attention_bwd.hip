@@ -23,9 +23,9 @@
 // (logit <= -5e5) get P = 0; a row whose lse carries the -5e5 offset of a fully-masked
 // row (the forward ran it over its raw scores) takes every visible key's raw score.
 // S = Q K^T, dP = dO V^T and the three gradient products run on
-// v_mfma_f32_16x16x32_{bf16,f16}; every operand is read from LDS along its contraction
-// index (16 contiguous bytes per lane), so tiles needed with either index contiguous are
-// staged twice, row-major and transposed.  lse is the forward's natural-log row LSE.
+// v_mfma_f32_16x16x32_{bf16,f16}; tiles are staged row-major once, and an operand needed
+// along the other index comes out of the same tile through gfx950's transposed LDS reads
+// (tr_frag).  lse is the forward's natural-log row LSE.
 #include <algorithm>
 #include <type_traits>
 
@@ -206,9 +206,7 @@ __device__ __forceinline__ void row_stats(float lse_nat, bool valid, float& lse2
 
 // Staging of rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) in two steps:
 // loads into registers (16-byte chunks, zeros past the last row and the head dim), issued
-// a tile ahead, and their LDS stores, row-major at pitch DP + 8 and, when dstT is set,
-// transposed ([DP][TP]).  Consecutive lanes take consecutive rows of one 8-column chunk,
-// so the transposed 2-byte stores of a wavefront spread over the banks.
+// a tile ahead, and their LDS stores, row-major at pitch DP + 8.
 template <int DP>
 struct TileRegs {
     static constexpr int NV = BT * DP / 8;  // 16-byte chunks of a tile
@@ -231,18 +229,13 @@ __device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int 
 }
 
 template <typename T, int DP>
-__device__ __forceinline__ void store_regs(const TileRegs<DP>& t, T* dst, T* dstT) {
+__device__ __forceinline__ void store_regs(const TileRegs<DP>& t, T* dst) {
 #pragma unroll
     for (int j = 0; j < TileRegs<DP>::PER; ++j) {
         const int c = threadIdx.x + BWD_THREADS * j;
         if (c >= TileRegs<DP>::NV) break;
         const int r = c % BT, ch = c / BT;
         *reinterpret_cast<u32x4*>(dst + r * (DP + 8) + 8 * ch) = t.v[j];
-        if (dstT) {
-            const auto e = __builtin_bit_cast(typename BwdMfma<T>::v8, t.v[j]);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) dstT[(8 * ch + i) * TP + r] = e[i];
-        }
     }
 }
 
@@ -259,7 +252,7 @@ __device__ __forceinline__ u32x4 frag(const T* base, int64_t rs, int row, int nr
 // dK / dV: a workgroup takes KW keys of one K/V head; wavefront w owns keys
 // [kt0 + 16 w, + 16) with its K and V fragments in registers (the A operands of
 // S^T = K Q^T and dP^T = V dO^T).  Per (query head, 32-row query block) item the
-// workgroup stages Q and dO (row-major and transposed) once; each wavefront then forms P^T
+// workgroup stages Q and dO (row-major) once; each wavefront then forms P^T
 // and dS^T of its keys, passes them through its own LDS rows (one wavefront's LDS accesses
 // stay in order: no barrier) and accumulates dV += P^T dO and dK += dS^T Q over every
 // query head of the group.  Two barriers per item.
@@ -348,8 +341,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         int h, r0;
         item_at(it, h, r0);
         __syncthreads();  // the previous item's LDS reads are done
-        store_regs<T, DP>(qr, qs, nullptr);
-        store_regs<T, DP>(dor, dos, nullptr);
+        store_regs<T, DP>(qr, qs);
+        store_regs<T, DP>(dor, dos);
         if (threadIdx.x < BT) {
             const bool ok = r0 + static_cast<int>(threadIdx.x) < g.lq;
             float l2;
@@ -484,7 +477,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_sum(const BwdParams p) {
 
 // dQ: a workgroup takes QW query rows, wavefront w owns rows [r0 + 16 w, + 16) with its Q
 // and dO fragments in registers (the A operands of S = Q K^T and dP = dO V^T).  Per
-// 32-key tile the workgroup stages K (row-major and transposed) and V once; each wavefront
+// 32-key tile the workgroup stages K and V (row-major) once; each wavefront
 // forms dS of its rows, passes it through its own LDS rows and accumulates dQ += dS K.
 constexpr int QW = 64;
 
@@ -495,8 +488,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T ks[BT * RP];
     __shared__ __align__(16) T vs[BT * RP];
-    __shared__ __align__(16) T kt[DP * TP];
-    __shared__ __align__(16) T dss[4 * 16 * TP];  // per wavefront: dS [16 rows][32 keys]
+    __shared__ __align__(16) T dss[4 * 16 * TP];  // per wavefront: dS [16 rows][32 keys, perm_row order]
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -564,8 +556,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     }
     for (int k0 = ksp * BT; k0 < kend; k0 += kstep) {
         __syncthreads();
-        store_regs<T, DP>(kr, ks, kt);
-        store_regs<T, DP>(vr, vs, nullptr);
+        store_regs<T, DP>(kr, ks);
+        store_regs<T, DP>(vr, vs);
         __syncthreads();
         if (k0 + kstep < kend) {  // the next tile's loads overlap this tile's products
             load_regs<T, DP>(kbase, p.ks[2], k0 + kstep, g.lk, p.d, kr);
@@ -595,7 +587,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
                     add = raw[j] ? 0.f : ml * kLog2e;
                 }
                 const float e = keep ? __builtin_amdgcn_exp2f(sv[j] * p.c2 + add - l2[j]) : 0.f;
-                dsw[(4 * g4 + j) * TP + kb * 16 + l16] = from_f32<T>(e * (dpv[j] - drv[j]));
+                dsw[(4 * g4 + j) * TP + perm_row(kb * 16 + l16)] = from_f32<T>(e * (dpv[j] - drv[j]));
             }
         }
         // The compiler keeps this LDS read after the stores above (same array); the hardware
@@ -603,8 +595,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
         __asm__ volatile("" ::: "memory");
         const v8 da = *reinterpret_cast<const v8*>(dsw + l16 * TP + 8 * g4);
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-            dq[db] = BwdMfma<T>::run(da, *reinterpret_cast<const v8*>(kt + (db * 16 + l16) * TP + 8 * g4), dq[db]);
+        for (int db = 0; db < DB; ++db) dq[db] = BwdMfma<T>::run(da, tr_frag<T>(ks, RP, 16 * db, g4, l16), dq[db]);
     }
     // Lane (g4, l16) of block db holds rows rw0 + 4 g4 + j, dim db 16 + l16.
     if (p.pdq) {
