@@ -36,6 +36,7 @@ namespace {
 
 constexpr int BT = 32;          // keys per K/V tile and rows per query block
 constexpr int TP = BT + 8;      // pitch of transposed / [32][32] tiles (elements)
+constexpr int PP = 24;          // pitch of a wavefront's [32][16] P / dS tiles (elements)
 constexpr int BWD_THREADS = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 // A forward lse below this carries the -5e5 offset of a row with no kept key.
@@ -61,10 +62,10 @@ struct BwdMfma<f16> {
 // gfx950's transposed LDS read: within each 16-lane group, output lane j, slot s receives
 // element j % 4 of the 4-element chunk that source lane 4 s + j / 4 addressed.  Source lane
 // k of group g pointing at M[row(g, k / 4)][col0 + 4 (k % 4)] so delivers M[row(g, s)][col0
-// + j] to lane j, slot s.  tr_frag reads the B operand of a product contracted over the
-// 32 rows of a row-major tile: lane (g, l) gets column col0 + l of rows 4 g + s (slots
-// 0..3) and 16 + 4 g + s (slots 4..7).  The A operand pairs with it when its row k-slots
-// follow the same order (P^T / dS^T rows stored at perm_row()).
+// + j] to lane j, slot s.  tr_frag reads an operand of a product contracted over the 32
+// rows of a row-major tile: lane (g, l) gets column col0 + l of rows 4 g + s (slots 0..3)
+// and 16 + 4 g + s (slots 4..7).  Both operands of such a product come from tr_frag, so
+// their k orders agree (P, dS and dS^T are stored row-major for that, 8 bytes per lane).
 template <typename T>
 __device__ __forceinline__ typename BwdMfma<T>::v8 tr_frag(const T* tile, int pitch, int col0, int g4, int l16) {
     const T* src = tile + (4 * g4 + (l16 >> 2)) * pitch + col0 + 4 * (l16 & 3);
@@ -85,9 +86,6 @@ __device__ __forceinline__ typename BwdMfma<T>::v8 tr_frag(const T* tile, int pi
     return __builtin_bit_cast(typename BwdMfma<T>::v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 }
 
-// Position of row r (0..31) in the k order tr_frag delivers: rows 4 g + s, 16 + 4 g + s
-// at 8 g + s, 8 g + 4 + s.
-__device__ __forceinline__ int perm_row(int r) { return 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3); }
 
 struct BwdParams {
     const void *q, *k, *v, *o, *dout;
@@ -265,8 +263,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T qs[BT * RP];
     __shared__ __align__(16) T dos[BT * RP];
-    __shared__ __align__(16) T pt[4 * 16 * TP];   // per wavefront: P^T [16 keys][32 rows, perm_row order]
-    __shared__ __align__(16) T dst[4 * 16 * TP];  // per wavefront: dS^T
+    __shared__ __align__(16) T pt[4 * BT * PP];   // per wavefront: P [32 rows][16 keys]
+    __shared__ __align__(16) T dst[4 * BT * PP];  // per wavefront: dS [32 rows][16 keys]
     __shared__ float lse2[BT], drs[BT];
     __shared__ int raws[BT];
 
@@ -300,8 +298,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     f32x4 dk[DB], dv[DB];
 #pragma unroll
     for (int i = 0; i < DB; ++i) dk[i] = dv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    T* ptw = pt + wave * 16 * TP;
-    T* dsw = dst + wave * 16 * TP;
+    T* ptw = pt + wave * BT * PP;
+    T* dsw = dst + wave * BT * PP;
 
     // Items: (query head of the group, 32-row query block), blocks from the first that
     // sees this tile (causal: rows i >= kt0 - coff); split s takes items s, s + splits, ...
@@ -374,9 +372,10 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
             }
             const int rl = rb * 16 + l16;
             const int row = r0 + rl;
-            const int pr = perm_row(rl);
             const float l2 = lse2[rl], dr = drs[rl];
             const bool raw = raws[rl] != 0;
+            typedef T t4 __attribute__((ext_vector_type(4)));
+            t4 pv, sv;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int key = kw0 + 4 * g4 + j;
@@ -389,15 +388,19 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
                 }
                 // Rows past the end carry lse2 = +inf: their P is exactly 0.
                 const float e = keep ? __builtin_amdgcn_exp2f(st[j] * p.c2 + add - l2) : 0.f;
-                ptw[(4 * g4 + j) * TP + pr] = from_f32<T>(e);
-                dsw[(4 * g4 + j) * TP + pr] = from_f32<T>(e * (dpt[j] - dr));
+                pv[j] = from_f32<T>(e);
+                sv[j] = from_f32<T>(e * (dpt[j] - dr));
             }
+            // Row rl, keys 4 g4 .. + 3: one 8-byte store each.
+            *reinterpret_cast<t4*>(ptw + rl * PP + 4 * g4) = pv;
+            *reinterpret_cast<t4*>(dsw + rl * PP + 4 * g4) = sv;
         }
         // The compiler keeps these LDS reads after the stores above (same arrays); the
         // hardware runs one wavefront's LDS accesses in order.
         __asm__ volatile("" ::: "memory");
-        const v8 pa = *reinterpret_cast<const v8*>(ptw + l16 * TP + 8 * g4);
-        const v8 sa = *reinterpret_cast<const v8*>(dsw + l16 * TP + 8 * g4);
+        // P^T and dS^T fragments (key l16, rows in tr_frag's order) by transposed reads.
+        const v8 pa = tr_frag<T>(ptw, PP, 0, g4, l16);
+        const v8 sa = tr_frag<T>(dsw, PP, 0, g4, l16);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             // dO^T and Q^T straight from the row-major tiles (transposed reads).
@@ -488,7 +491,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T ks[BT * RP];
     __shared__ __align__(16) T vs[BT * RP];
-    __shared__ __align__(16) T dss[4 * 16 * TP];  // per wavefront: dS [16 rows][32 keys, perm_row order]
+    __shared__ __align__(16) T dss[4 * BT * PP];  // per wavefront: dS^T [32 keys][16 rows]
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -542,7 +545,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     f32x4 dq[DB];
 #pragma unroll
     for (int i = 0; i < DB; ++i) dq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    T* dsw = dss + wave * 16 * TP;
+    T* dsw = dss + wave * BT * PP;
 
     // Causal: the block's last row sees keys up to its position + coff.
     const int kend = p.causal ? min(g.lk, max(0, min(r0 + QW, g.lq) - 1 + g.coff + 1)) : g.lk;
@@ -576,6 +579,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
                 dpv = BwdMfma<T>::run(of[c], vbv, dpv);
             }
             const int key = k0 + kb * 16 + l16;
+            typedef T t4 __attribute__((ext_vector_type(4)));
+            t4 dsv;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = rw0 + 4 * g4 + j;
@@ -587,13 +592,16 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
                     add = raw[j] ? 0.f : ml * kLog2e;
                 }
                 const float e = keep ? __builtin_amdgcn_exp2f(sv[j] * p.c2 + add - l2[j]) : 0.f;
-                dsw[(4 * g4 + j) * TP + perm_row(kb * 16 + l16)] = from_f32<T>(e * (dpv[j] - drv[j]));
+                dsv[j] = from_f32<T>(e * (dpv[j] - drv[j]));
             }
+            // Key kb 16 + l16, rows 4 g4 .. + 3: one 8-byte store.
+            *reinterpret_cast<t4*>(dsw + (kb * 16 + l16) * PP + 4 * g4) = dsv;
         }
         // The compiler keeps this LDS read after the stores above (same array); the hardware
         // runs one wavefront's LDS accesses in order.
         __asm__ volatile("" ::: "memory");
-        const v8 da = *reinterpret_cast<const v8*>(dsw + l16 * TP + 8 * g4);
+        // dS fragments (row l16, keys in tr_frag's order) by transposed reads.
+        const v8 da = tr_frag<T>(dsw, PP, 0, g4, l16);
 #pragma unroll
         for (int db = 0; db < DB; ++db) dq[db] = BwdMfma<T>::run(da, tr_frag<T>(ks, RP, 16 * db, g4, l16), dq[db]);
     }
