@@ -700,19 +700,26 @@ const char* check_bwd(const kmi_attn_bwd_args* a) {
 int64_t rows_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q; }
 int64_t keys_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_k : a->batch * a->seq_k; }
 
-// dK / dV splits: enough workgroups for about two per CU (at most 16 splits, at most one
-// per (query head, query block) item).
+// Workgroups the split rules aim for (eight per CU: each backward workgroup runs its items
+// with one wavefront per SIMD and two barriers per item, so it is latency-bound; C1
+// backward 143 us at 512, 114 at 1024, 108 at 2048, 116 at 4096), and the split caps.
+constexpr int64_t kBwdTargetWgs = 2048;
+constexpr int64_t kBwdMaxSplits = 32;
+constexpr int64_t kBwdMaxKsplit = 8;
+
+// dK / dV splits: about kBwdTargetWgs workgroups (at most kBwdMaxSplits splits, at most
+// one per (query head, query block) item).
 int bwd_splits(const kmi_attn_bwd_args* a) {
     const int64_t wgs = a->batch * a->heads_kv * ceil_div(a->seq_k, KW);
     const int64_t items = (a->heads_q / a->heads_kv) * ceil_div(a->seq_q, BT);
-    const int64_t s = std::min<int64_t>(16, std::max<int64_t>(1, ceil_div(512, wgs)));
+    const int64_t s = std::min<int64_t>(kBwdMaxSplits, std::max<int64_t>(1, ceil_div(kBwdTargetWgs, wgs)));
     return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(s, items)));
 }
 
 // dQ key splits, by the same rule over (query head, 64-row block) workgroups.
 int bwd_ksplit(const kmi_attn_bwd_args* a) {
     const int64_t wgs = a->batch * a->heads_q * ceil_div(a->seq_q, QW);
-    const int64_t ks = std::min<int64_t>(4, std::max<int64_t>(1, ceil_div(512, wgs)));
+    const int64_t ks = std::min<int64_t>(kBwdMaxKsplit, std::max<int64_t>(1, ceil_div(kBwdTargetWgs, wgs)));
     return static_cast<int>(std::min<int64_t>(ks, ceil_div(a->seq_k, BT)));
 }
 
