@@ -227,6 +227,10 @@ int enqueue(const kmi_attn_args* a, const Plan& pl, void* workspace, void* strea
     p.rs_shared = pl.rs && pl.rs_shared ? 1 : 0;
     p.total_q = static_cast<int>(a->total_q);
     p.total_k = static_cast<int>(a->total_k);
+    p.fd_splits = fast_div(static_cast<uint32_t>(p.splits));
+    p.fd_units = fast_div(static_cast<uint32_t>(p.batch * p.hkv));
+    p.fd_hkv = fast_div(static_cast<uint32_t>(p.hkv));
+    p.fd_group = fast_div(static_cast<uint32_t>(p.group));
     if (pl.splits > 1) {
         p.part_o = static_cast<float*>(workspace);
         p.part_lse = p.part_o + static_cast<size_t>(pl.splits) * p.rows_total * p.hq * padded_head_dim(a->head_dim);

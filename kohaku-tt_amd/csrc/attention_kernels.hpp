@@ -245,7 +245,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     const int g4 = lane >> 4;
     const int l16 = lane & 15;
 
-    const int seq = bh / p.hkv;
+    const int seq = fdiv(bh, p.fd_hkv);
     const int kvh = bh - seq * p.hkv;
     const int G = p.group;
 
@@ -309,11 +309,11 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     const int r_end = min(vrows, r_begin + BM);
     const int coff = p.cu_q ? (lk - lq) : 0;  // causal: position i sees keys <= i + coff
     int kend = lk;
-    if (p.causal) kend = max(0, min(lk, (r_end - 1) / G + 1 + coff));
+    if (p.causal) kend = max(0, min(lk, fdiv(r_end - 1, p.fd_group) + 1 + coff));
     const int ntiles = (kend + TW - 1) / TW;
     // Keys below lim_min are visible to every row of the workgroup: tiles past it need the
     // per-element causal / tail test, the rest do not.
-    const int lim_min = p.causal ? min(lk, r_begin / G + coff + 1) : lk;
+    const int lim_min = p.causal ? min(lk, fdiv(r_begin, p.fd_group) + coff + 1) : lk;
     int t_begin = 0, t_end = ntiles;
     if (p.splits > 1) {
         t_begin = split * p.tiles_per_split;
@@ -343,7 +343,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         const int r = r_begin + 16 * b + l16;
         const bool valid = r < r_end;
         const int rr = valid ? r : r_begin;
-        const int pos = rr / G;
+        const int pos = fdiv(rr, p.fd_group);
         const int head = kvh * G + (rr - pos * G);
         lim[b] = p.causal ? min(lk, pos + coff + 1) : lk;  // keys [0, lim) are visible
         const T* src = qp + qb_off + head * p.qs[1] + static_cast<int64_t>(q0 + pos) * p.qs[2];
@@ -964,7 +964,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             const int r = r_begin + 16 * b + l16;
             const float l = lacc[b][0];
             if (r >= r_end) continue;
-            const int pos = r / G;
+            const int pos = fdiv(r, p.fd_group);
             const int head = kvh * G + (r - pos * G);
             const float inv = l > 0.f ? 1.f / l : 0.f;
             T* dst = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2];
@@ -1013,7 +1013,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     };
     auto write_row = [&](int r, int col, const f32x4& acc) {
         if (col >= p.d) return;  // padded head-dim columns
-        const int pos = r / G;
+        const int pos = fdiv(r, p.fd_group);
         const int head = kvh * G + (r - pos * G);
         if (p.splits > 1) {
             const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
@@ -1028,7 +1028,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         }
     };
     auto write_lse = [&](int r, float row_lse, bool row_raw) {
-        const int pos = r / G;
+        const int pos = fdiv(r, p.fd_group);
         const int head = kvh * G + (r - pos * G);
         if (p.splits > 1) {
             const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
@@ -1181,22 +1181,24 @@ void attn_fwd_kernel(const AttnParams p) {
         attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, 0, bh, xi);
         return;
     }
-    const int split = lin % p.splits;
-    lin /= p.splits;
+    const int lsp = fdiv(lin, p.fd_splits);
+    const int split = lin - lsp * p.splits;
+    lin = lsp;
     if (p.snake > 0) {
         // One resident round: the rank order alternates direction per round of CU count
         // blocks (C1: the most key tiles on one CU 148 -> 121, mean 114).
-        const int round = lin / p.snake, pos = lin - round * p.snake;
+        const int round = fdiv(lin, p.fd_snake), pos = lin - round * p.snake;
         const int in_round = min(p.snake, p.nx * units - round * p.snake);
         if (round & 1) lin = round * p.snake + (in_round - 1 - pos);
     }
-    const int xi = lin / units;
+    const int xi = fdiv(lin, p.fd_units);
     // Varlen: the units of a query tile row are rotated by 9 per row.  Workgroups are dealt
     // to XCDs and then shader engines in fixed rotation, so without it the units that have
     // work at a given row (the long sequences of the batch) land on the same engines row
     // after row, fill them, and stall the in-order dispatch while the rest of the chip
     // idles.  Equal-length batches keep each XCD on few units (their K/V stay in its L2).
-    const int bh = (lin - xi * units + (p.cu_q ? xi * 9 : 0)) % units;
+    const int bu = lin - xi * units + (p.cu_q ? xi * 9 : 0);
+    const int bh = bu - fdiv(bu, p.fd_units) * units;
     if (!p.causal) {
         attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, split, bh, xi);
         return;
@@ -1246,14 +1248,14 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     const int l16 = lane & 15;
 
     const int wg_per_unit = p.splits;
-    const int bh = blockIdx.x / wg_per_unit;
+    const int bh = fdiv(static_cast<int>(blockIdx.x), p.fd_splits);
     const int split = blockIdx.x - bh * wg_per_unit;
     const int nslots = wg_per_unit * NWAVES;
     // Wavefront-major slots: workgroup `split` takes tiles split, split + wg_per_unit, ...
     // across the whole key range, so every workgroup meets the live keys of a padded row
     // (no workgroup of only masked tiles) and the work spreads evenly.
     const int slot = wave * wg_per_unit + split;
-    const int seq = bh / p.hkv;
+    const int seq = fdiv(bh, p.fd_hkv);
     const int kvh = bh - seq * p.hkv;
     const int G = p.group;
 
@@ -1276,14 +1278,14 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     if (vrows <= 0) return;
     const int coff = p.cu_q ? (lk - lq) : 0;
     int kend = max(lk, 0);
-    if (p.causal) kend = max(0, min(lk, (vrows - 1) / G + 1 + coff));
+    if (p.causal) kend = max(0, min(lk, fdiv(vrows - 1, p.fd_group) + 1 + coff));
     const int ntiles = (kend + WN - 1) / WN;
     const int n_t = slot < ntiles ? (ntiles - 1 - slot) / nslots + 1 : 0;  // this wavefront's tiles
 
     // This lane's row.
     const bool valid = l16 < vrows;
     const int rr = valid ? l16 : 0;
-    const int pos = rr / G;
+    const int pos = fdiv(rr, p.fd_group);
     const int head = kvh * G + (rr - pos * G);
     const int lim = p.causal ? min(lk, pos + coff + 1) : lk;
     v8 qf[DC];
@@ -1796,6 +1798,7 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
     p.xcd_map = 0;
     p.snake = 0;
     if (p.causal && !p.cu_q && p.splits == 1 && p.npair == 0 && slots > 0 && grid <= slots) p.snake = cu_count();
+    p.fd_snake = fast_div(static_cast<uint32_t>(p.snake));
     const int64_t kv_bytes = units * static_cast<int64_t>(p.seq_k) * p.d * 2 * static_cast<int64_t>(sizeof(T));
     if (!RS && p.splits == 1 && p.npair == 0 && kv_bytes > (int64_t{4} << 20) && xcd_map_mode() != 0) {
         if (p.cu_q || p.causal) {

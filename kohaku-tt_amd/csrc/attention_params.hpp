@@ -15,6 +15,30 @@ constexpr int WN = 32;
 // slower: fewer workgroups fit per CU).
 constexpr int kRsTiles = 4;
 
+// n / d for 0 <= n < 2^31 by a multiply-high (the round-up method of Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994): with
+// l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, m) + n) >> l
+// (the sum stays below 2^32 since mulhi(n, m) <= n).  The kernels' tile and row indices
+// divide by a few per-call values (the split count, the unit count, the K/V heads, the
+// GQA group); a runtime integer division is a ~30-instruction sequence through the
+// reciprocal unit, this is three.
+struct FastDiv {
+    uint32_t m, l;
+};
+
+inline FastDiv fast_div(uint32_t d) {
+    if (d == 0) d = 1;
+    uint32_t l = 0;
+    while ((uint64_t{1} << l) < d) ++l;
+    const uint64_t m = ((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1;
+    return FastDiv{static_cast<uint32_t>(m), l};
+}
+
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+    const uint32_t u = static_cast<uint32_t>(n);
+    return static_cast<int>((__umulhi(u, f.m) + u) >> f.l);
+}
+
 struct AttnParams {
     const void* q;
     const void* k;
@@ -55,6 +79,8 @@ struct AttnParams {
     // ... run on one CU, so the heaviest-first rank order runs forward in even rounds of n
     // blocks and backward in odd ones, which evens out the work each CU gets.
     int snake;
+    // Divisors of the index arithmetic (see FastDiv): splits, batch * hkv, hkv, group, snake.
+    FastDiv fd_splits, fd_units, fd_hkv, fd_group, fd_snake;
     int total_q, total_k;  // varlen packed token counts
     int64_t rows_total;
 };
