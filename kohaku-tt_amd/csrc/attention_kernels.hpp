@@ -432,22 +432,21 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 #pragma unroll
         for (int d = 0; d < DB; ++d) vtro[d] = r * D + 8 * (((2 * d) ^ vswz(r)) | ((l16 >> 1) & 1)) + 4 * (l16 & 1);
     }
-    auto dma_tile = [&](int tt) {
+    // One operand's tile: K (V = false) or V into its half of the wavefront's buffer.
+    auto dma_half = [&](int tt, bool V) {
         if constexpr (DMA2) {
             const int key0 = tt * TW;
             const int rows_here = min(lk - key0, TW);
-            const auto rk = buffer_rsrc(kunit + key0 * kstride, static_cast<uint32_t>(rows_here) * kspan);
-            const auto rv = buffer_rsrc(vunit + key0 * vstride, static_cast<uint32_t>(rows_here) * vspan);
+            const int64_t stride = V ? vstride : kstride;
+            const auto rs = buffer_rsrc((V ? vunit : kunit) + key0 * stride,
+                                        static_cast<uint32_t>(rows_here) * (V ? vspan : kspan));
+            T* const dst = V ? vd2 : kd2;
             if (rows_here == TW) {
 #pragma unroll
-                for (int i = 0; i < TW / 8; ++i) {
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(kd2 + i * 512),
-                                                             16, dk_b[i & 1],
-                                                             static_cast<int>(8 * i * static_cast<uint32_t>(kstride)), 0, 0);
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vd2 + i * 512),
-                                                             16, dv_b[i & 1],
-                                                             static_cast<int>(8 * i * static_cast<uint32_t>(vstride)), 0, 0);
-                }
+                for (int i = 0; i < TW / 8; ++i)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 512),
+                                                             16, V ? dv_b[i & 1] : dk_b[i & 1],
+                                                             static_cast<int>(8 * i * static_cast<uint32_t>(stride)), 0, 0);
             } else {
                 // Last tile: rows past the unit's last key repeat it (finite; their scores
                 // are masked), so every lane reads in range and every slot is written.
@@ -456,19 +455,20 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                 for (int i = 0; i < TW / 8; ++i) {
                     const int r = 8 * i + (lane >> 3);
                     const uint32_t rr = static_cast<uint32_t>(min(r, rows_here - 1));
-                    const uint32_t ok = rr * static_cast<uint32_t>(kstride) +
-                                        16u * static_cast<uint32_t>(min((lane & 7) ^ kswz(r), cmax));
-                    const uint32_t ov = rr * static_cast<uint32_t>(vstride) +
-                                        16u * static_cast<uint32_t>(min((lane & 7) ^ vswz(r), cmax));
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rk, (__attribute__((address_space(3))) void*)(kd2 + i * 512), 16, ok, 0, 0, 0);
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rv, (__attribute__((address_space(3))) void*)(vd2 + i * 512), 16, ov, 0, 0, 0);
+                    const uint32_t off = rr * static_cast<uint32_t>(stride) +
+                                         16u * static_cast<uint32_t>(min((lane & 7) ^ (V ? vswz(r) : kswz(r)), cmax));
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 512),
+                                                             16, off, 0, 0, 0);
                 }
             }
         } else {
             (void)tt;
+            (void)V;
         }
+    };
+    auto dma_tile = [&](int tt) {
+        dma_half(tt, false);
+        dma_half(tt, true);
     };
     v8 vpre[DMA2 ? DB : 1];  // DMA2: this tile's V fragments, read at the top of its step
 
@@ -817,21 +817,36 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     int t = next_tile(t_spec);
     if (!DMA2 && S::PREFETCH && t != t_spec && t < t_end && !rs_shared) load_tile(t);
     if (DMA2 && !rs_shared) {
-        while (t < t_end) {
-            // This tile's K and V fragments, once its DMA has landed: an explicit wait, as the
-            // compiler's own wait covers the transposed reads but not the plain ones.
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            v8 kf[KB][DC];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int c = 0; c < DC; ++c) kf[kb][c] = *reinterpret_cast<const v8*>(kd2 + 16 * kb * D + kfo[c]);
+        // A tile's K loads are requested before its V loads.  Row-split tiles: a step waits
+        // for its K alone (the four V loads after it may still be in flight; an explicit
+        // wait, as the compiler's own covers the transposed reads but not the plain ones),
+        // reads the K fragments and issues the S MFMAs, then waits for its V and reads V^T
+        // while they run (C2 B=32 17.1 -> 16.5 us).  Key-split tiles read K and V^T first,
+        // then issue the S MFMAs (the split order measured 21.3 -> 23.0 us on C1, with a
+        // wide spread, and 3% slower on C5 self).  Either way the next tile is requested
+        // (K, then V) once every read of this one is done.
+        static_assert(TW / 8 == 4, "four DMA loads per operand (the vmcnt(4) waits)");
+        constexpr bool KFIRST = RS;
+        auto read_v = [&]() {
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
                 const u32x2 lo = lds_read_tr(vd2 + vtro[d]);           // keys 4 g + s
                 const u32x2 hi = lds_read_tr(vd2 + 16 * D + vtro[d]);  // keys 16 + 4 g + s (same swizzle)
                 vpre[d] = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
             }
+        };
+        while (t < t_end) {
+            const int t_next = next_tile(t + TS);
+            if constexpr (KFIRST) {
+                __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            } else {
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            v8 kf[KB][DC];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int c = 0; c < DC; ++c) kf[kb][c] = *reinterpret_cast<const v8*>(kd2 + 16 * kb * D + kfo[c]);
             if (kpad) {
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb)
@@ -839,7 +854,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                     for (int c = 0; c < DC; ++c)
                         if (32 * c + 8 * g4 >= p.d) kf[kb][c] = v8{};
             }
-            // The reads are done before the next tile's DMA lands in the same buffer.
+            if constexpr (!KFIRST) read_v();
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             f32x4 s[KB][NQB];
 #pragma unroll
@@ -851,8 +866,12 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                     for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
                 }
             }
-            // The next tile's request issues while the S MFMAs run.
-            const int t_next = next_tile(t + TS);
+            if constexpr (KFIRST) {
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's V landed
+                read_v();
+                // The V reads are done before the next tile lands in the same buffer.
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
             if (t_next < t_end) dma_tile(t_next);
             const MCur mnone{};
             consume(t, s, mnone);
