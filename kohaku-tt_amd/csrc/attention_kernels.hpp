@@ -405,6 +405,12 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // instruction i fills rows 8 i .. 8 i + 7; lane q the slot of row 8 i + q / 8,
     // physical chunk q % 8.
     constexpr bool DMA2 = fwd_dma<T, D, NQB, MK, RS, TWIDTH>();
+    // 32-row DMA tiles raise the wavefront's issue priority over its S and PV MFMA
+    // sections (s_setprio 1, back to 0 for the softmax and the loads): of the three or four
+    // wavefronts on a SIMD, one in an MFMA section then wins the arbitration while the
+    // others run their softmax, which keeps the matrix unit fed (C1 23.3 -> 22.1 us; 64-row
+    // tiles measured 2-5% slower with it, head dim 128 no change).
+    constexpr bool PRIO = DMA2 && NQB == 2;
     // Swizzles chosen so that rows r and r + 16 share one (the fragment reads of the second
     // 16-key block are an immediate offset away) and, within a DMA instruction's eight rows
     // 8 i + a, depend on a and the parity of i only (the row term 8 i * stride goes to the
@@ -769,6 +775,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         // The V fragments are requested first; the MFMAs of row block b then interleave
         // with the exponentials of row block b + 1 (scheduling groups below).
         v8 vf[KH][DB];
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
         if (DMA2 && !rs_shared) {
 #pragma unroll
             for (int d = 0; d < DB; ++d) vf[0][d] = vpre[d];
@@ -802,6 +809,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             }
         }
         __builtin_amdgcn_iglp_opt(2);
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     };
     auto take_mask = [&](MCur& mcur) {
         if constexpr (MASKED) {
@@ -817,16 +825,16 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     int t = next_tile(t_spec);
     if (!DMA2 && S::PREFETCH && t != t_spec && t < t_end && !rs_shared) load_tile(t);
     if (DMA2 && !rs_shared) {
-        // A tile's K loads are requested before its V loads.  Row-split tiles: a step waits
-        // for its K alone (the four V loads after it may still be in flight; an explicit
-        // wait, as the compiler's own covers the transposed reads but not the plain ones),
-        // reads the K fragments and issues the S MFMAs, then waits for its V and reads V^T
-        // while they run (C2 B=32 17.1 -> 16.5 us).  Key-split tiles read K and V^T first,
-        // then issue the S MFMAs (the split order measured 21.3 -> 23.0 us on C1, with a
-        // wide spread, and 3% slower on C5 self).  Either way the next tile is requested
-        // (K, then V) once every read of this one is done.
+        // A tile's K loads are requested before its V loads.  32-row tiles (row split or
+        // not): a step waits for its K alone (the four V loads after it may still be in
+        // flight; an explicit wait, as the compiler's own covers the transposed reads but
+        // not the plain ones), reads the K fragments and issues the S MFMAs, then waits for
+        // its V and reads V^T while they run (C2 B=32 17.1 -> 16.5 us; C1, with the MFMA
+        // priority above, 22.2 -> 21.9 us).  64-row key-split tiles read K and V^T first,
+        // then issue the S MFMAs (the split order measured 3% slower on C5 self).  Either
+        // way the next tile is requested (K, then V) once every read of this one is done.
         static_assert(TW / 8 == 4, "four DMA loads per operand (the vmcnt(4) waits)");
-        constexpr bool KFIRST = RS;
+        constexpr bool KFIRST = RS || NQB == 2;
         auto read_v = [&]() {
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
@@ -857,6 +865,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             if constexpr (!KFIRST) read_v();
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             f32x4 s[KB][NQB];
+            if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
@@ -866,6 +875,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                     for (int c = 0; c < DC; ++c) s[kb][b] = Mfma<T>::run(kf[kb][c], qf[b][c], s[kb][b]);
                 }
             }
+            if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
             if constexpr (KFIRST) {
                 __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's V landed
                 read_v();
