@@ -30,12 +30,16 @@ def test_refusal_reasons():
 
 
 def test_ktt_rms_norm_composite_on_cpu():
-    x = torch.randn(3, 40, dtype=torch.float64)
-    w = torch.randn(40, dtype=torch.float64)
-    b = torch.randn(40, dtype=torch.float64)
+    # The composite computes in fp32 whatever the input dtype, as the reference's does
+    # (aten_fused.cpp:13-28): float64 inputs agree with the float64 oracle to fp32 rounding.
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(3, 40, dtype=torch.float64, generator=g)
+    w = torch.randn(40, dtype=torch.float64, generator=g)
+    b = torch.randn(40, dtype=torch.float64, generator=g)
     y = kohakutt_amd.rms_norm(x, w, b, 1e-6)
     yr, _ = N.rms_norm(x.numpy(), w.numpy(), b.numpy(), 1e-6)
-    assert np.abs(y.numpy() - yr).max() < 1e-6
+    err = np.abs(y.numpy() - yr) / (np.abs(yr) + 1.0)
+    assert err.max() < 2e-6
 
 
 @pytest.mark.parametrize(
