@@ -450,6 +450,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     }
 }
 
+// Partials a sum kernel loads before it adds them.
+constexpr int kSumBatch = 8;
+
 // dK / dV rows from the splits' fp32 partials, added in split order.  One item per
 // (K/V head, key row, 4 head-dim columns).
 template <typename T, int DP>
@@ -462,10 +465,26 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_sum(const BwdParams p) {
     const int64_t krow = (item / nq) % p.keys_total;
     const int kvh = static_cast<int>(item / (static_cast<int64_t>(nq) * p.keys_total));
     f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = sk;
-    for (int s = 0; s < p.splits; ++s) {
-        const int64_t row = (static_cast<int64_t>(kvh) * p.splits + s) * p.keys_total + krow;
-        sk += *reinterpret_cast<const f32x4*>(p.pdk + row * DP + 4 * c);
-        sv += *reinterpret_cast<const f32x4*>(p.pdv + row * DP + 4 * c);
+    auto at = [&](int s) { return ((static_cast<int64_t>(kvh) * p.splits + s) * p.keys_total + krow) * DP + 4 * c; };
+    // Eight splits' partials are loaded before they are added (in split order, so the
+    // sums are those of a plain loop): one round trip per eight splits instead of one each.
+    int s = 0;
+    for (; s + kSumBatch <= p.splits; s += kSumBatch) {
+        f32x4 bk[kSumBatch], bv[kSumBatch];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j) {
+            bk[j] = *reinterpret_cast<const f32x4*>(p.pdk + at(s + j));
+            bv[j] = *reinterpret_cast<const f32x4*>(p.pdv + at(s + j));
+        }
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j) {
+            sk += bk[j];
+            sv += bv[j];
+        }
+    }
+    for (; s < p.splits; ++s) {
+        sk += *reinterpret_cast<const f32x4*>(p.pdk + at(s));
+        sv += *reinterpret_cast<const f32x4*>(p.pdv + at(s));
     }
     int64_t koff, voff;
     if (p.cu_q) {
@@ -654,9 +673,17 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_sum(const BwdParams p) {
     const int64_t row = (item / nq) % p.rows_total;
     const int h = static_cast<int>(item / (static_cast<int64_t>(nq) * p.rows_total));
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < p.ksplit; ++k)
-        acc += *reinterpret_cast<const f32x4*>(p.pdq + ((static_cast<int64_t>(h) * p.ksplit + k) * p.rows_total + row) * DP +
-                                               4 * c);
+    auto at = [&](int k) { return ((static_cast<int64_t>(h) * p.ksplit + k) * p.rows_total + row) * DP + 4 * c; };
+    // As in attn_bwd_kv_sum: a batch of loads, then the adds in split order.
+    int k = 0;
+    for (; k + kSumBatch <= p.ksplit; k += kSumBatch) {
+        f32x4 b[kSumBatch];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j) b[j] = *reinterpret_cast<const f32x4*>(p.pdq + at(k + j));
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j) acc += b[j];
+    }
+    for (; k < p.ksplit; ++k) acc += *reinterpret_cast<const f32x4*>(p.pdq + at(k));
     int64_t off;
     if (p.cu_q) {
         off = row * p.dqs[2];
