@@ -17,7 +17,8 @@
 //                    tile -- split s takes items s, s + splits, ... -- the same P / dS;
 //                    dV += P^T dO, dK += dS^T Q in fp32 registers.  One split: it
 //                    writes dK / dV; several: fp32 partials per split that
-//   attn_bwd_kv_sum  adds in split order (no atomics: repeat calls are bit-identical)
+//   attn_bwd_sums    adds in split order (no atomics: repeat calls are bit-identical),
+//                    together with attn_bwd_dq's key-split dQ partials
 //
 // Probabilities follow the forward exactly: keys past the causal limit or masked
 // (logit <= -5e5) get P = 0; a row whose lse carries the -5e5 offset of a fully-masked
@@ -456,9 +457,8 @@ constexpr int kSumBatch = 8;
 // dK / dV rows from the splits' fp32 partials, added in split order.  One item per
 // (K/V head, key row, 4 head-dim columns).
 template <typename T, int DP>
-__global__ __launch_bounds__(256) void attn_bwd_kv_sum(const BwdParams p) {
+__device__ __forceinline__ void kv_sum_item(const BwdParams& p, const int64_t item) {
     const int nq = p.d / 4;  // float4 items per key row (head dims are multiples of 8)
-    const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     const int64_t items = static_cast<int64_t>(p.hkv) * p.keys_total * nq;
     if (item >= items) return;
     const int c = static_cast<int>(item % nq);
@@ -664,9 +664,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
 // dQ rows from the key splits' fp32 partials, in split order.  One item per (query head,
 // query row, 4 head-dim columns).
 template <typename T, int DP>
-__global__ __launch_bounds__(256) void attn_bwd_dq_sum(const BwdParams p) {
+__device__ __forceinline__ void dq_sum_item(const BwdParams& p, const int64_t item) {
     const int nq = p.d / 4;
-    const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     const int64_t items = static_cast<int64_t>(p.hq) * p.rows_total * nq;
     if (item >= items) return;
     const int c = static_cast<int>(item % nq);
@@ -674,7 +673,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_sum(const BwdParams p) {
     const int h = static_cast<int>(item / (static_cast<int64_t>(nq) * p.rows_total));
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     auto at = [&](int k) { return ((static_cast<int64_t>(h) * p.ksplit + k) * p.rows_total + row) * DP + 4 * c; };
-    // As in attn_bwd_kv_sum: a batch of loads, then the adds in split order.
+    // As in kv_sum_item: a batch of loads, then the adds in split order.
     int k = 0;
     for (; k + kSumBatch <= p.ksplit; k += kSumBatch) {
         f32x4 b[kSumBatch];
@@ -694,6 +693,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_sum(const BwdParams p) {
     T* dst = static_cast<T*>(p.dq) + off + h * p.dqs[1] + 4 * c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(acc[e]);
+}
+
+// Both sums in one launch (after dK / dV: neither reads the other's output): blocks
+// [0, dq_blocks) take dQ items (attn_bwd_dq's key-split partials), the rest dK / dV items.
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void attn_bwd_sums(const BwdParams p, const int64_t dq_blocks) {
+    const int64_t b = blockIdx.x;
+    if (b < dq_blocks) {
+        dq_sum_item<T, DP>(p, b * 256 + threadIdx.x);
+    } else {
+        kv_sum_item<T, DP>(p, (b - dq_blocks) * 256 + threadIdx.x);
+    }
 }
 
 const char* check_bwd(const kmi_attn_bwd_args* a) {
@@ -791,19 +802,14 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
     hipLaunchKernelGGL((attn_bwd_dq<T, DP, MK>),
                        dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit)),
                        dim3(BWD_THREADS), 0, s, p);
-    if (p.pdq) {
-        const int64_t items = static_cast<int64_t>(p.hq) * p.rows_total * (p.d / 4);
-        hipLaunchKernelGGL((attn_bwd_dq_sum<T, DP>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0, s,
-                           p);
-    }
     hipLaunchKernelGGL((attn_bwd_dkdv<T, DP, MK>),
                        dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hkv * ntk * p.splits)),
                        dim3(BWD_THREADS), 0, s, p);
-    if (p.pdk) {
-        const int64_t items = static_cast<int64_t>(p.hkv) * p.keys_total * (p.d / 4);
-        hipLaunchKernelGGL((attn_bwd_kv_sum<T, DP>), dim3(static_cast<unsigned>(ceil_div(items, 256))), dim3(256), 0, s,
-                           p);
-    }
+    const int64_t dq_blocks = p.pdq ? ceil_div(static_cast<int64_t>(p.hq) * p.rows_total * (p.d / 4), 256) : 0;
+    const int64_t kv_blocks = p.pdk ? ceil_div(static_cast<int64_t>(p.hkv) * p.keys_total * (p.d / 4), 256) : 0;
+    if (dq_blocks + kv_blocks > 0)
+        hipLaunchKernelGGL((attn_bwd_sums<T, DP>), dim3(static_cast<unsigned>(dq_blocks + kv_blocks)), dim3(256), 0, s,
+                           p, dq_blocks);
     return hipGetLastError();
 }
 
