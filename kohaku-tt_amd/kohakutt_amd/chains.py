@@ -1,31 +1,49 @@
-"""torch.compile graph pass: RMSNorm written out in torch ops becomes one ``ktt::rms_norm``.
+"""torch.compile graph pass: an RMSNorm written out in torch ops becomes one ``ktt::rms_norm``.
 
-The reference's compile backends rewrite such chains before lowering
-(``src/kohakutt/torch_backend/chains.py:1-4,278-338``); this module does the same for
-graphs compiled for the MI355X kernels, so a model that spells RMSNorm as
+The reference's compile backends fuse such chains before lowering
+(``src/kohakutt/torch_backend/chains.py:1-4``); this module does it for graphs compiled
+for the MI355X kernels, so a model that spells RMSNorm as
 
     h = x.to(torch.float32)
     h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
     y = weight * h.to(x.dtype)
 
 (Hugging Face's Llama / Qwen2 norms) runs the fused norm kernel instead of five
-elementwise and reduction kernels.  What is matched: ``t * rsqrt(mean(t*t or t**2, last
-dim, keepdim) + eps)``, ``t`` optionally a cast of the source, followed by casts and at
-most one multiplication by a ``[width]`` floating weight.  What is refused (the graph is
-left as it was): intermediate values with other users, chains whose result needs a
-gradient (``ktt::rms_norm`` has no derivative), a result shaped unlike the input, a
-result dtype that neither the source nor its cast has, and graphs that write the source
-or the weight in place between the chain's first node and its end.
+elementwise and reduction kernels.
 
-``KTT_FUSE_CHAINS`` (read at each compile) selects rewrites as in the reference: unset,
-``1``, ``on`` or ``true`` the default set, ``0``, ``off`` or ``false`` none, ``all``, or a
-comma list of ``norm``, ``rotary``, ``mask``, ``gqa``; another name raises ValueError.
-Only ``norm`` is a rewrite here: RoPE fusion and the reference's mask / GQA conversions
-serve its own device and are outside this build's hot path.
+How it matches.  RMSNorm is a product: ``x · rsqrt(rowmean(x²) + eps) · w``.  The pass
+therefore looks at products, not at chains of calls:
+
+1. Each FX node is read as a term of a small vocabulary (``_term``): ``mul``, ``add``,
+   ``sq`` (both ``t * t`` and ``t ** 2``), ``rowmean`` (a mean over the last dim with
+   keepdim and no dtype), ``rsqrt`` and ``cast`` (any dtype conversion), whatever the
+   spelling (torch function, operator, tensor method, aten or prims overload).
+2. Every maximal product in the graph (nested ``mul`` nodes, casts between them included)
+   is flattened into its factor list, last product first.
+3. The factors must be: one ``rsqrt(rowmean(sq(u)) + eps)`` (either operand order of the
+   add, eps a Python number), one tensor ``t`` that is ``u`` up to casts, and at most one
+   floating vector whose size is the row width.  Factor order and nesting do not matter,
+   so ``(x * r) * w``, ``w * (x * r)`` and ``(x * w) * r`` all match.
+4. The fused op reads the cast of ``x`` (or ``x`` itself) whose dtype is the product's,
+   because ``ktt::rms_norm`` returns its input's dtype; a product in a dtype that no such
+   value has is left alone.
+5. The nodes between that input, the weight and the product's result form the region
+   the fused call replaces.  It must be closed (no node outside it reads an interior
+   node), hold only nodes of the vocabulary, and see no in-place write to its input or
+   weight between its first node and its result.  Results that need a gradient are left
+   alone (``ktt::rms_norm`` has no derivative here), as are results shaped unlike the
+   input.
+
+``KTT_FUSE_CHAINS`` (read at each compile) selects rewrites by the reference's names:
+unset, ``1``, ``on``, ``true`` or ``all`` every one; ``0``, ``off`` or ``false`` none; else
+a comma list of ``norm``, ``rotary``, ``mask``, ``gqa`` (an unknown name raises
+ValueError).  Only ``norm`` exists here: RoPE fusion and the reference's mask / GQA
+conversions serve its own device and are outside this build's hot path.
 """
 
 from __future__ import annotations
 
+import functools
 import operator
 import os
 
@@ -36,215 +54,297 @@ __all__ = ["REWRITES", "selected", "rewrite_rms_norms", "backend"]
 
 REWRITES = ("norm", "rotary", "mask", "gqa")
 
-_A = torch.ops.aten
-_P = torch.ops.prims
-# What a node computes, keyed by call_function target or call_method name.
-_BY_TARGET = {
-    operator.mul: "mul", torch.mul: "mul", _A.mul.Tensor: "mul",
-    operator.add: "add", torch.add: "add", _A.add.Tensor: "add", _A.add.Scalar: "add",
-    torch.rsqrt: "rsqrt", _A.rsqrt.default: "rsqrt",
-    operator.pow: "pow", torch.pow: "pow", _A.pow.Tensor_Scalar: "pow",
-    torch.mean: "mean", _A.mean.dim: "mean",
-    _A._to_copy.default: "cast", _P.convert_element_type.default: "cast",
-}
-_BY_METHOD = {
-    "mul": "mul", "add": "add", "rsqrt": "rsqrt", "pow": "pow", "mean": "mean",
-    "to": "cast", "float": "cast", "bfloat16": "cast", "half": "cast", "type_as": "cast",
-}
+_ALL_WORDS = ("", "1", "on", "true", "all")
+_NONE_WORDS = ("0", "off", "false")
 
 
 def selected() -> set:
-    """The rewrites ``KTT_FUSE_CHAINS`` asks for (see the module docstring)."""
-    raw = os.environ.get("KTT_FUSE_CHAINS")
-    names = [t.strip().lower() for t in (raw or "").split(",") if t.strip()]
-    if not names or names in (["1"], ["on"], ["true"]):
-        return set(REWRITES)
-    if names in (["0"], ["off"], ["false"]):
-        return set()
-    bad = sorted(n for n in names if n not in REWRITES and n != "all")
-    if bad:
+    """The rewrite names ``KTT_FUSE_CHAINS`` selects (case and spaces ignored)."""
+    raw = os.environ.get("KTT_FUSE_CHAINS", "")
+    words = {w.strip().lower() for w in raw.split(",")} - {""}
+    if len(words) <= 1:
+        word = next(iter(words), "")
+        if word in _ALL_WORDS:
+            return set(REWRITES)
+        if word in _NONE_WORDS:
+            return set()
+    unknown = sorted(words - set(REWRITES) - {"all"})
+    if unknown:
         raise ValueError(
-            f"KTT_FUSE_CHAINS={raw!r}: unknown {', '.join(bad)}; use 0, 1, all or a comma list of "
-            f"{', '.join(REWRITES)}"
+            f"KTT_FUSE_CHAINS={raw!r} names unknown rewrite(s) {', '.join(unknown)}; "
+            f"give 0, 1, all, or names from {', '.join(REWRITES)}"
         )
-    return set(REWRITES) if "all" in names else set(names)
+    return set(REWRITES) if "all" in words else words
 
 
-def _what(n) -> str | None:
+# --- step 1: nodes as terms -------------------------------------------------------------
+
+# Names of dtype conversions, as aten / prims packets and as tensor methods.
+_CASTS = frozenset({"_to_copy", "convert_element_type", "to", "float", "half", "bfloat16",
+                    "double", "type_as"})
+# Positional parameter names of each operation; keyword spellings map onto them.
+_PARAMS = {
+    "mul": ("a", "b"), "add": ("a", "b"), "pow": ("a", "exp"), "rsqrt": ("a",),
+    "mean": ("a", "dim", "keepdim", "dtype"), "cast": ("a",),
+}
+_KEYWORDS = {"input": "a", "self": "a", "other": "b", "exponent": "exp"}
+
+
+def _op_name(n) -> str | None:
+    """The operation an FX node calls, by name, for calls into torch, ``operator``, tensor
+    methods and the aten / prims namespaces; None for anything else."""
     if not isinstance(n, torch.fx.Node):
         return None
-    if n.op == "call_function":
-        return _BY_TARGET.get(n.target)
     if n.op == "call_method":
-        return _BY_METHOD.get(n.target)
-    return None
+        name = n.target
+    elif n.op == "call_function":
+        fn = n.target
+        if isinstance(fn, torch._ops.OpOverload):
+            if fn.namespace not in ("aten", "prims"):
+                return None
+            name = fn.overloadpacket.__name__
+        else:
+            name = getattr(fn, "__name__", None)
+            if name is None or not (getattr(torch, name, None) is fn
+                                    or getattr(operator, name, None) is fn):
+                return None
+    else:
+        return None
+    return "cast" if name in _CASTS else name
 
 
-def _operand(n: torch.fx.Node, i: int, name: str | None = None, default=None):
-    if len(n.args) > i:
-        return n.args[i]
-    if name is not None and name in n.kwargs:
-        return n.kwargs[name]
-    if i == 0:
-        return n.kwargs.get("input", n.kwargs.get("self", default))
-    return default
+def _bind(n: torch.fx.Node, op: str) -> dict:
+    """The node's operands under the parameter names of `op`."""
+    bound = dict(zip(_PARAMS[op], n.args))
+    for key, value in n.kwargs.items():
+        bound.setdefault(_KEYWORDS.get(key, key), value)
+    return bound
 
 
-class _Graph:
-    """A graph module and what its nodes compute (fake or real tensors)."""
+def _term(n):
+    """(kind, operands) of a node in the pass's vocabulary, or None.
+
+    kinds: ``mul`` (a, b), ``add`` (a, b), ``sq`` (t,), ``rowmean`` (t,), ``rsqrt`` (t,),
+    ``cast`` (t,).  ``rowmean`` needs the node's value to know the rank, so it is decided in
+    ``_Region``; here a mean is returned as ``mean`` with its bound operands."""
+    op = _op_name(n)
+    if op not in _PARAMS:
+        return None
+    b = _bind(n, op)
+    if op == "mul":
+        if b.get("b") is None:
+            return None
+        if b["a"] is b["b"] and isinstance(b["a"], torch.fx.Node):
+            return "sq", (b["a"],)
+        return "mul", (b["a"], b["b"])
+    if op == "pow":
+        e = b.get("exp")
+        if isinstance(e, (int, float)) and not isinstance(e, bool) and e == 2:
+            return "sq", (b["a"],)
+        return None
+    if op == "add":
+        if b.get("b") is None or b.get("alpha", 1) != 1:
+            return None
+        return "add", (b["a"], b["b"])
+    if op == "mean":
+        return "mean", (b.get("a"), b.get("dim"), b.get("keepdim", False), b.get("dtype"))
+    return op, (b.get("a"),)
+
+
+def _is_number(v) -> bool:
+    return isinstance(v, (int, float)) and not isinstance(v, bool)
+
+
+def _mutates(n: torch.fx.Node) -> bool:
+    """Whether a node may write one of its operands in place."""
+    if n.op == "call_method":
+        name = str(n.target)
+        return name.endswith("_") and not name.endswith("__")
+    if n.op == "call_function":
+        return n.is_impure()
+    return n.op == "call_module"
+
+
+class _Region:
+    """One attempt at one product root of a graph."""
 
     def __init__(self, gm: torch.fx.GraphModule):
         self.gm = gm
-        self.order = {n: i for i, n in enumerate(gm.graph.nodes)}
+        self.pos = {n: i for i, n in enumerate(gm.graph.nodes)}
 
     def value(self, n):
-        """The tensor a node computes, from its metadata (Dynamo ``example_value``, AOT
-        ``val``) or, for a module attribute, the attribute itself; else None."""
+        """The (fake or real) tensor a node computes, or None."""
         if not isinstance(n, torch.fx.Node):
             return None
         v = n.meta.get("val", n.meta.get("example_value"))
         if v is None and n.op == "get_attr":
-            obj = self.gm
             try:
-                for part in str(n.target).split("."):
-                    obj = getattr(obj, part)
+                v = functools.reduce(getattr, str(n.target).split("."), self.gm)
             except AttributeError:
-                return None
-            v = obj
+                v = None
         return v if isinstance(v, torch.Tensor) else None
 
+    def kind(self, n):
+        t = _term(n)
+        if t is None or t[0] != "mean":
+            return t
+        src, dim, keepdim, dtype = t[1]
+        sv = self.value(src)
+        if sv is None or sv.dim() == 0 or keepdim is not True or dtype is not None:
+            return None
+        if isinstance(dim, (list, tuple)):
+            dim = dim[0] if len(dim) == 1 else None
+        if not _is_number(dim) or int(dim) % sv.dim() != sv.dim() - 1:
+            return None
+        return "rowmean", (src,)
 
-def _pair(n, kind):
-    """The two operands of a binary node of `kind`, else None."""
-    if _what(n) != kind:
+    # --- step 2: flatten a product ------------------------------------------------------
+
+    def factors(self, root: torch.fx.Node):
+        """The factor list of the maximal product ending at `root` (casts peeled at the top
+        and between products), or None when root is not a product."""
+        top = root
+        while (k := self.kind(top)) is not None and k[0] == "cast":
+            top = k[1][0]
+        k = self.kind(top)
+        if k is None or k[0] != "mul":
+            return None
+        out, todo = [], list(k[1])
+        while todo:
+            f = todo.pop()
+            if not isinstance(f, torch.fx.Node):
+                out.append(f)
+                continue
+            # A product read only by this one joins it, through casts read only here.
+            inner = f
+            while len(inner.users) == 1 and (fk := self.kind(inner)) is not None and fk[0] == "cast":
+                inner = fk[1][0]
+            fk = self.kind(inner)
+            if fk is not None and fk[0] == "mul" and len(inner.users) == 1:
+                todo.extend(fk[1])
+            else:
+                out.append(f)
+        return out
+
+    # --- step 3: classify the factors ---------------------------------------------------
+
+    def statistic(self, f):
+        """(u, eps) when f = rsqrt(rowmean(sq(u)) + eps), possibly cast, else None."""
+        k = self.kind(self.cast_chain(f)[-1])
+        if k is None or k[0] != "rsqrt":
+            return None
+        k = self.kind(k[1][0])
+        if k is None or k[0] != "add":
+            return None
+        a, b = k[1]
+        mean, eps = (a, b) if _is_number(b) else (b, a)
+        if not _is_number(eps):
+            return None
+        k = self.kind(mean)
+        if k is None or k[0] != "rowmean":
+            return None
+        k = self.kind(k[1][0])
+        if k is None or k[0] != "sq":
+            return None
+        return k[1][0], float(eps)
+
+    def cast_chain(self, n):
+        """n, then each value it is a cast of, down to the first node that is not a cast."""
+        chain = [n]
+        while isinstance(n, torch.fx.Node) and (k := self.kind(n)) is not None and k[0] == "cast":
+            n = k[1][0]
+            chain.append(n)
+        return chain
+
+    def match(self, root: torch.fx.Node):
+        """(input, weight, eps, region) for an RMSNorm product ending at root, else None."""
+        fs = self.factors(root)
+        if fs is None or not 2 <= len(fs) <= 3:
+            return None
+        stats = [(i, s) for i, f in enumerate(fs) if (s := self.statistic(f)) is not None]
+        if len(stats) != 1:
+            return None
+        i, (u, eps) = stats[0]
+        rest = fs[:i] + fs[i + 1:]
+        u_chain = self.cast_chain(u)
+        rv = self.value(root)
+        if rv is None or rv.requires_grad or rv.dim() == 0:
+            return None
+        width = rv.shape[-1]
+        picks = []
+        for ti, t in enumerate(rest):
+            t_chain = self.cast_chain(t)
+            if t_chain[-1] is not u_chain[-1]:
+                continue
+            others = rest[:ti] + rest[ti + 1:]
+            w = others[0] if others else None
+            if w is not None:
+                wv = self.value(w)
+                if wv is None or tuple(wv.shape) != (width,) or not wv.dtype.is_floating_point:
+                    continue
+            # step 4: the input whose dtype is the result's, the source first
+            for cand in reversed(t_chain + u_chain):
+                cv = self.value(cand)
+                if (cv is not None and cv.dtype == rv.dtype and cv.dtype.is_floating_point
+                        and tuple(cv.shape) == tuple(rv.shape)):
+                    picks.append((cand, w))
+                    break
+        for x, w in picks:
+            region = self.region(root, {x, w})
+            if region is not None:
+                return x, w, eps, region
         return None
-    a, b = _operand(n, 0), _operand(n, 1, "other")
-    return (a, b) if b is not None else None
 
+    # --- step 5: the region -------------------------------------------------------------
 
-def _square_of(g: _Graph, n):
-    """t when n computes t * t or t ** 2."""
-    p = _pair(n, "mul")
-    if p is not None and p[0] is p[1] and isinstance(p[0], torch.fx.Node):
-        return p[0]
-    if _what(n) == "pow" and _operand(n, 1, "exponent") == 2:
-        t = _operand(n, 0)
-        return t if isinstance(t, torch.fx.Node) else None
-    return None
-
-
-def _over_last_dim(dims, rank: int) -> bool:
-    if isinstance(dims, (list, tuple)):
-        if len(dims) != 1:
-            return False
-        dims = dims[0]
-    return isinstance(dims, int) and dims in (-1, rank - 1)
-
-
-def _match_core(g: _Graph, r: torch.fx.Node):
-    """(core, t, eps, nodes) for r = rsqrt(mean(t^2, -1, keepdim) + eps) with a user
-    core = t * r, else None."""
-    den = _operand(r, 0)
-    p = _pair(den, "add")
-    if p is None:
-        return None
-    mean, eps = (p[0], p[1]) if isinstance(p[1], (int, float)) else (p[1], p[0])
-    if not isinstance(eps, (int, float)) or isinstance(eps, bool) or _what(mean) != "mean":
-        return None
-    sq = _operand(mean, 0)
-    sv = g.value(sq)
-    if sv is None or sv.dim() == 0 or not _over_last_dim(_operand(mean, 1, "dim"), sv.dim()):
-        return None
-    if not _operand(mean, 2, "keepdim", False) or _operand(mean, 3, "dtype") is not None:
-        return None
-    t = _square_of(g, sq)
-    if t is None:
-        return None
-    for user in r.users:
-        q = _pair(user, "mul")
-        if q is not None and (q[0] is t or q[1] is t) and (q[0] is r or q[1] is r):
-            return user, t, float(eps), [den, mean, sq, r]
-    return None
-
-
-def _writes(n: torch.fx.Node, targets) -> bool:
-    """Whether n may write one of `targets` in place (an in-place method or a mutating
-    aten overload taking it)."""
-    if not any(a in targets for a in n.all_input_nodes):
-        return False
-    if n.op == "call_method":
-        return str(n.target).endswith("_")
-    schema = getattr(n.target, "_schema", None)
-    return bool(schema is not None and schema.is_mutable)
-
-
-def _rewrite_one(g: _Graph, r: torch.fx.Node) -> bool:
-    found = _match_core(g, r)
-    if found is None:
-        return False
-    core, t, eps, inner = found
-    if any(len(n.users) != 1 for n in inner):
-        return False
-    source = _operand(t, 0) if _what(t) == "cast" else t
-    xv = g.value(source)
-    if xv is None or xv.dim() == 0 or not xv.dtype.is_floating_point:
-        return False
-    width = xv.shape[-1]
-    # Forward from t * r: single-user casts and at most one weight row.
-    chain, end, weight = inner + [core], core, None
-    while len(end.users) == 1:
-        nxt = next(iter(end.users))
-        if _what(nxt) == "cast":
-            end = nxt
-        elif weight is None and _pair(nxt, "mul") is not None:
-            a, b = _pair(nxt, "mul")
-            w = b if a is end else a
-            wv = g.value(w)
-            if wv is None or tuple(wv.shape) != (width,) or not wv.dtype.is_floating_point:
-                break
-            end, weight = nxt, w
-        else:
-            break
-        chain.append(end)
-    ev = g.value(end)
-    if ev is None or tuple(ev.shape) != tuple(xv.shape) or ev.requires_grad:
-        return False
-    # ktt::rms_norm returns its input's dtype: read the source, or the cast the chain
-    # starts from when that one has the result's dtype.
-    if ev.dtype != xv.dtype:
-        tv = g.value(t)
-        if t is source or tv is None or tv.dtype != ev.dtype:
-            return False
-        source = t
-    elif t is not source:
-        chain.append(t)  # the cast goes with the chain when nothing else reads it
-    first = min(g.order[n] for n in chain)
-    last = g.order[end]
-    guarded = {source} | ({weight} if isinstance(weight, torch.fx.Node) else set())
-    if any(_writes(n, guarded) for n in g.gm.graph.nodes if first <= g.order[n] <= last):
-        return False
-    graph = g.gm.graph
-    with graph.inserting_before(end):
-        fused = graph.call_function(torch.ops.ktt.rms_norm.default, (source, weight, None, eps))
-    fused.meta = dict(end.meta)
-    end.replace_all_uses_with(fused)
-    for n in sorted(set(chain), key=lambda n: -g.order[n]):
-        if not n.users:
-            graph.erase_node(n)
-    return True
+    def region(self, root: torch.fx.Node, stops: set):
+        """Nodes that root depends on short of `stops`, when they form a closed region of
+        vocabulary nodes with no in-place write to a stop inside its span; else None."""
+        inside, todo = set(), [root]
+        while todo:
+            n = todo.pop()
+            if n in inside or n in stops:
+                continue
+            k = self.kind(n)
+            if k is None:
+                return None
+            inside.add(n)
+            todo.extend(a for a in n.all_input_nodes)
+        if any(u not in inside for n in inside if n is not root for u in n.users):
+            return None
+        first = min(self.pos[n] for n in inside)
+        last = self.pos[root]
+        guarded = {s for s in stops if isinstance(s, torch.fx.Node)}
+        for n in self.gm.graph.nodes:
+            if first <= self.pos[n] <= last and _mutates(n) and guarded & set(n.all_input_nodes):
+                return None
+        return inside
 
 
 def rewrite_rms_norms(gm: torch.fx.GraphModule) -> int:
-    """Rewrites every RMSNorm chain of `gm` into ``ktt::rms_norm`` (when ``KTT_FUSE_CHAINS``
-    selects ``norm``); returns how many, recompiling `gm` when any."""
+    """Replaces every RMSNorm product of `gm` by one ``ktt::rms_norm`` call (when
+    ``KTT_FUSE_CHAINS`` selects ``norm``); returns how many, recompiling `gm` when any."""
     if "norm" not in selected():
         return 0
-    done = 0
-    for r in [n for n in gm.graph.nodes if _what(n) == "rsqrt"]:
-        if r.graph is gm.graph and _rewrite_one(_Graph(gm), r):
-            done += 1
+    graph, done, gone = gm.graph, 0, set()
+    for root in reversed(list(graph.nodes)):
+        if root in gone or _term(root) is None or _term(root)[0] not in ("mul", "cast"):
+            continue
+        found = _Region(gm).match(root)
+        if found is None:
+            continue
+        x, w, eps, region = found
+        with graph.inserting_before(root):
+            fused = graph.call_function(torch.ops.ktt.rms_norm.default, (x, w, None, eps))
+        fused.meta = dict(root.meta)
+        root.replace_all_uses_with(fused)
+        order = {n: i for i, n in enumerate(graph.nodes)}
+        for n in sorted(region, key=order.__getitem__, reverse=True):
+            graph.erase_node(n)
+            gone.add(n)
+        done += 1
     if done:
-        gm.graph.lint()
+        graph.lint()
         gm.recompile()
     return done
 

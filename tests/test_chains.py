@@ -141,8 +141,75 @@ def test_env_selects_the_rewrites(monkeypatch):
     monkeypatch.setenv("KTT_FUSE_CHAINS", "all")
     assert chains.selected() == set(chains.REWRITES)
     monkeypatch.setenv("KTT_FUSE_CHAINS", "norm,fuse")
-    with pytest.raises(ValueError, match="unknown fuse"):
+    with pytest.raises(ValueError, match="unknown rewrite.*fuse"):
         chains.selected()
+
+
+@pytest.mark.parametrize("order", ["xw_r", "w_xr", "r_wx", "cast_r"])
+def test_factor_order_and_nesting_do_not_matter(order):
+    """The product is matched as a factor set: any nesting of x, the statistic and the
+    weight is one call, and a cast on the statistic factor is peeled."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(6, 48, generator=g)
+    w = torch.randn(48, generator=g)
+
+    def f(x, w):
+        r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+        if order == "xw_r":
+            return (x * w) * r
+        if order == "w_xr":
+            return w * (x * r)
+        if order == "r_wx":
+            return r * (w * x)
+        return x * r.to(torch.float32) * w
+
+    y, n, code = _compile(f, x, w)
+    assert n == 1 and code.count("ktt.rms_norm") == 1
+    torch.testing.assert_close(y, F.rms_norm(x, [48], w, 1e-5), rtol=1e-5, atol=1e-6)
+
+
+def test_in_place_write_inside_the_region_is_refused():
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(4, 32, generator=g)
+
+    def f(x):
+        r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+        x.mul_(2)
+        return x * r
+
+    y, n, code = _compile(f, x.clone())
+    assert n == 0 and "ktt.rms_norm" not in code
+
+
+@pytest.mark.parametrize("extra", ["weight_twice", "scalar"])
+def test_extra_factors_stay_outside_the_fused_call(extra):
+    """A product with more factors than a norm keeps the extra ones: the largest
+    sub-product that is a norm becomes the call and the rest multiplies its result."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(4, 32, generator=g)
+    w = torch.randn(32, generator=g)
+
+    def f(x, w):
+        r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+        return x * r * w * w if extra == "weight_twice" else x * r * 2.0
+
+    y, n, code = _compile(f, x, w)
+    assert n == 1 and code.count("ktt.rms_norm") == 1
+    ref = F.rms_norm(x, [32], w, 1e-6) * w if extra == "weight_twice" else F.rms_norm(x, [32], None, 1e-6) * 2.0
+    torch.testing.assert_close(y, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_shared_statistic_is_left_alone():
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(4, 32, generator=g)
+    w = torch.randn(32, generator=g)
+
+    def f(x, w):
+        r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+        return x * r * w, r
+
+    y, n, code = _compile(f, x, w)
+    assert n == 0 and "ktt.rms_norm" not in code
 
 
 def test_transformers_qwen2_norm_module():
