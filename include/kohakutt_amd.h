@@ -189,7 +189,10 @@ typedef struct kmi_attn_bwd_args {
     int64_t lse_stride[3];
     double scale;
     /* ABI 3: the forward's mask (as in kmi_attn_args) and varlen offsets (cu_seqlens_q !=
-     * NULL: `batch` packed sequences, seq_q / seq_k the longest lengths). */
+     * NULL: `batch` packed sequences, seq_q / seq_k the longest lengths).  With device
+     * offsets seq_q / seq_k must cover every sequence (the host cannot check them): the
+     * backward sizes its grids and partial sums from them, and gradient rows past them
+     * hold unspecified values. */
     const void* mask;
     int32_t mask_dtype;
     int32_t mask_mode;

@@ -1178,9 +1178,16 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
 // longest of that set, so no pair outlasts the heaviest tile), which keeps the grid within
 // one round of resident workgroups.
 // The 32-row D = 64 unmasked variant (K and V by DMA, no staging registers) is held to
-// four wavefronts per SIMD.
+// four wavefronts per SIMD (128 VGPRs), its row-split form to three (168 VGPRs: at 128 it
+// spilled, and a spill reload between a tile's DMA and its fixed vmcnt wait would release
+// the wait early; the build checks that no DMA variant spills).
+template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH>
+constexpr int fwd_waves_per_simd() {
+    return fwd_dma<T, D, NQB, MK, RS, TWIDTH>() ? (NQB == 2 ? (RS ? 3 : 4) : 2) : 1;
+}
+
 template <typename T, int D, int NQB, int MK, bool RS, int TWIDTH, int NW>
-__global__ __launch_bounds__(NW * kWave, (fwd_dma<T, D, NQB, MK, RS, TWIDTH>() ? (NQB == 2 ? 4 : 2) : 1))
+__global__ __launch_bounds__(NW * kWave, (fwd_waves_per_simd<T, D, NQB, MK, RS, TWIDTH>()))
 void attn_fwd_kernel(const AttnParams p) {
     int lin = blockIdx.x;
     const int units = p.batch * p.hkv;

@@ -91,17 +91,26 @@ struct MaskRaw<MK_F16> {
     typedef uint16_t type;
 };
 
-// A loaded mask element in logit units, clamped at the masked logit.
+// A loaded mask element in logit units, clamped at the masked logit; a NaN entry is a
+// masked key.  NaN is recognised from the bits: the attention kernels are compiled with
+// -fno-honor-nans, under which a floating-point NaN test (or fmaxf's NaN rule) may be
+// folded away.
 template <int MK, typename R>
 __device__ __forceinline__ float mask_logit_of(R raw) {
     if constexpr (MK == MK_BOOL) {
         return raw ? 0.f : kMaskedLogit;
     } else if constexpr (MK == MK_BF16) {
-        return fmaxf(static_cast<float>(__builtin_bit_cast(bf16, raw)), kMaskedLogit);
+        const uint32_t mag = __builtin_bit_cast(uint16_t, raw) & 0x7fffu;
+        const float v = fmaxf(static_cast<float>(__builtin_bit_cast(bf16, raw)), kMaskedLogit);
+        return mag > 0x7f80u ? kMaskedLogit : v;
     } else if constexpr (MK == MK_F16) {
-        return fmaxf(static_cast<float>(__builtin_bit_cast(f16, raw)), kMaskedLogit);
+        const uint32_t mag = __builtin_bit_cast(uint16_t, raw) & 0x7fffu;
+        const float v = fmaxf(static_cast<float>(__builtin_bit_cast(f16, raw)), kMaskedLogit);
+        return mag > 0x7c00u ? kMaskedLogit : v;
     } else {
-        return fmaxf(static_cast<float>(raw), kMaskedLogit);
+        const uint32_t mag = __builtin_bit_cast(uint32_t, raw) & 0x7fffffffu;
+        const float v = fmaxf(static_cast<float>(raw), kMaskedLogit);
+        return mag > 0x7f800000u ? kMaskedLogit : v;
     }
 }
 

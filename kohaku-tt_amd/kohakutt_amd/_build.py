@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import re
 import subprocess
 import sys
 from pathlib import Path
@@ -66,8 +67,56 @@ def _run(cmd):
 
 
 # Per-source extra flags.  The attention kernels never produce NaN from finite inputs
-# (masked logits are -inf or clamped), so max needs no NaN canonicalisation there.
+# (masked logits are -inf or clamped, NaN mask entries are recognised from their bits), so
+# max needs no NaN canonicalisation there.
 SOURCE_FLAGS = {f"attention_d{d}.hip": ["-fno-honor-nans"] for d in (32, 64, 96, 128, 192, 256)}
+# The unit holding the DMA-staged forward kernels also prints the compiler's per-kernel
+# resource usage, which check_dma_spills reads.
+RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
+SOURCE_FLAGS["attention_d64.hip"] = SOURCE_FLAGS["attention_d64.hip"] + [RESOURCE_REMARKS]
+
+# attn_fwd_kernel<T, D, NQB, MK, RS, TWIDTH, NW> as the Itanium ABI mangles it.
+_FWD_KERNEL = re.compile(
+    r"attn_fwd_kernelI(DF16b|DF16_|Dh|f)Li(\d+)ELi(\d+)ELi(\d+)ELb([01])ELi(\d+)ELi(\d+)E"
+)
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs Spill|ScratchSize \[bytes/lane\]): (\S+)")
+
+
+def is_dma_forward(mangled: str) -> bool:
+    """Whether a forward kernel instantiation stages K / V by LDS DMA: the condition of
+    ``fwd_dma`` in ``csrc/attention_kernels.hpp`` (unmasked, 16-bit, padded head dim 64,
+    32-key tiles, 32 rows, or 64 rows without row split)."""
+    m = _FWD_KERNEL.search(mangled)
+    if m is None:
+        return False
+    t, d, nqb, mk, rs, tw = m.group(1), *map(int, m.group(2, 3, 4, 5, 6))
+    return (t != "f" and d == 64 and mk == 0 and tw == 32
+            and (nqb == 2 or (nqb == 4 and rs == 0)))
+
+
+def check_dma_spills(remarks: str) -> int:
+    """Fails when a DMA-staged forward kernel spills VGPRs or uses scratch; returns how many
+    such kernels the remarks list.
+
+    Those kernels wait for their tile loads with a fixed ``s_waitcnt vmcnt(4)``, which
+    counts only the loads the loop issues itself.  A scratch access between a tile's DMA
+    and that wait (a VGPR spill reload) would make the wait release early, a silent race.
+    SGPR spills go to VGPR lanes and issue no memory instruction."""
+    kernels, name = {}, None
+    for key, value in _REMARK.findall(remarks):
+        if key == "Function Name":
+            name = value
+            kernels[name] = {}
+        elif name is not None:
+            kernels[name][key] = int(value)
+    dma = {k: v for k, v in kernels.items() if is_dma_forward(k)}
+    bad = [k for k, v in dma.items() if v.get("VGPRs Spill", 0) or v.get("ScratchSize [bytes/lane]", 0)]
+    if bad:
+        raise RuntimeError(
+            "DMA-staged forward kernels spill VGPRs or use scratch, which breaks their fixed "
+            "vmcnt waits: " + ", ".join(sorted(bad))
+        )
+    return len(dma)
 
 
 def build_capi(jobs: int = 8) -> Path:
@@ -80,7 +129,10 @@ def build_capi(jobs: int = 8) -> Path:
         objs.append(obj)
         cmds.append([str(HIPCC), *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)])
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        list(pool.map(_run, cmds))
+        outs = list(pool.map(_run, cmds))
+    for src, out in zip(HIP_SOURCES, outs):
+        if RESOURCE_REMARKS in SOURCE_FLAGS.get(src, []) and check_dma_spills(out) == 0:
+            raise RuntimeError(f"{src}: no DMA-staged forward kernel in the resource remarks")
     tmp = CAPI_LIB.with_suffix(".so.tmp")
     _run([str(HIPCC), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, CAPI_LIB)

@@ -224,12 +224,22 @@ def _offsets_setup(ctx, inputs, output):
     ctx.args = (max_q, max_k, causal, scale)
 
 
+def _narrowed_backward(grad, q, k, v, out, *rest):
+    """The varlen backward kernels on (grad, q, k, v, out).  fp32 operands -- the forward
+    casts them to bf16 and returns fp32 -- run on bf16 copies, and the gradients come
+    back in fp32."""
+    wide = q.dtype == torch.float32
+    if wide:
+        grad, q, k, v, out = (t.to(torch.bfloat16) for t in (grad, q, k, v, out))
+    grads = torch.ops.ktt._sdpa_varlen_offsets_backward(grad.contiguous(), q, k, v, out, *rest)
+    return tuple(g.float() for g in grads) if wide else tuple(grads)
+
+
 def _offsets_backward(ctx, grad, _grad_lse):
     q, k, v, out, lse, cu_q, cu_k, key_mask, packed_mask = ctx.saved_tensors
     max_q, max_k, causal, scale = ctx.args
-    dq, dk, dv = torch.ops.ktt._sdpa_varlen_offsets_backward(
-        grad.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k, causal, scale,
-        key_mask, packed_mask,
+    dq, dk, dv = _narrowed_backward(
+        grad, q, k, v, out, lse, cu_q, cu_k, max_q, max_k, causal, scale, key_mask, packed_mask,
     )
     return dq, dk, dv, None, None, None, None, None, None, None, None
 
@@ -269,8 +279,8 @@ def _varlen_attn_backward_gpu(grad_out, query, key, value, out, lse, cu_seq_q, c
                               max_q, max_k, is_causal, rng_state):
     """torch_attn::_varlen_attn_backward on GPU tensors: (dq, dk, dv) from the forward's
     output and lse (``torch_backend/varlen.py:117-160``)."""
-    return torch.ops.ktt._sdpa_varlen_offsets_backward(
-        grad_out.contiguous(), query, key, value, out, lse, cu_seq_q, cu_seq_k,
+    return _narrowed_backward(
+        grad_out, query, key, value, out, lse, cu_seq_q, cu_seq_k,
         int(max_q), int(max_k), bool(is_causal), None, None, None,
     )
 

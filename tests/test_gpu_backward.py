@@ -228,6 +228,31 @@ def test_varlen_backward_matches_float64_autograd(native, dev, kind):
         assert err <= 3e-2 * max(want.abs().max().item(), 1.0), (kind, name, err)
 
 
+def test_varlen_fp32_inputs_give_fp32_gradients(native, dev):
+    """fp32 q / k / v that require gradients: the forward casts to bf16 and returns fp32,
+    the backward runs the bf16 kernels on bf16 copies and returns fp32 gradients, within
+    bf16 accuracy of float64 autograd."""
+    g = C.gen(977)
+    hq, hk, d = 4, 2, 64
+    lq = [50, 17, 90]
+    cu = [0] + list(torch.tensor(lq).cumsum(0).tolist())
+    q, go = torch.randn(cu[-1], hq, d, generator=g), torch.randn(cu[-1], hq, d, generator=g)
+    k, v = torch.randn(cu[-1], hk, d, generator=g), torch.randn(cu[-1], hk, d, generator=g)
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    native.reset_counters()
+    out = native.sdpa_varlen(qd, kd, vd, cu, cu, is_causal=True)
+    assert out.dtype == torch.float32
+    out.backward(go.to(dev))
+    torch.cuda.synchronize()
+    assert native.counters()["attention_backward"] == 1, native.counters()
+    # The kernels see bf16 operands: compare with float64 autograd of those.
+    ref = _varlen_ref_grads(*(t.bfloat16() for t in (q, k, v, go)), cu, cu, True)
+    for name, got, want in zip(("dq", "dk", "dv"), (qd.grad, kd.grad, vd.grad), ref):
+        assert got.dtype == torch.float32, name
+        err = (got.cpu().double() - want).abs().max().item()
+        assert err <= 3e-2 * max(want.abs().max().item(), 1.0), (name, err)
+
+
 def test_reference_varlen_ops_forward_and_backward(native, dev):
     """The reference's packed ops as its glue calls them (``torch_backend/varlen.py``):
     ``_varlen_plan`` on the host, ``_sdpa_varlen(..., stats=True, key_mask)`` and

@@ -228,6 +228,45 @@ def test_layer_norm_backward_kernel(native, dev, shape, x_dtype, w_dtype, has_bi
     assert all(torch.equal(a, b2) for a, b2 in zip(got, again))
 
 
+@pytest.mark.parametrize("case", ["x_offset_1", "weight_slice_bf16", "weight_slice_f32"])
+def test_layer_norm_backward_misaligned_operands(native, dev, case):
+    """A contiguous x at storage offset 1 and a weight sliced at offset 4 from a flat
+    parameter buffer are valid LayerNorm inputs: the forward takes them and the backward
+    (whose one-pass kernel needs 16-byte vectors) hands them to torch's kernel; the
+    gradients match float64 autograd under the ruler."""
+    from oracle.ruler import diff_stats
+
+    print(f"LN backward misaligned {case}", flush=True)
+    g = torch.Generator().manual_seed(43)
+    rows, width = 37, 256
+    wdt = torch.float32 if case == "weight_slice_f32" else torch.bfloat16
+    xs = torch.randn(rows * width + 1, generator=g).bfloat16()
+    ws = (1 + 0.1 * torch.randn(width + 4, generator=g)).to(wdt)
+    b = (0.1 * torch.randn(width, generator=g)).to(wdt)
+    gy = torch.randn(rows, width, generator=g).bfloat16()
+    x_off = 1 if case == "x_offset_1" else 0
+    w_off = 4 if case != "x_offset_1" else 0
+
+    def run(device, dtype=None):
+        cast = (lambda t: t.to(dtype)) if dtype is not None else (lambda t: t)
+        xbuf = cast(xs).to(device).detach().clone().requires_grad_()
+        wbuf = cast(ws).to(device).detach().clone().requires_grad_()
+        bb = cast(b).to(device).detach().clone().requires_grad_()
+        x = xbuf[x_off:x_off + rows * width].view(rows, width)
+        w = wbuf[w_off:w_off + width]
+        F.layer_norm(x, (width,), w, bb, 1e-5).backward(cast(gy).to(device))
+        return (xbuf.grad[x_off:x_off + rows * width].view(rows, width), wbuf.grad[w_off:w_off + width], bb.grad)
+
+    native.reset_counters()
+    got = run(dev)
+    torch.cuda.synchronize()
+    assert native.counters()["norms"] == 1, native.counters()
+    ref, cpu = run("cpu", torch.float64), run("cpu")
+    for name, a, c, r in zip(("dx", "dw", "db"), got, cpu, ref):
+        sg, sc = diff_stats(a.cpu(), r), diff_stats(c, r)
+        assert sg["nonfinite"] == 0 and sg["rel_median"] <= 1.5 * sc["rel_median"] + 1e-7, (name, sg, sc)
+
+
 def test_layer_norm_backward_wide_rows_keep_torch_kernel(native, dev):
     """Rows past 256 vectors take torch's own CUDA backward (fed this build's statistics)."""
     x = torch.randn(4, 4096, device=dev, dtype=torch.bfloat16, requires_grad=True)
