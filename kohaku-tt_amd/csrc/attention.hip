@@ -61,6 +61,15 @@ int nqb_override() {
     return v;
 }
 
+// KMI_ATTN_PIPE=0 (read once) keeps head-dim-64 prefill calls on attn_fwd_kernel.
+bool pipe_enabled() {
+    static const bool v = [] {
+        const char* e = std::getenv("KMI_ATTN_PIPE");
+        return !(e && std::atoi(e) == 0);
+    }();
+    return v;
+}
+
 // KMI_ATTN_SPLITS=n (read once) pins the split-KV count of calls the plan would split.
 int splits_override() {
     static const int v = [] {
@@ -143,6 +152,15 @@ Plan make_plan(const kmi_attn_args* a) {
             pl.nx = static_cast<int>(nx_rs);
         }
     }
+    // Causal head-dim-64 unmasked dense prefill with 16-byte output rows: the kernel of
+    // attention_pipe.hip (non-causal calls keep 64-row tiles, which read K/V from L2 half
+    // as often per row).
+    bool out16 = reinterpret_cast<uintptr_t>(a->out) % 16 == 0;
+    for (int i = 0; i < 3; ++i) out16 = out16 && a->o_stride[i] % 8 == 0;
+    // Its buffer resources span a unit's keys with 32-bit offsets.
+    const bool span32 = a->seq_k * std::max<int64_t>({a->k_stride[2], a->v_stride[2], 64}) * 2 < (int64_t{1} << 31);
+    pl.pipe = a->causal && !pl.decode && !pl.rs && pl.splits == 1 && a->mask_mode == KMI_MASK_NONE && !a->cu_seqlens_q &&
+              !a->key_lengths && a->head_dim == 64 && out16 && span32 && pipe_enabled();
     pl.rows_total = a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q;
     pl.ws_bytes = 0;
     return pl;
@@ -151,6 +169,7 @@ Plan make_plan(const kmi_attn_args* a) {
 // Split partials are indexed by query row: b * Sq + i (dense) or the packed token (varlen).
 template <typename T>
 hipError_t launch_dim(const AttnParams& p, const Plan& pl, hipStream_t s) {
+    if (pl.pipe) return launch_pipe<T>(p, s);
     switch (padded_head_dim(p.d)) {
         case 32: return launch_all<T, 32>(p, pl, s);
         case 64: return launch_all<T, 64>(p, pl, s);

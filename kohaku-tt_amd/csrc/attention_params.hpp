@@ -83,12 +83,16 @@ struct AttnParams {
     FastDiv fd_splits, fd_units, fd_hkv, fd_group, fd_snake;
     int total_q, total_k;  // varlen packed token counts
     int64_t rows_total;
+    // attn_pipe_kernel with eight wavefronts: the heaviest grp_single query tiles run
+    // alone, the next 2 grp_pair in pairs (attention_pipe.hip).
+    int grp_single, grp_pair;
 };
 
 struct Plan {
     bool decode;  // attn_decode_kernel: per-wavefront key ranges, fp32 partials + merge
     bool rs;      // row split: short key ranges, one row block per wavefront
     bool rs_shared;  // row split with the unit's key tiles (at most four) staged in LDS once
+    bool pipe;       // attn_pipe_kernel: head dim 64, unmasked, dense, one split (attention_pipe.hip)
     int nqb, nx, splits, tiles_per_split;
     int64_t rows_total;
     size_t ws_bytes;
@@ -101,6 +105,10 @@ int cu_count();
 // (explicit instantiations in attention_d<D>.hip).
 template <typename T, int D>
 hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream);
+
+// Enqueues attn_pipe_kernel for a call the plan gave it (instantiated in attention_pipe.hip).
+template <typename T>
+hipError_t launch_pipe(const AttnParams& p, hipStream_t stream);
 
 }  // namespace fwd
 }  // namespace kmi

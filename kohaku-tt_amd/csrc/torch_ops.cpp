@@ -1079,18 +1079,17 @@ std::tuple<Tensor, Tensor, Tensor> native_layer_norm_backward(const Tensor& grad
         return at::cuda::native_layer_norm_backward(grad_out, input, normalized_shape, mean, rstd, weight, bias,
                                                     output_mask);
     c10::DeviceGuard guard(input.device());
-    const Tensor x = input.contiguous(), gy = grad_out.contiguous();
-    const Tensor w = hw ? weight->contiguous() : Tensor();
     // The one-pass kernel reads whole 16-byte vectors of x and dy and the matching run of
-    // weight elements: a contiguous view at an odd storage offset, or a weight sliced from
-    // a flat parameter buffer, goes to torch's kernel instead.
-    const auto at_multiple = [](const Tensor& t, int64_t bytes) {
-        return reinterpret_cast<uintptr_t>(t.data_ptr()) % static_cast<uintptr_t>(bytes) == 0;
+    // weight elements.  A contiguous view at an odd storage offset, or a weight sliced
+    // from a flat parameter buffer, is copied once into a fresh (aligned) allocation;
+    // torch's own kernel is no fallback here, as it refuses an fp32 weight on bf16 rows.
+    const auto aligned_to = [](const Tensor& t, int64_t bytes) {
+        const Tensor c = t.contiguous();
+        if (reinterpret_cast<uintptr_t>(c.data_ptr()) % static_cast<uintptr_t>(bytes) == 0) return c;
+        return c.clone(at::MemoryFormat::Contiguous);
     };
-    if (!at_multiple(x, 16) || !at_multiple(gy, 16) ||
-        (hw && !at_multiple(w, (16 / xs) * static_cast<int64_t>(c10::elementSize(wt)))))
-        return at::cuda::native_layer_norm_backward(grad_out, input, normalized_shape, mean, rstd, weight, bias,
-                                                    output_mask);
+    const Tensor x = aligned_to(input, 16), gy = aligned_to(grad_out, 16);
+    const Tensor w = hw ? aligned_to(*weight, (16 / xs) * static_cast<int64_t>(c10::elementSize(wt))) : Tensor();
     const Tensor m = mean.contiguous(), r = rstd.contiguous();
     const int64_t rows = x.numel() / width;
     Tensor dx = at::empty_like(x);

@@ -36,6 +36,7 @@ HIP_SOURCES = [
     "norm.hip",
     "attention.hip",
     *[f"attention_d{d}.hip" for d in (32, 64, 96, 128, 192, 256)],
+    "attention_pipe.hip",
     "attention_bwd.hip",
 ]
 HIP_FLAGS = [
@@ -69,7 +70,7 @@ def _run(cmd):
 # Per-source extra flags.  The attention kernels never produce NaN from finite inputs
 # (masked logits are -inf or clamped, NaN mask entries are recognised from their bits), so
 # max needs no NaN canonicalisation there.
-SOURCE_FLAGS = {f"attention_d{d}.hip": ["-fno-honor-nans"] for d in (32, 64, 96, 128, 192, 256)}
+SOURCE_FLAGS = {f"attention_d{d}.hip": ["-fno-honor-nans"] for d in (32, 64, 96, 128, 192, 256, "_pipe")}
 # The unit holding the DMA-staged forward kernels also prints the compiler's per-kernel
 # resource usage, which check_dma_spills reads.
 RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"

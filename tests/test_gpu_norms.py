@@ -232,8 +232,8 @@ def test_layer_norm_backward_kernel(native, dev, shape, x_dtype, w_dtype, has_bi
 def test_layer_norm_backward_misaligned_operands(native, dev, case):
     """A contiguous x at storage offset 1 and a weight sliced at offset 4 from a flat
     parameter buffer are valid LayerNorm inputs: the forward takes them and the backward
-    (whose one-pass kernel needs 16-byte vectors) hands them to torch's kernel; the
-    gradients match float64 autograd under the ruler."""
+    (whose one-pass kernel needs 16-byte vectors) copies the misaligned operand once and
+    runs the kernel; the gradients match float64 autograd under the ruler."""
     from oracle.ruler import diff_stats
 
     print(f"LN backward misaligned {case}", flush=True)
@@ -260,7 +260,8 @@ def test_layer_norm_backward_misaligned_operands(native, dev, case):
     native.reset_counters()
     got = run(dev)
     torch.cuda.synchronize()
-    assert native.counters()["norms"] == 1, native.counters()
+    c = native.counters()
+    assert c["norms"] == 1 and c["norms_backward"] == 1, c
     ref, cpu = run("cpu", torch.float64), run("cpu")
     for name, a, c, r in zip(("dx", "dw", "db"), got, cpu, ref):
         sg, sc = diff_stats(a.cpu(), r), diff_stats(c, r)
