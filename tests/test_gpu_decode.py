@@ -85,11 +85,24 @@ def test_decode_matches_oracle(native, dev, name, dtype):
     assert native.counters()["attention"] == 1
     m64 = None if mask is None else (mask.numpy() if mask.dtype == torch.bool else C.f64(mask))
     ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), m64)
-    err = np.abs(out.cpu().double().numpy() - ref)
-    # Outputs are convex combinations of N(0, 1) values: bf16 / fp16 rounding of the
-    # probabilities and the output bounds the error well below 2e-2.
-    assert err.max() < 2e-2, (name, err.max())
-    assert err.mean() < 2e-3, (name, err.mean())
+    out = out.cpu()
+    # Rows that keep a key: the ruler against torch CPU at the same dtype (1.5x its median
+    # relative error against float64).  Rows whose every key is masked follow the
+    # reference (softmax over the raw scores) where torch CPU returns zeros, so they are
+    # compared with the oracle alone.
+    if m64 is None:
+        kept = np.ones(out.shape[:-1], dtype=bool)
+    else:
+        keeps = m64 if m64.dtype == np.bool_ else m64 > -5e5
+        kept = np.broadcast_to(keeps.any(-1), out.shape[:-1])
+    cpu = C.torch_cpu_sdpa(q, k, v, mask)
+    sel = torch.from_numpy(np.ascontiguousarray(kept))
+    ok, sg, sc = C.ruler_ok(out[sel], cpu[sel], torch.from_numpy(np.ascontiguousarray(ref[kept])))
+    print(f"  kept rows: gpu rel_median {sg['rel_median']:.3e} cpu {sc['rel_median']:.3e}", flush=True)
+    assert ok, (name, sg, sc)
+    if (~kept).any():
+        err = np.abs(out.double().numpy()[~kept] - ref[~kept])
+        assert err.max() < 2e-2, (name, err.max())
 
 
 @pytest.mark.parametrize("nseq,hk", [(8, 2), (600, 1)])
