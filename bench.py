@@ -118,7 +118,8 @@ def build_rows():
                 kk, vv = k.repeat_interleave(hq // k.size(1), 1), v.repeat_interleave(hq // k.size(1), 1)
             return lambda: F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask, is_causal=causal)
 
-        rows[name] = Row(name, label, bound, flops, nbytes, (make, cpu), "attn_fwd_kernel", "attention")
+        kernel = "attn_pipe_kernel" if causal and mask is None and d == 64 and sq > 16 else "attn_fwd_kernel"
+        rows[name] = Row(name, label, bound, flops, nbytes, (make, cpu), kernel, "attention")
 
     def norm_row(name, label, x, w, b, eps, kind):
         rows_, width = x.numel() // x.size(-1), x.size(-1)
@@ -561,7 +562,7 @@ def main():
             "frac": round(achieved / PEAK_TFLOPS, 4),
             "traffic": traffic_for("c1_attn"),
             "mfma_busy_profiled": (counters_for("c1_attn") or {}).get("mfma_busy_frac"),
-            "kernel": "attn_fwd_kernel<bf16,64,*>",
+            "kernel": "attn_pipe_kernel<bf16,causal,4 wavefronts,plain step>",
             "kernel_ms": head["ms_per_call"],
             "kernel_ms_eager_event_pairs": head["kernel_ms"],
         },
