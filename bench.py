@@ -118,7 +118,12 @@ def build_rows():
                 kk, vv = k.repeat_interleave(hq // k.size(1), 1), v.repeat_interleave(hq // k.size(1), 1)
             return lambda: F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask, is_causal=causal)
 
-        kernel = "attn_pipe_kernel" if causal and mask is None and d == 64 and sq > 16 else "attn_fwd_kernel"
+        if sq * (hq // k.size(1)) <= 16:
+            kernel = "attn_decode_kernel"
+        elif causal and mask is None and d == 64:
+            kernel = "attn_pipe_kernel"
+        else:
+            kernel = "attn_fwd_kernel"
         rows[name] = Row(name, label, bound, flops, nbytes, (make, cpu), kernel, "attention")
 
     def norm_row(name, label, x, w, b, eps, kind):

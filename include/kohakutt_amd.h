@@ -131,7 +131,12 @@ typedef struct kmi_attn_args {
 /* Bytes of workspace kmi_attn_fwd needs for `args` (0 when it does not split). */
 int kmi_attn_workspace_bytes(const kmi_attn_args* args, size_t* bytes);
 
-/* Enqueues the attention forward of `args` on `stream` (hipStream_t). */
+/*
+ * Enqueues the attention forward of `args` on `stream` (hipStream_t).  Split decode calls
+ * merge their splits in the same launch through a library-owned counter array (one slab
+ * per stream for the first 16 streams of a device; other streams merge in a second launch
+ * with the same arithmetic).
+ */
 int kmi_attn_fwd(const kmi_attn_args* args, void* workspace, size_t workspace_bytes,
                  void* stream);
 

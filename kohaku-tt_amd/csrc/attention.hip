@@ -70,6 +70,15 @@ bool pipe_enabled() {
     return v;
 }
 
+// KMI_ATTN_DECODE_FUSED=0 (read once) merges decode splits in a separate launch.
+bool decode_fused_enabled() {
+    static const bool v = [] {
+        const char* e = std::getenv("KMI_ATTN_DECODE_FUSED");
+        return !(e && std::atoi(e) == 0);
+    }();
+    return v;
+}
+
 // KMI_ATTN_SPLITS=n (read once) pins the split-KV count of calls the plan would split.
 int splits_override() {
     static const int v = [] {
@@ -124,13 +133,15 @@ Plan make_plan(const kmi_attn_args* a) {
     pl.tiles_per_split = static_cast<int>(ceil_div(nk, splits));
     pl.splits = static_cast<int>(ceil_div(nk, pl.tiles_per_split));
     // Decode (at most 16 rows per K/V head): four wavefronts per workgroup deal the key
-    // tiles round-robin and merge in LDS; about two workgroups per CU in all, at most 32
-    // per unit (the merge reads their partials in one round), at least one tile per
-    // wavefront.  One workgroup per unit writes the output directly.
+    // tiles round-robin and merge in LDS; about one workgroup per CU in all, at most 32 per
+    // unit (the split counter's bits), at least one tile per wavefront.  One workgroup per
+    // unit writes the output directly.  (Fewer, longer splits: each split costs the merge a
+    // partial and each workgroup a fixed start-up; C3 at 16 splits and the 128-unit sweep at
+    // 2 ran faster than at 32 and 4.)
     pl.decode = vrows <= 16 && a->num_splits != 1;
     if (pl.decode) {
         const int64_t most = std::max<int64_t>(1, ceil_div(nk, NWAVES));
-        int64_t wgs = std::min<int64_t>({ceil_div(512, units), int64_t{32}, most});
+        int64_t wgs = std::min<int64_t>({ceil_div(256, units), int64_t{32}, most});
         if (a->num_splits > 1) wgs = std::min<int64_t>(a->num_splits, most);
         if (splits_override() > 0) wgs = std::min<int64_t>(splits_override(), most);
         pl.splits = static_cast<int>(wgs);
@@ -255,6 +266,8 @@ int enqueue(const kmi_attn_args* a, const Plan& pl, void* workspace, void* strea
         p.part_lse = p.part_o + static_cast<size_t>(pl.splits) * p.rows_total * p.hq * padded_head_dim(a->head_dim);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (pl.decode && pl.splits > 1 && pl.splits <= 32)
+        p.ctr = decode_counters(s, static_cast<int64_t>(p.batch) * p.hkv);
     const hipError_t err = a->dtype == KMI_BF16 ? launch_dim<bf16>(p, pl, s) : launch_dim<f16>(p, pl, s);
     return hip_status(err, name);
 }
@@ -280,6 +293,37 @@ void* scratch_on_current_device() {
         addr[dev] = ptr;
     }
     return addr[dev];
+}
+
+// Decode split counters: kCtrSlabs slabs of kCtrUnits 64-bit words, zero from the load of
+// the code object on and left zero by every merge (the last workgroup of a unit clears its
+// word).  A slab belongs to one stream for the life of the process, so calls on one
+// stream (which run in order) share it and calls on different streams never do; a stream
+// beyond the slab count, or a call over more units, merges in a separate launch instead
+// (the same arithmetic, so the results do not depend on which).
+constexpr int kCtrSlabs = 16;
+constexpr int kCtrUnits = 4096;
+static __device__ __align__(256) unsigned long long decode_ctr[kCtrSlabs * kCtrUnits];
+
+unsigned long long* decode_counters(hipStream_t stream, int64_t units) {
+    if (units > kCtrUnits || !decode_fused_enabled()) return nullptr;
+    static std::mutex mu;
+    static unsigned long long* base[64] = {};
+    static hipStream_t owner[64][kCtrSlabs] = {};
+    static int used[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!base[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(decode_ctr)) != hipSuccess) return nullptr;
+        base[dev] = static_cast<unsigned long long*>(ptr);
+    }
+    for (int i = 0; i < used[dev]; ++i)
+        if (owner[dev][i] == stream) return base[dev] + static_cast<size_t>(i) * kCtrUnits;
+    if (used[dev] == kCtrSlabs) return nullptr;
+    owner[dev][used[dev]] = stream;
+    return base[dev] + static_cast<size_t>(used[dev]++) * kCtrUnits;
 }
 
 }  // namespace fwd

@@ -1250,6 +1250,147 @@ void attn_fwd_kernel(const AttnParams p) {
     attn_block<T, D, NQB, MK, RS, TWIDTH, NW>(p, split, bh, j);
 }
 
+// A decode unit's query side: sequence, K/V head, first query position and count, the
+// row of its split partials, and its virtual rows (Sq x G, at most 16).
+struct DecodeRows {
+    int seq, kvh, q0, lq, vrows;
+    int64_t row_base;
+};
+
+__device__ __forceinline__ DecodeRows decode_rows(const AttnParams& p, const int bh) {
+    DecodeRows u;
+    u.seq = fdiv(bh, p.fd_hkv);
+    u.kvh = bh - u.seq * p.hkv;
+    u.q0 = 0;
+    u.lq = p.seq_q;
+    u.row_base = static_cast<int64_t>(u.seq) * p.seq_q;
+    if (p.cu_q) {
+        u.q0 = min(max(p.cu_q[u.seq], 0), p.total_q);
+        u.lq = min(min(max(p.cu_q[u.seq + 1], u.q0), p.total_q) - u.q0, p.seq_q);
+        u.row_base = u.q0;
+    }
+    u.vrows = min(u.lq * p.group, 16);
+    return u;
+}
+
+// Decode partials go through device-scope accesses: the stores write through to the level
+// that every XCD reads and the loads read from it (past the reader's own L2), so a
+// workgroup's partials are visible to the one that merges them with no L2-wide writeback
+// or invalidate (an agent-scope fence costs one of each; with thousands of wavefronts
+// they serialise into tens of microseconds).  The order: each wavefront waits for its
+// stores (vmcnt(0)) before the workgroup barrier, the barrier precedes the count, and the
+// merging workgroup loads only after its count returned the final value.
+__device__ __forceinline__ void store_dev(float* p, f32x2 v) {
+    __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ f32x2 load_dev(const float* p) {
+    return __builtin_bit_cast(f32x2, __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float*>(p)),
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// Merge of a decode unit's split partials, in split order (deterministic).  Two running
+// merges per row: the splits that met a kept key (masked mode) and the raw-score ones;
+// a row that met a kept key in some split takes the first, a fully masked row the second
+// (the reference's raw-score result for such rows).  Splits whose partial carries no
+// weight for a row add nothing to it, so `live` (bit s: split s carries weight for some
+// row) only saves the loads of the others.  Thread t of the workgroup takes columns
+// 4 (t % (D / 4)) .. + 3 of virtual row t / (D / 4), then the next 256 (row, columns)
+// items.  Reference: the split-KV combine of the decode path (device_attention.cpp:836-907).
+template <typename T, int D>
+__device__ __forceinline__ void decode_merge_unit(const AttnParams& p, const int bh, const uint32_t live) {
+    constexpr int C4 = D / 4;
+    constexpr int CH = 16;  // splits per round of loads
+    const DecodeRows u = decode_rows(p, bh);
+    const int items = u.vrows * C4;
+    const int64_t split_rows = p.rows_total * p.hq;
+    // Splits that are not live load the first live split's record (no per-split branch;
+    // their weight is zero).
+    const int s_any = live ? __builtin_ctz(live) : 0;
+    for (int item = threadIdx.x; item < items; item += NTHREADS) {
+        const int rr = item / C4;
+        const int c = 4 * (item - rr * C4);
+        const int pos = fdiv(rr, p.fd_group);
+        const int head = u.kvh * p.group + (rr - pos * p.group);
+        const int64_t row0 = (u.row_base + pos) * p.hq + head;
+        float mk = -INFINITY, sk = 0.f, mr = -INFINITY, sr = 0.f;
+        f32x4 ak = f32x4{0.f, 0.f, 0.f, 0.f}, ar = ak;
+        for (int s0 = 0; s0 < p.splits; s0 += CH) {
+            f32x2 e[CH];
+            f32x4 v[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int s = s0 + j;
+                const bool use = s < p.splits && ((live >> s) & 1u);
+                const int64_t prow = static_cast<int64_t>(use ? s : s_any) * split_rows + row0;
+                e[j] = load_dev(p.part_lse + 2 * prow);
+                const f32x2 lo = load_dev(p.part_o + prow * D + c), hi = load_dev(p.part_o + prow * D + c + 2);
+                v[j] = f32x4{lo[0], lo[1], hi[0], hi[1]};
+                if (!use) e[j] = f32x2{-INFINITY, 0.f};
+            }
+            float ck = mk, cr = mr;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                if (e[j][1] == 0.f) ck = fmaxf(ck, e[j][0]);
+                else cr = fmaxf(cr, e[j][0]);
+            }
+            // Rescale what the earlier rounds added (exactly 0 while nothing was).
+            const float fk = ck == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mk - ck);
+            const float fr = cr == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mr - cr);
+            sk *= fk;
+            ak *= fk;
+            sr *= fr;
+            ar *= fr;
+            mk = ck;
+            mr = cr;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const bool raw = e[j][1] != 0.f;
+                const float m = raw ? mr : mk;
+                const float w = e[j][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[j][0] - m);
+                if (w != 0.f) {
+                    if (raw) {
+                        sr += w;
+                        ar += w * v[j];
+                    } else {
+                        sk += w;
+                        ak += w * v[j];
+                    }
+                }
+            }
+        }
+        const bool masked = sk > 0.f;
+        const float m = masked ? mk : mr, l = masked ? sk : sr;
+        const f32x4 a = masked ? ak : ar;
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        if (c < p.d) {
+            const int64_t ob_off = p.cu_q ? 0 : u.seq * p.os[0];
+            T* out = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(u.q0 + pos) * p.os[2] + c;
+            typedef __attribute__((__vector_size__(2 * sizeof(T)))) T t2;
+            t2 w0, w1;
+            w0[0] = static_cast<T>(a[0] * inv);
+            w0[1] = static_cast<T>(a[1] * inv);
+            w1[0] = static_cast<T>(a[2] * inv);
+            w1[1] = static_cast<T>(a[3] * inv);
+            *reinterpret_cast<t2*>(out) = w0;
+            *reinterpret_cast<t2*>(out + 2) = w1;
+        }
+        if (p.lse && c == 0) {
+            const int64_t lb_off = p.cu_q ? 0 : u.seq * p.ls[0];
+            p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(u.q0 + pos) * p.ls[2]] =
+                l > 0.f ? (m + log2f(l)) * kLn2 + (masked ? 0.f : kMaskedLogit) : -INFINITY;
+        }
+    }
+}
+
+// The merge of decode_merge_unit as a launch of its own (one workgroup per unit), for
+// calls without split counters.
+template <typename T, int D>
+__global__ __launch_bounds__(NTHREADS) void attn_decode_merge_kernel(const AttnParams p) {
+    decode_merge_unit<T, D>(p, blockIdx.x, 0xffffffffu);
+}
+
 // Decode: at most 16 "virtual rows" (Sq x G) per (sequence, K/V head).  The key tiles of a
 // unit are dealt round-robin to its wavefronts (wavefront slot s of S takes tiles s, s + S,
 // ...): K goes straight from global memory into MFMA A-operand registers, V through a
@@ -1257,8 +1398,9 @@ void attn_fwd_kernel(const AttnParams p) {
 // softmax.  With a mask shared by the rows (a padding mask), tiles whose keys are all
 // masked are skipped once a kept key among the first 64 proves that no row is fully
 // masked (their keys then carry exactly zero weight).  The four wavefronts of a workgroup
-// merge their (m, l, O) in LDS and write one fp32 partial; attn_merge_kernel combines the
-// workgroups' partials.
+// merge their (m, l, O) in LDS; one workgroup per unit writes the output, several write
+// fp32 partials that the last of them to finish merges (split counter), or that
+// attn_decode_merge_kernel merges in a launch of its own.
 template <typename T, int D, int MK>
 __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams p) {
     typedef typename Mfma<T>::v8 v8;
@@ -1291,26 +1433,22 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     // across the whole key range, so every workgroup meets the live keys of a padded row
     // (no workgroup of only masked tiles) and the work spreads evenly.
     const int slot = wave * wg_per_unit + split;
-    const int seq = fdiv(bh, p.fd_hkv);
-    const int kvh = bh - seq * p.hkv;
+    const DecodeRows u = decode_rows(p, bh);
+    const int seq = u.seq, kvh = u.kvh, q0 = u.q0, lq = u.lq, vrows = u.vrows;
+    const int64_t row_base = u.row_base;
     const int G = p.group;
 
-    int q0 = 0, lq = p.seq_q, k0 = 0, lk = p.seq_k;
+    int k0 = 0, lk = p.seq_k;
     int64_t qb_off = seq * p.qs[0], kb_off = seq * p.ks[0], vb_off = seq * p.vs[0];
-    int64_t row_base = static_cast<int64_t>(seq) * p.seq_q;
     if (p.cu_q) {
-        q0 = min(max(p.cu_q[seq], 0), p.total_q);
-        lq = min(max(p.cu_q[seq + 1], q0), p.total_q) - q0;
         k0 = min(max(p.cu_k[seq], 0), p.total_k);
-        lk = min(max(p.cu_k[seq + 1], k0), p.total_k) - k0;
-        lq = min(lq, p.seq_q);
-        lk = min(lk, p.seq_k);
+        lk = min(min(max(p.cu_k[seq + 1], k0), p.total_k) - k0, p.seq_k);
         qb_off = kb_off = vb_off = 0;
-        row_base = q0;
     }
     if (p.klen) lk = min(max(p.klen[seq], 1), p.seq_k);
-    // Uniform over the workgroup: an empty sequence leaves before any barrier.
-    const int vrows = min(lq * G, 16);
+    // Uniform over the workgroup: an empty sequence leaves before any barrier.  (With
+    // split counters every split of such a unit leaves here and none merges: its rows
+    // have no output to write.)
     if (vrows <= 0) return;
     const int coff = p.cu_q ? (lk - lq) : 0;
     int kend = max(lk, 0);
@@ -1352,43 +1490,6 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
         shared_row = (lq == 1 || (!packed && p.ms[2] == 0)) && (G == 1 || packed || p.ms[1] == 0);
     }
 
-    // Tiles this wavefront runs: bit i of `live` stands for tile slot + i * nslots.
-    uint32_t live = 0xffffffffu;
-    const bool use_bits = MASKED && shared_row && n_t > 0 && n_t <= 2 * SCAN;
-    if constexpr (MASKED) {
-        if (use_bits) {
-            const MRaw* mp = static_cast<const MRaw*>(p.mask);
-            const int lim0 = p.causal ? min(lk, coff + 1) : lk;
-            const int pk = lane;
-            const MRaw first = mask_load(mp, mrow, pk < lim0 ? pk : -1, lk, m_key, m_end);
-            MRaw sv[SCAN];
-#pragma unroll
-            for (int j = 0; j < SCAN; ++j) {
-                const int i = 2 * j + (lane >> 5);
-                const int key = (slot + i * nslots) * WN + (lane & 31);
-                sv[j] = mask_load(mp, mrow, i < n_t ? key : -1, lk, m_key, m_end);
-            }
-            const bool proof = __builtin_amdgcn_ballot_w64(pk < lim0 && mask_logit_of<MK>(first) > kMaskedLogit) != 0;
-            if (proof) {
-                live = 0;
-#pragma unroll
-                for (int j = 0; j < SCAN; ++j) {
-                    const int i = 2 * j + (lane >> 5);
-                    const int key = (slot + i * nslots) * WN + (lane & 31);
-                    const uint64_t b = __builtin_amdgcn_ballot_w64(i < n_t && key < lk &&
-                                                                   mask_logit_of<MK>(sv[j]) > kMaskedLogit);
-                    live |= (static_cast<uint32_t>(b) != 0u ? 1u : 0u) << (2 * j);
-                    live |= (static_cast<uint32_t>(b >> 32) != 0u ? 1u : 0u) << (2 * j + 1);
-                }
-            }
-        }
-    }
-    auto next_i = [&](int i) -> int {  // the first tile index after i that runs
-        if (!use_bits) return i + 1;
-        const uint32_t rest = live & (0xfffffffeu << i);
-        return rest ? __builtin_ctz(rest) : n_t;
-    };
-
     // K fragments of a tile come straight from memory: lane (g4, l16) holds key
     // 16 kb + l16, dims 32 c + 8 g4 .. + 7 -- the A operand of S^T = K Q^T.  Both K and V
     // load through one buffer resource per tile that ends at the unit's last key (rows past
@@ -1410,6 +1511,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : p.d * static_cast<int64_t>(sizeof(T)));
     T* vl = reinterpret_cast<T*>(smem) + wave * WN * VP;
 
+    // One tile's registers: K fragments, the V rows this lane stages, the mask values.
     v8 kreg[KB][DC];
     u32x4 vreg[KIT];
     MRaw mpre[MASKED ? KB : 1][4];
@@ -1451,6 +1553,43 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
                 }
             }
         }
+    };
+
+    // Tiles this wavefront runs: bit i of `live` stands for tile slot + i * nslots.
+    uint32_t live = 0xffffffffu;
+    const bool use_bits = MASKED && shared_row && n_t > 0 && n_t <= 2 * SCAN;
+    if constexpr (MASKED) {
+        if (use_bits) {
+            const MRaw* mp = static_cast<const MRaw*>(p.mask);
+            const int lim0 = p.causal ? min(lk, coff + 1) : lk;
+            const int pk = lane;
+            const MRaw first = mask_load(mp, mrow, pk < lim0 ? pk : -1, lk, m_key, m_end);
+            MRaw sv[SCAN];
+#pragma unroll
+            for (int j = 0; j < SCAN; ++j) {
+                const int i = 2 * j + (lane >> 5);
+                const int key = (slot + i * nslots) * WN + (lane & 31);
+                sv[j] = mask_load(mp, mrow, i < n_t ? key : -1, lk, m_key, m_end);
+            }
+            const bool proof = __builtin_amdgcn_ballot_w64(pk < lim0 && mask_logit_of<MK>(first) > kMaskedLogit) != 0;
+            if (proof) {
+                live = 0;
+#pragma unroll
+                for (int j = 0; j < SCAN; ++j) {
+                    const int i = 2 * j + (lane >> 5);
+                    const int key = (slot + i * nslots) * WN + (lane & 31);
+                    const uint64_t b = __builtin_amdgcn_ballot_w64(i < n_t && key < lk &&
+                                                                   mask_logit_of<MK>(sv[j]) > kMaskedLogit);
+                    live |= (static_cast<uint32_t>(b) != 0u ? 1u : 0u) << (2 * j);
+                    live |= (static_cast<uint32_t>(b >> 32) != 0u ? 1u : 0u) << (2 * j + 1);
+                }
+            }
+        }
+    }
+    auto next_i = [&](int i) -> int {  // the first tile index after i that runs
+        if (!use_bits) return i + 1;
+        const uint32_t rest = live & (0xfffffffeu << i);
+        return rest ? __builtin_ctz(rest) : n_t;
     };
 
     f32x4 o[DB];
@@ -1620,11 +1759,9 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
         wt[w] = lw[w] > 0.f ? __builtin_amdgcn_exp2f(mw[w] - M) : 0.f;
         L += wt[w] * lw[w];
     }
-    if (!valid) return;
     // PER (= D / 16, even) columns per lane, in pairs; pairs past the head dim are skipped.
     constexpr int PER = D / 16;
     const int c0 = wave * (D / 4) + g4 * PER;
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
     float acc[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) acc[j] = 0.f;
@@ -1639,6 +1776,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
     if (p.splits == 1) {
+        if (!valid) return;
         // One workgroup per unit: the merged rows are the output.
         const int64_t ob_off = p.cu_q ? 0 : seq * p.os[0];
         T* out = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(q0 + pos) * p.os[2] + c0;
@@ -1657,15 +1795,35 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
         }
         return;
     }
-    const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
-    float* dst = p.part_o + prow * D + c0;
+    if (valid) {
+        const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
+        float* dst = p.part_o + prow * D + c0;
 #pragma unroll
-    for (int j = 0; j < PER; j += 2)
-        if (c0 + j < p.d) *reinterpret_cast<f32x2*>(dst + j) = f32x2{acc[j] * inv, acc[j + 1] * inv};
-    if (wave == 0 && g4 == 0) {
-        p.part_lse[2 * prow] = L > 0.f ? M + log2f(L) : -INFINITY;
-        p.part_lse[2 * prow + 1] = (MASKED && !sel_masked) ? 1.f : 0.f;
+        for (int j = 0; j < PER; j += 2)
+            if (c0 + j < p.d) store_dev(dst + j, f32x2{acc[j] * inv, acc[j + 1] * inv});
+        if (wave == 0 && g4 == 0)
+            store_dev(p.part_lse + 2 * prow,
+                      f32x2{L > 0.f ? M + log2f(L) : -INFINITY, (MASKED && !sel_masked) ? 1.f : 0.f});
     }
+    if (!p.ctr) return;
+    // Split counter: the workgroup that completes the count merges every split's partials
+    // and clears the word for the next call.
+    const bool carries = __builtin_amdgcn_ballot_w64(valid && L > 0.f) != 0;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's partials are stored
+    __syncthreads();  // ... and every wavefront's; the LDS is free
+    uint32_t* flag = reinterpret_cast<uint32_t*>(smem);
+    if (threadIdx.x == 0) {
+        const unsigned long long add = (1ull << 32) | (carries ? 1ull << split : 0ull);
+        const unsigned long long now =
+            __hip_atomic_fetch_add(p.ctr + bh, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+        const bool last = static_cast<int>(now >> 32) == wg_per_unit;
+        if (last) __hip_atomic_store(p.ctr + bh, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        flag[0] = last ? 1u : 0u;
+        flag[1] = static_cast<uint32_t>(now);
+    }
+    __syncthreads();
+    if (!flag[0]) return;
+    decode_merge_unit<T, D>(p, bh, flag[1]);
 }
 
 // Merge of split-KV partials: one wavefront per (query row, head); lanes over splits for
@@ -1924,6 +2082,12 @@ hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream) {
         err = launch_mask<T, D, 1>(p, grid, stream);
     }
     if (err != hipSuccess || pl.splits <= 1) return err;
+    if (pl.decode) {
+        if (p.ctr) return hipSuccess;  // merged by the last workgroup of each unit
+        hipLaunchKernelGGL((attn_decode_merge_kernel<T, D>), dim3(static_cast<unsigned>(p.batch * p.hkv)),
+                           dim3(NTHREADS), 0, stream, p);
+        return hipGetLastError();
+    }
     const int64_t items = p.rows_total * p.hq;
     hipLaunchKernelGGL((attn_merge_kernel<T, D>), dim3(static_cast<unsigned>(ceil_div(items, 4))), dim3(256), 0,
                        stream, p);

@@ -86,6 +86,11 @@ struct AttnParams {
     // attn_pipe_kernel with eight wavefronts: the heaviest grp_single query tiles run
     // alone, the next 2 grp_pair in pairs (attention_pipe.hip).
     int grp_single, grp_pair;
+    // Decode split counters (or null: a separate merge launch): one 64-bit word per
+    // (sequence, K/V head), zero between calls.  Each workgroup adds 2^32 plus bit `split`
+    // when its partial carries weight; the one that brings the count to `splits` merges
+    // the unit's partials and clears the word.
+    unsigned long long* ctr;
 };
 
 struct Plan {
@@ -105,6 +110,12 @@ int cu_count();
 // (explicit instantiations in attention_d<D>.hip).
 template <typename T, int D>
 hipError_t launch_all(const AttnParams& p, const Plan& pl, hipStream_t stream);
+
+// The current device's decode split counters for calls on `stream` (zero-initialised
+// device memory that every merge leaves zero; one slab per stream so that calls on
+// different streams never share a word), or null when a call over `units` units must
+// merge in a separate launch.
+unsigned long long* decode_counters(hipStream_t stream, int64_t units);
 
 // Enqueues attn_pipe_kernel for a call the plan gave it (instantiated in attention_pipe.hip).
 template <typename T>

@@ -177,3 +177,28 @@ def test_decode_split_counts_agree(native, dev):
         assert np.allclose(lse.double().numpy(), ref_lse, rtol=1e-7, atol=2e-2), ns
         again, lse2, _ = _capi_call(qd, kd, vd, md, ns)
         assert torch.equal(again, out) and torch.equal(lse2, lse), ns
+
+
+def test_decode_merge_is_the_same_on_every_stream(native, dev):
+    """The split merge runs inside the decode kernel (the last workgroup of a unit merges,
+    found by a per-stream counter that the merge clears) on up to 16 streams and as a
+    launch of its own beyond them, with the same arithmetic: twenty streams in turn, each
+    called twice, give bit-identical output and LSE, and match the oracle."""
+    q, k, v, mask = _case("padding_with_empty_rows")
+    qd, kd, vd, md = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), mask.numpy())
+    first, first_lse, _ = _capi_call(qd, kd, vd, md, 0)
+    assert np.abs(first.double().numpy() - ref).max() < 2e-2
+    streams = [torch.cuda.Stream() for _ in range(20)]
+    for i, s in enumerate(streams):
+        with torch.cuda.stream(s):
+            for rep in range(2):
+                out, lse, _ = _capi_call(qd, kd, vd, md, 0)
+                assert torch.equal(out, first) and torch.equal(lse, first_lse), (i, rep)
+    # More than 32 splits (past the counter word's split bits): the separate merge.
+    q, k, v, mask = _case("long_cache")
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(k), C.f64(v), mask.numpy())
+    for ns in (33, 40):
+        print(f"num_splits {ns}", flush=True)
+        out, _, _ = _capi_call(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), ns)
+        assert np.abs(out.double().numpy() - ref).max() < 2e-2, ns
