@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KMI_ABI_VERSION 3
+#define KMI_ABI_VERSION 4
 
 /* Element types of operands. */
 enum kmi_dtype {
@@ -82,8 +82,8 @@ enum kmi_mask_mode {
  *   its row keeps any key and a fully-masked row is the softmax over its raw scores.
  * lse (optional, fp32, natural log): dense [B, Hq, Sq] / varlen [Hq, Tq] with strides
  *   lse_stride (batch, head, seq); varlen ignores lse_stride[0].
- * Supported: dtype BF16 or F16, head_dim a multiple of 8 up to 256, heads_kv dividing
- * heads_q.
+ * Supported: dtype BF16 or F16, head_dim (and head_dim_v) a multiple of 8 up to 256,
+ * heads_kv dividing heads_q.
  */
 typedef struct kmi_attn_args {
     const void* q;
@@ -115,7 +115,11 @@ typedef struct kmi_attn_args {
     /* 0: chosen by the library (split-KV for short query tiles over long key ranges);
      * 1: no split; n > 1: at most n key splits. */
     int32_t num_splits;
-    int32_t reserved;
+    /* ABI 4: the value head dim Dv (0: head_dim).  v [.., Dv] and out [.., Dv]; q and k
+     * keep head_dim.  A multiple of 8 up to 256.  The reference's packed op takes it
+     * (aten_varlen.cpp:160-208: v [Tk, Hk, Dv], out [Tq, H, Dv]); the kernels run at the
+     * larger of the two dims, padded, so dense calls take it too. */
+    int32_t head_dim_v;
     /* Dense calls only (ABI 2; NULL: every key).  Device int32 [batch]: sequence b's
      * queries see keys [0, L_b), L_b = key_lengths[b] clamped to [1, seq_k]; no mask is
      * built or read and key tiles past L_b are not loaded.  Query rows past L_b still see
@@ -209,6 +213,8 @@ typedef struct kmi_attn_bwd_args {
     int64_t total_q, total_k;
     /* Dense calls only (NULL: every key): the forward's key_lengths (kmi_attn_args). */
     const int32_t* key_lengths;
+    /* ABI 4: the value head dim Dv (0: head_dim): v, out, grad_out and grad_v [.., Dv]. */
+    int64_t head_dim_v;
 } kmi_attn_bwd_args;
 
 /* Bytes of workspace kmi_attn_bwd needs for `args`. */

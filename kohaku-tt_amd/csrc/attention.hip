@@ -14,10 +14,17 @@ namespace fwd {
 namespace {
 
 
+// The value / output head dim, and the padded dim the kernels run at (the larger of q's
+// and v's).
+int64_t value_dim(const kmi_attn_args* a) { return a->head_dim_v > 0 ? a->head_dim_v : a->head_dim; }
+int kernel_dim(const kmi_attn_args* a) { return padded_head_dim(std::max<int64_t>(a->head_dim, value_dim(a))); }
+
 const char* check_args(const kmi_attn_args* a) {
     if (!a) return "null args";
     if (a->dtype != KMI_BF16 && a->dtype != KMI_F16) return "dtype must be BF16 or F16";
     if (!head_dim_supported(a->head_dim)) return "head_dim must be a multiple of 8 up to 256";
+    if (a->head_dim_v != 0 && !head_dim_supported(a->head_dim_v))
+        return "head_dim_v must be 0 or a multiple of 8 up to 256";
     if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seq_q < 0 || a->seq_k <= 0)
         return "sizes must be positive (seq_q may be 0)";
     if (a->heads_q % a->heads_kv != 0) return "heads_kv must divide heads_q";
@@ -100,7 +107,7 @@ Plan make_plan(const kmi_attn_args* a) {
     const int64_t G = a->heads_q / a->heads_kv;
     const int64_t vrows = a->seq_q * G;
     const int64_t units = a->batch * a->heads_kv;
-    const int dp = padded_head_dim(a->head_dim);
+    const int dp = padded_head_dim(std::max<int64_t>(a->head_dim, value_dim(a)));
     int nqb = dp == 64 ? 4 : (dp <= 128 ? 2 : 1);
     // Fewer rows per workgroup when the larger tile would leave under two workgroups per
     // CU, and short query tiles (decode: Sq x G rows per K/V head) take only what they have.
@@ -171,7 +178,7 @@ Plan make_plan(const kmi_attn_args* a) {
     // Its buffer resources span a unit's keys with 32-bit offsets.
     const bool span32 = a->seq_k * std::max<int64_t>({a->k_stride[2], a->v_stride[2], 64}) * 2 < (int64_t{1} << 31);
     pl.pipe = a->causal && !pl.decode && !pl.rs && pl.splits == 1 && a->mask_mode == KMI_MASK_NONE && !a->cu_seqlens_q &&
-              !a->key_lengths && a->head_dim == 64 && out16 && span32 && pipe_enabled();
+              !a->key_lengths && a->head_dim == 64 && value_dim(a) == 64 && out16 && span32 && pipe_enabled();
     pl.rows_total = a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q;
     pl.ws_bytes = 0;
     return pl;
@@ -181,7 +188,7 @@ Plan make_plan(const kmi_attn_args* a) {
 template <typename T>
 hipError_t launch_dim(const AttnParams& p, const Plan& pl, hipStream_t s) {
     if (pl.pipe) return launch_pipe<T>(p, s);
-    switch (padded_head_dim(p.d)) {
+    switch (padded_head_dim(std::max(p.d, p.dv))) {
         case 32: return launch_all<T, 32>(p, pl, s);
         case 64: return launch_all<T, 64>(p, pl, s);
         case 96: return launch_all<T, 96>(p, pl, s);
@@ -193,7 +200,7 @@ hipError_t launch_dim(const AttnParams& p, const Plan& pl, hipStream_t s) {
 
 size_t ws_bytes_for(const kmi_attn_args* a, const Plan& pl) {
     if (pl.splits <= 1) return 0;
-    return static_cast<size_t>(pl.splits) * pl.rows_total * a->heads_q * (padded_head_dim(a->head_dim) + 2) *
+    return static_cast<size_t>(pl.splits) * pl.rows_total * a->heads_q * (kernel_dim(a) + 2) *
            sizeof(float);
 }
 
@@ -248,6 +255,7 @@ int enqueue(const kmi_attn_args* a, const Plan& pl, void* workspace, void* strea
     p.seq_q = static_cast<int>(a->seq_q);
     p.seq_k = static_cast<int>(a->seq_k);
     p.d = static_cast<int>(a->head_dim);
+    p.dv = static_cast<int>(value_dim(a));
     p.causal = a->causal ? 1 : 0;
     p.scale_log2 = static_cast<float>(a->scale * 1.4426950408889634);
     p.splits = pl.splits;
@@ -263,7 +271,7 @@ int enqueue(const kmi_attn_args* a, const Plan& pl, void* workspace, void* strea
     p.fd_group = fast_div(static_cast<uint32_t>(p.group));
     if (pl.splits > 1) {
         p.part_o = static_cast<float*>(workspace);
-        p.part_lse = p.part_o + static_cast<size_t>(pl.splits) * p.rows_total * p.hq * padded_head_dim(a->head_dim);
+        p.part_lse = p.part_o + static_cast<size_t>(pl.splits) * p.rows_total * p.hq * kernel_dim(a);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (pl.decode && pl.splits > 1 && pl.splits <= 32)

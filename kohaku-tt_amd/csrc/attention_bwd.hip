@@ -107,7 +107,8 @@ struct BwdParams {
     const int32_t *cu_q, *cu_k;
     const int32_t* klen;  // dense key lengths [batch] (or null)
     int total_q, total_k;
-    int batch, hq, hkv, group, seq_q, seq_k, causal, d;
+    int batch, hq, hkv, group, seq_q, seq_k, causal;
+    int d, dval;  // q / k and v / out head dims (DP: the larger, padded)
     int64_t rows_total, keys_total;
     float scale, c2;  // c2 = scale * log2(e)
 };
@@ -293,7 +294,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
             kf[c] = __builtin_bit_cast(v8, frag(kp, p.ks[2], kw0 + l16, g.lk, 32 * c + 8 * g4, p.d));
-            vf[c] = __builtin_bit_cast(v8, frag(vp, p.vs[2], kw0 + l16, g.lk, 32 * c + 8 * g4, p.d));
+            vf[c] = __builtin_bit_cast(v8, frag(vp, p.vs[2], kw0 + l16, g.lk, 32 * c + 8 * g4, p.dval));
         }
     }
     f32x4 dk[DB], dv[DB];
@@ -333,7 +334,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         int h, r0;
         item_at(split, h, r0);
         load_regs<T, DP>(q_of(h), p.qs[2], r0, g.lq, p.d, qr);
-        load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, p.d, dor);
+        load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, p.dval, dor);
         load_stats(h, r0);
     }
     for (int it = split; it < items; it += p.splits) {
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
             int h2, r2;
             item_at(it + p.splits, h2, r2);
             load_regs<T, DP>(q_of(h2), p.qs[2], r2, g.lq, p.d, qr);
-            load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, p.d, dor);
+            load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, p.dval, dor);
             load_stats(h2, r2);
         }
 #pragma unroll
@@ -427,9 +428,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int key = kw0 + 4 * g4 + j;
-                if (key < kwrite && d < p.d) {
-                    p.pdk[(base + key) * DP + d] = dk[db][j] * p.scale;
-                    p.pdv[(base + key) * DP + d] = dv[db][j];
+                if (key < kwrite) {
+                    if (d < p.d) p.pdk[(base + key) * DP + d] = dk[db][j] * p.scale;
+                    if (d < p.dval) p.pdv[(base + key) * DP + d] = dv[db][j];
                 }
             }
         }
@@ -443,9 +444,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int key = kw0 + 4 * g4 + j;
-            if (key < kwrite && d < p.d) {
-                dkp[static_cast<int64_t>(key) * p.dks[2] + d] = from_f32<T>(dk[db][j] * p.scale);
-                dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[db][j]);
+            if (key < kwrite) {
+                if (d < p.d) dkp[static_cast<int64_t>(key) * p.dks[2] + d] = from_f32<T>(dk[db][j] * p.scale);
+                if (d < p.dval) dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[db][j]);
             }
         }
     }
@@ -458,7 +459,7 @@ constexpr int kSumBatch = 8;
 // (K/V head, key row, 4 head-dim columns).
 template <typename T, int DP>
 __device__ __forceinline__ void kv_sum_item(const BwdParams& p, const int64_t item) {
-    const int nq = p.d / 4;  // float4 items per key row (head dims are multiples of 8)
+    const int nq = max(p.d, p.dval) / 4;  // float4 items per key row (head dims are multiples of 8)
     const int64_t items = static_cast<int64_t>(p.hkv) * p.keys_total * nq;
     if (item >= items) return;
     const int c = static_cast<int>(item % nq);
@@ -499,8 +500,8 @@ __device__ __forceinline__ void kv_sum_item(const BwdParams& p, const int64_t it
     T* dvp = static_cast<T*>(p.dv) + voff + kvh * p.dvs[1] + 4 * c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        dkp[e] = from_f32<T>(sk[e]);
-        dvp[e] = from_f32<T>(sv[e]);
+        if (4 * c < p.d) dkp[e] = from_f32<T>(sk[e]);
+        if (4 * c < p.dval) dvp[e] = from_f32<T>(sv[e]);
     }
 }
 
@@ -547,8 +548,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
         for (int c = 0; c < DC; ++c) {
             const int col = 32 * c + 8 * g4;
             qf[c] = __builtin_bit_cast(v8, frag(qp, p.qs[2], rw0 + l16, g.lq, col, p.d));
-            of[c] = __builtin_bit_cast(v8, frag(dp, p.dos[2], rw0 + l16, g.lq, col, p.d));
-            const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], rw0 + l16, g.lq, col, p.d));
+            of[c] = __builtin_bit_cast(v8, frag(dp, p.dos[2], rw0 + l16, g.lq, col, p.dval));
+            const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], rw0 + l16, g.lq, col, p.dval));
 #pragma unroll
             for (int e = 0; e < 8; ++e) rdot += to_f32(of[c][e]) * to_f32(yv[e]);
         }
@@ -581,7 +582,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int kstep = p.ksplit * BT;
     if (ksp * BT < kend) {
         load_regs<T, DP>(kbase, p.ks[2], ksp * BT, g.lk, p.d, kr);
-        load_regs<T, DP>(vbase, p.vs[2], ksp * BT, g.lk, p.d, vr);
+        load_regs<T, DP>(vbase, p.vs[2], ksp * BT, g.lk, p.dval, vr);
     }
     for (int k0 = ksp * BT; k0 < kend; k0 += kstep) {
         __syncthreads();
@@ -590,7 +591,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
         __syncthreads();
         if (k0 + kstep < kend) {  // the next tile's loads overlap this tile's products
             load_regs<T, DP>(kbase, p.ks[2], k0 + kstep, g.lk, p.d, kr);
-            load_regs<T, DP>(vbase, p.vs[2], k0 + kstep, g.lk, p.d, vr);
+            load_regs<T, DP>(vbase, p.vs[2], k0 + kstep, g.lk, p.dval, vr);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -707,10 +708,15 @@ __global__ __launch_bounds__(256) void attn_bwd_sums(const BwdParams p, const in
     }
 }
 
+// The value / output head dim (head_dim_v, or head_dim when 0).
+int64_t bwd_value_dim(const kmi_attn_bwd_args* a) { return a->head_dim_v > 0 ? a->head_dim_v : a->head_dim; }
+
 const char* check_bwd(const kmi_attn_bwd_args* a) {
     if (!a) return "null args";
     if (a->dtype != KMI_BF16 && a->dtype != KMI_F16) return "dtype must be BF16 or F16";
     if (!head_dim_supported(a->head_dim)) return "head_dim must be a multiple of 8 up to 256";
+    if (a->head_dim_v != 0 && !head_dim_supported(a->head_dim_v))
+        return "head_dim_v must be 0 or a multiple of 8 up to 256";
     if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seq_q <= 0 || a->seq_k <= 0)
         return "sizes must be positive";
     if (a->heads_q % a->heads_kv != 0) return "heads_kv must divide heads_q";
@@ -780,7 +786,7 @@ struct BwdLayout {
 
 BwdLayout bwd_layout(const kmi_attn_bwd_args* a) {
     BwdLayout l{};
-    const int64_t dp = padded_head_dim(a->head_dim);
+    const int64_t dp = padded_head_dim(std::max(a->head_dim, bwd_value_dim(a)));
     l.dr = static_cast<size_t>(ceil_div(a->heads_q * rows_total_of(a), 4) * 4);
     // One split sums the query heads of a K/V head in its registers and writes dK / dV.
     const int s = bwd_splits(a);
@@ -806,7 +812,8 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
                        dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hkv * ntk * p.splits)),
                        dim3(BWD_THREADS), 0, s, p);
     const int64_t dq_blocks = p.pdq ? ceil_div(static_cast<int64_t>(p.hq) * p.rows_total * (p.d / 4), 256) : 0;
-    const int64_t kv_blocks = p.pdk ? ceil_div(static_cast<int64_t>(p.hkv) * p.keys_total * (p.d / 4), 256) : 0;
+    const int64_t kv_blocks =
+        p.pdk ? ceil_div(static_cast<int64_t>(p.hkv) * p.keys_total * (std::max(p.d, p.dval) / 4), 256) : 0;
     if (dq_blocks + kv_blocks > 0)
         hipLaunchKernelGGL((attn_bwd_sums<T, DP>), dim3(static_cast<unsigned>(dq_blocks + kv_blocks)), dim3(256), 0, s,
                            p, dq_blocks);
@@ -826,7 +833,7 @@ hipError_t launch_bwd_mask(const BwdParams& p, int mk, hipStream_t s) {
 
 template <typename T>
 hipError_t launch_bwd_dim(const BwdParams& p, int mk, hipStream_t s) {
-    switch (padded_head_dim(p.d)) {
+    switch (padded_head_dim(std::max(p.d, p.dval))) {
         case 32: return launch_bwd_mask<T, 32>(p, mk, s);
         case 64: return launch_bwd_mask<T, 64>(p, mk, s);
         case 96: return launch_bwd_mask<T, 96>(p, mk, s);
@@ -905,6 +912,7 @@ extern "C" int kmi_attn_bwd(const kmi_attn_bwd_args* a, void* workspace, size_t 
     p.seq_k = static_cast<int>(a->seq_k);
     p.causal = a->causal ? 1 : 0;
     p.d = static_cast<int>(a->head_dim);
+    p.dval = static_cast<int>(bwd_value_dim(a));
     p.rows_total = rows_total_of(a);
     p.keys_total = keys_total_of(a);
     p.scale = static_cast<float>(a->scale);

@@ -287,12 +287,12 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             for (int j = 0; j < MAXV; ++j) {
                 const int v = min(tid + (NW * kWave) * j, nvec - 1);
                 const int row = min(v / VPR_, lk - 1), ch = v % VPR_;
-                // Columns past the head dim read in range and are zeroed.
-                const int col = min(8 * ch, p.d - 8);
-                const u32x4 kx = *reinterpret_cast<const u32x4*>(kg + static_cast<int64_t>(row) * p.ks[2] + col);
-                const u32x4 vx = *reinterpret_cast<const u32x4*>(vg + static_cast<int64_t>(row) * p.vs[2] + col);
+                // Columns past the head dims read in range and are zeroed.
+                const int colk = min(8 * ch, p.d - 8), colv = min(8 * ch, p.dv - 8);
+                const u32x4 kx = *reinterpret_cast<const u32x4*>(kg + static_cast<int64_t>(row) * p.ks[2] + colk);
+                const u32x4 vx = *reinterpret_cast<const u32x4*>(vg + static_cast<int64_t>(row) * p.vs[2] + colv);
                 kv[j] = 8 * ch < p.d ? kx : u32x4{0u, 0u, 0u, 0u};
-                vv[j] = 8 * ch < p.d ? vx : u32x4{0u, 0u, 0u, 0u};
+                vv[j] = 8 * ch < p.dv ? vx : u32x4{0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int j = 0; j < MAXV; ++j) {
@@ -376,8 +376,8 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // Staging lanes past the padded row idle; chunks past the head dim stage zeros (their
     // loads stay within the row's range).
     const bool stage_lane = dg < NCH;
-    const bool stage_live = 8 * dg < p.d;
-    const int dgc = min(dg, (p.d - 1) / 8);
+    const bool stage_live = 8 * dg < p.d;  // (K's chunks; V's past dv need not be zero)
+    const int dgc = min(dg, (p.d - 1) / 8), dgcv = min(dg, (p.dv - 1) / 8);
     // Padded head dims: K's columns past d must be zeros (they meet Q's zero columns in
     // S, and a finite value of another row there could still be inf); V's need not be
     // (they only reach output columns past d, which are never written).  Uniform.
@@ -388,10 +388,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     const char* vunit = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + vb_off + kvh * p.vs[1] +
                                                       static_cast<int64_t>(k0) * p.vs[2]);
     const uint32_t k_lane = KD ? static_cast<uint32_t>(l16 * kstride + 16 * g4) : static_cast<uint32_t>(krow * kstride + 16 * dgc);
-    const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dgc);
+    const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dgcv);
     // Bytes per key of a resource's range (a zero row stride repeats one row).
     const uint32_t kspan = static_cast<uint32_t>(kstride > 0 ? kstride : p.d * static_cast<int64_t>(sizeof(T)));
-    const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : p.d * static_cast<int64_t>(sizeof(T)));
+    const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : p.dv * static_cast<int64_t>(sizeof(T)));
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
     T* vl = kl + (KD ? 0 : TW * KP);
 
@@ -423,14 +423,15 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     int kfo[DMA2 ? DC : 1];                          // K fragment element offsets (keys 0..15)
     int vtro[DMA2 ? DB : 1];                         // V transposed-read element offsets (first 16 keys)
     if constexpr (DMA2) {
-        const int cmax = (p.d - 1) / 8;  // padded head dims: chunks past d repeat the last
+        // Padded head dims: chunks past d (K) / dv (V) repeat the last.
+        const int cmax = (p.d - 1) / 8, cmaxv = (p.dv - 1) / 8;
         const int a = lane >> 3, q7 = lane & 7;
 #pragma unroll
         for (int par = 0; par < 2; ++par) {
             dk_b[par] = static_cast<uint32_t>(a) * static_cast<uint32_t>(kstride) +
                         16u * static_cast<uint32_t>(min(q7 ^ kswz(8 * par + a), cmax));
             dv_b[par] = static_cast<uint32_t>(a) * static_cast<uint32_t>(vstride) +
-                        16u * static_cast<uint32_t>(min(q7 ^ vswz(8 * par + a), cmax));
+                        16u * static_cast<uint32_t>(min(q7 ^ vswz(8 * par + a), cmaxv));
         }
 #pragma unroll
         for (int c = 0; c < DC; ++c) kfo[c] = l16 * D + 8 * ((4 * c + g4) ^ kswz(l16));
@@ -456,7 +457,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             } else {
                 // Last tile: rows past the unit's last key repeat it (finite; their scores
                 // are masked), so every lane reads in range and every slot is written.
-                const int cmax = (p.d - 1) / 8;
+                const int cmax = ((V ? p.dv : p.d) - 1) / 8;
 #pragma unroll
                 for (int i = 0; i < TW / 8; ++i) {
                     const int r = 8 * i + (lane >> 3);
@@ -1003,7 +1004,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                 v4 w;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(o[d][b][i] * inv);
-                if (16 * d + 4 * g4 < p.d) *reinterpret_cast<v4*>(dst + 16 * d + 4 * g4) = w;
+                if (16 * d + 4 * g4 < p.dv) *reinterpret_cast<v4*>(dst + 16 * d + 4 * g4) = w;
             }
             if (p.lse && g4 == 0)
                 p.lse[lb_off + head * p.ls[1] + static_cast<int64_t>(q0 + pos) * p.ls[2]] =
@@ -1041,7 +1042,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
         }
     };
     auto write_row = [&](int r, int col, const f32x4& acc) {
-        if (col >= p.d) return;  // padded head-dim columns
+        if (col >= p.dv) return;  // padded head-dim columns
         const int pos = fdiv(r, p.fd_group);
         const int head = kvh * G + (r - pos * G);
         if (p.splits > 1) {
@@ -1364,7 +1365,7 @@ __device__ __forceinline__ void decode_merge_unit(const AttnParams& p, const int
         const float m = masked ? mk : mr, l = masked ? sk : sr;
         const f32x4 a = masked ? ak : ar;
         const float inv = l > 0.f ? 1.f / l : 0.f;
-        if (c < p.d) {
+        if (c < p.dv) {
             const int64_t ob_off = p.cu_q ? 0 : u.seq * p.os[0];
             T* out = static_cast<T*>(p.out) + ob_off + head * p.os[1] + static_cast<int64_t>(u.q0 + pos) * p.os[2] + c;
             typedef __attribute__((__vector_size__(2 * sizeof(T)))) T t2;
@@ -1501,14 +1502,14 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
                                                       static_cast<int64_t>(k0) * p.vs[2]);
     const int krow = lane / VPR, dg = lane - (lane / VPR) * VPR;
     const bool stage_lane = dg < NCH;  // staging lanes past the padded row idle
-    const int dgc = min(dg, (p.d - 1) / 8);
+    const int dgc = min(dg, (p.dv - 1) / 8);  // V's chunk (V's columns past dv repeat the last)
     // Padded head dims: K's columns past d are zeroed (as in the prefill kernel); V's
-    // reach only output columns past d, which are never written.  Uniform.
+    // reach only output columns past dv, which are never written.  Uniform.
     const bool kpad = p.d < D;
     const uint32_t k_lane = static_cast<uint32_t>(l16 * kstride + 16 * g4);
     const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dgc);
     const uint32_t kspan = static_cast<uint32_t>(kstride > 0 ? kstride : p.d * static_cast<int64_t>(sizeof(T)));
-    const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : p.d * static_cast<int64_t>(sizeof(T)));
+    const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : p.dv * static_cast<int64_t>(sizeof(T)));
     T* vl = reinterpret_cast<T*>(smem) + wave * WN * VP;
 
     // One tile's registers: K fragments, the V rows this lane stages, the mask values.
@@ -1786,7 +1787,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
             t2 w2;
             w2[0] = static_cast<T>(acc[j] * inv);
             w2[1] = static_cast<T>(acc[j + 1] * inv);
-            if (c0 + j < p.d) *reinterpret_cast<t2*>(out + j) = w2;
+            if (c0 + j < p.dv) *reinterpret_cast<t2*>(out + j) = w2;
         }
         if (p.lse && wave == 0 && g4 == 0) {
             const int64_t lb_off = p.cu_q ? 0 : seq * p.ls[0];
@@ -1800,7 +1801,7 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
         float* dst = p.part_o + prow * D + c0;
 #pragma unroll
         for (int j = 0; j < PER; j += 2)
-            if (c0 + j < p.d) store_dev(dst + j, f32x2{acc[j] * inv, acc[j + 1] * inv});
+            if (c0 + j < p.dv) store_dev(dst + j, f32x2{acc[j] * inv, acc[j + 1] * inv});
         if (wave == 0 && g4 == 0)
             store_dev(p.part_lse + 2 * prow,
                       f32x2{L > 0.f ? M + log2f(L) : -INFINITY, (MASKED && !sel_masked) ? 1.f : 0.f});
@@ -1842,7 +1843,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     constexpr int PER = (D + 63) / 64;
     int colc[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) colc[j] = min(lane + 64 * j, p.d - 1);
+    for (int j = 0; j < PER; ++j) colc[j] = min(lane + 64 * j, p.dv - 1);
     float acc[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) acc[j] = 0.f;
@@ -1935,7 +1936,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     T* dst = static_cast<T*>(p.out) + ob_off + h * p.os[1] + static_cast<int64_t>(posn) * p.os[2];
 #pragma unroll
     for (int j = 0; j < PER; ++j)
-        if (lane + 64 * j < p.d) dst[lane + 64 * j] = static_cast<T>(acc[j] * inv);
+        if (lane + 64 * j < p.dv) dst[lane + 64 * j] = static_cast<T>(acc[j] * inv);
     if (p.lse && lane == 0)
         p.lse[lb_off + h * p.ls[1] + static_cast<int64_t>(posn) * p.ls[2]] =
             wsum > 0.f ? (m + log2f(wsum)) * kLn2 + (any_masked ? 0.f : kMaskedLogit) : -INFINITY;
@@ -1993,7 +1994,7 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
     p.snake = 0;
     if (p.causal && !p.cu_q && p.splits == 1 && p.npair == 0 && slots > 0 && grid <= slots) p.snake = cu_count();
     p.fd_snake = fast_div(static_cast<uint32_t>(p.snake));
-    const int64_t kv_bytes = units * static_cast<int64_t>(p.seq_k) * p.d * 2 * static_cast<int64_t>(sizeof(T));
+    const int64_t kv_bytes = units * static_cast<int64_t>(p.seq_k) * (p.d + p.dv) * static_cast<int64_t>(sizeof(T));
     if (!RS && p.splits == 1 && p.npair == 0 && kv_bytes > (int64_t{4} << 20) && xcd_map_mode() != 0) {
         if (p.cu_q || p.causal) {
             if (units >= 8 && xcd_map_mode() == 1) {

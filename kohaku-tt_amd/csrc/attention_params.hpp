@@ -65,7 +65,8 @@ struct AttnParams {
     // Packed masks: device int64 [batch + 1] block offsets (or null: added up in-kernel).
     const int64_t* mask_off;
     int batch, hq, hkv, group, seq_q, seq_k;
-    int d;  // head dim (the kernels' D template argument is it padded to a multiple of 32)
+    int d;   // q / k head dim
+    int dv;  // v / out head dim (the kernels' D template argument is the larger, padded to a multiple of 32)
     int causal;
     float scale_log2;
     int splits, tiles_per_split;

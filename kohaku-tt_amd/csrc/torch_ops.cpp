@@ -335,6 +335,7 @@ std::tuple<Tensor, Tensor, Tensor> run_backward(const BwdCall& c) {
     a.causal = c.causal ? 1 : 0;
     const int64_t D = q.size(-1);
     a.head_dim = D;
+    a.head_dim_v = v.size(-1);
     if (varlen) {
         a.batch = c.nseq;
         a.heads_q = q.size(1);
@@ -667,11 +668,11 @@ struct VarlenCall {
     bool packed = false;
 };
 
-// Forward of a packed call: (out [Tq, H, D] in the input dtype, lse [H, Tq] fp32).
+// Forward of a packed call: (out [Tq, H, Dv] in the input dtype, lse [H, Tq] fp32).
 std::tuple<Tensor, Tensor> run_varlen(const VarlenCall& c, bool fp32) {
     const Tensor q = kernel_operand(c.q, 0), k = kernel_operand(c.k, 0), v = kernel_operand(c.v, 0);
-    const int64_t Tq = q.size(0), H = q.size(1), D = q.size(2), Tk = k.size(0);
-    Tensor out = at::empty({Tq, H, D}, q.options());
+    const int64_t Tq = q.size(0), H = q.size(1), D = q.size(2), Dv = v.size(2), Tk = k.size(0);
+    Tensor out = at::empty({Tq, H, Dv}, q.options());
     Tensor lse = at::empty({H, Tq}, q.options().dtype(at::kFloat));
     if (Tq == 0) return {fp32 ? out.to(at::kFloat) : out, lse};
     TORCH_CHECK(Tk > 0, "kohakutt_amd: sdpa_varlen: a sequence with queries needs keys");
@@ -689,6 +690,7 @@ std::tuple<Tensor, Tensor> run_varlen(const VarlenCall& c, bool fp32) {
     a.seq_q = std::max<int64_t>(1, c.max_q);
     a.seq_k = std::max<int64_t>(1, c.max_k);
     a.head_dim = D;
+    a.head_dim_v = static_cast<int32_t>(Dv);
     // [T, H, D] tensors: stride[1] is the head stride, stride[2] the token stride.
     a.q_stride[1] = q.stride(1);
     a.q_stride[2] = q.stride(0);
@@ -727,21 +729,23 @@ std::tuple<Tensor, Tensor> run_varlen(const VarlenCall& c, bool fp32) {
     return {fp32 ? out.to(at::kFloat) : out, lse};
 }
 
-// q, k, v of a packed call as the kernels take them: [T, H, D] of one dtype (fp32 cast to
-// bf16 at entry, like the dense route), K/V heads dividing Q heads, one head dim.
+// q, k, v of a packed call as the kernels take them: [T, H, D] (v [T, Hk, Dv]) of one
+// dtype (fp32 cast to bf16 at entry, like the dense route), K/V heads dividing Q heads.
+// The value head dim may differ from q's and k's (the reference's packed op,
+// aten_varlen.cpp:160-208).
 void packed_operands(const char* op, const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, VarlenCall& c,
                      bool& fp32) {
     TORCH_CHECK(q_in.is_cuda() && k_in.is_cuda() && v_in.is_cuda() && k_in.device() == q_in.device() &&
                     v_in.device() == q_in.device(),
                 "kohakutt_amd: ", op, " needs GPU tensors on one device");
     TORCH_CHECK_NOT_IMPLEMENTED(q_in.dim() == 3 && k_in.dim() == 3 && v_in.dim() == 3,
-                                "kohakutt_amd: ", op, " takes q [Tq, H, D], k / v [Tk, Hk, D]");
+                                "kohakutt_amd: ", op, " takes q [Tq, H, D], k [Tk, Hk, D], v [Tk, Hk, Dv]");
     TORCH_CHECK_NOT_IMPLEMENTED(k_in.size(0) == v_in.size(0) && k_in.size(1) == v_in.size(1) &&
                                     k_in.size(1) > 0 && q_in.size(1) % k_in.size(1) == 0,
                                 "kohakutt_amd: ", op, " q / k / v shapes do not match (K / V heads must divide Q heads)");
-    TORCH_CHECK_NOT_IMPLEMENTED(q_in.size(2) == k_in.size(2) && v_in.size(2) == q_in.size(2) &&
-                                    head_dim_ok(q_in.size(2)),
-                                "kohakutt_amd: ", op, " needs one head dim, a multiple of 8 up to 256");
+    TORCH_CHECK_NOT_IMPLEMENTED(q_in.size(2) == k_in.size(2) && head_dim_ok(q_in.size(2)) && head_dim_ok(v_in.size(2)),
+                                "kohakutt_amd: ", op, " needs q and k of one head dim and head dims that are multiples of 8 "
+                                "up to 256");
     fp32 = q_in.scalar_type() == at::kFloat;
     c.q = fp32 ? q_in.to(at::kBFloat16) : q_in;
     c.k = fp32 ? k_in.to(at::kBFloat16) : k_in;
@@ -844,7 +848,8 @@ std::tuple<Tensor, Tensor, Tensor> sdpa_varlen_backward_ref(
     TORCH_CHECK_NOT_IMPLEMENTED(cu_q.back() == q.size(0) && cu_k.back() == k.size(0),
                                 "kohakutt_amd: ", op, " the offsets must end at the token counts");
     TORCH_CHECK_NOT_IMPLEMENTED(grad.sizes() == out.sizes() && grad.scalar_type() == q.scalar_type() &&
-                                    out.dim() == 3 && out.sizes() == q.sizes(),
+                                    out.dim() == 3 && out.size(0) == q.size(0) && out.size(1) == q.size(1) &&
+                                    out.size(2) == v.size(2),
                                 "kohakutt_amd: ", op, " grad and out must be the forward's [query tokens, heads, value dim]");
     const Tensor lse = stats_of(out);
     TORCH_CHECK_NOT_IMPLEMENTED(lse.defined(), "kohakutt_amd: ", op,
@@ -905,7 +910,7 @@ OffsetArgs offset_args(const char* op, const Tensor& cu_q_in, const Tensor& cu_k
 // what kohakutt_amd.sdpa_varlen and torch_attn::_varlen_attn call.  key_mask: [Tk] bool
 // keep-mask or additive (logit units); packed_mask: every sequence's row-major
 // [Lq_i, Lk_i] block, concatenated (bool or additive, shared by the heads, usable with
-// is_causal).  Returns (out [Tq, H, D], lse [H, Tq] fp32).
+// is_causal).  v may carry its own head dim: returns (out [Tq, H, Dv], lse [H, Tq] fp32).
 std::tuple<Tensor, Tensor> sdpa_varlen_offsets(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in,
                                                const Tensor& cu_q_in, const Tensor& cu_k_in, int64_t max_q,
                                                int64_t max_k, bool is_causal, optional<double> scale,
@@ -959,8 +964,9 @@ std::tuple<Tensor, Tensor, Tensor> sdpa_varlen_offsets_backward(
     bool fp32 = false;
     packed_operands(op, q, k, v, c, fp32);
     TORCH_CHECK_NOT_IMPLEMENTED(!fp32, "kohakutt_amd: ", op, " takes bf16 / fp16 tensors");
-    TORCH_CHECK(grad.sizes() == q.sizes() && out.sizes() == q.sizes() && grad.scalar_type() == q.scalar_type(),
-                "kohakutt_amd: ", op, " grad and out must be shaped and typed as q");
+    TORCH_CHECK(grad.dim() == 3 && grad.size(0) == q.size(0) && grad.size(1) == q.size(1) &&
+                    grad.size(2) == v.size(2) && out.sizes() == grad.sizes() && grad.scalar_type() == q.scalar_type(),
+                "kohakutt_amd: ", op, " grad and out must be [query tokens, heads, value dim] in q's dtype");
     TORCH_CHECK(lse.dim() == 2 && lse.size(0) == q.size(1) && lse.size(1) == q.size(0) &&
                     lse.scalar_type() == at::kFloat,
                 "kohakutt_amd: ", op, " lse must be the forward's fp32 [H, Tq]");

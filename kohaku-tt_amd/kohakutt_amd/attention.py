@@ -167,12 +167,13 @@ def sdpa_varlen(
     """Scaled dot-product attention over packed variable-length sequences (the
     reference's ``kohakutt.sdpa_varlen``, ``attention.py:26-76``).
 
-    q [Tq, H, D], k [Tk, Hkv, D], v [Tk, Hkv, D] (bf16 / fp16; fp32 is cast to bf16)
-    hold every sequence's tokens back to back.  ``cu_seq_q`` / ``cu_seq_k`` are the
+    q [Tq, H, D], k [Tk, Hkv, D], v [Tk, Hkv, Dv] (bf16 / fp16; fp32 is cast to bf16;
+    Dv may differ from D, as in the reference's packed op) hold every sequence's tokens
+    back to back.  ``cu_seq_q`` / ``cu_seq_k`` are the
     cumulative offsets [0, ..., total] (a list or an int tensor, host or GPU;
     ``cu_seq_k`` defaults to ``cu_seq_q``).  Each query attends to the keys of its own
     sequence; with ``is_causal``, query r of a sequence sees its first
-    min(Lk, r + 1 + Lk - Lq) keys.  Returns [Tq, H, D]; differentiable in q, k and v.
+    min(Lk, r + 1 + Lk - Lq) keys.  Returns [Tq, H, Dv]; differentiable in q, k and v.
 
     ``attn_mask``: a key mask [Tk] (bool: True keeps the key; float: added to its logits,
     clamped at -5e5), as the reference takes it.  ``packed_mask``: this build's per-row

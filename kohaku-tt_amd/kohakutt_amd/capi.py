@@ -70,7 +70,7 @@ class AttnArgs(ctypes.Structure):
         ("total_q", ctypes.c_int64),
         ("total_k", ctypes.c_int64),
         ("num_splits", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("head_dim_v", ctypes.c_int32),
         ("key_lengths", ctypes.c_void_p),
         ("mask_offsets", ctypes.c_void_p),
     ]
@@ -118,6 +118,7 @@ class AttnBwdArgs(ctypes.Structure):
         ("total_q", ctypes.c_int64),
         ("total_k", ctypes.c_int64),
         ("key_lengths", ctypes.c_void_p),
+        ("head_dim_v", ctypes.c_int64),
     ]
 
 

@@ -80,6 +80,8 @@ def _args(**kw):
         (dict(cu_seqlens_q=0x3000), "go together"),
         (dict(k_stride=(ctypes.c_int64 * 3)(4 * 8 * 64, 8 * 64, (1 << 24) + 8)), "row strides"),
         (dict(v_stride=(ctypes.c_int64 * 3)(4 * 8 * 64, 8 * 64, -64)), "row strides"),
+        (dict(head_dim_v=72 + 4), "head_dim_v must be 0 or a multiple of 8 up to 256"),
+        (dict(head_dim_v=264), "head_dim_v must be 0 or a multiple of 8 up to 256"),
     ],
 )
 def test_attention_rejects_malformed_calls(kw, msg):
@@ -99,6 +101,21 @@ def test_workspace_sizes_follow_the_split_plan():
     # prefill-shaped: no split
     b = _args(batch=1, heads_q=14, heads_kv=2, seq_q=2048, seq_k=2048)
     assert capi.workspace_bytes(b) == 0
+
+
+def test_value_head_dim_sizes_the_split_partials():
+    # The split partials are as wide as the larger head dim, padded (to 32, 64, 96, 128,
+    # 192 or 256; head_dim_v 0 means head_dim): D 128 with Dv 200 keeps partials of 256
+    # columns (+ 2 statistics).
+    a = _args(batch=8, heads_q=16, heads_kv=2, seq_q=1, seq_k=4096, head_dim=128)
+    same = capi.workspace_bytes(a)
+    a.head_dim_v = 128
+    assert capi.workspace_bytes(a) == same
+    a.head_dim_v = 200
+    wide = capi.workspace_bytes(a)
+    assert wide * 130 == same * 258
+    a.head_dim_v = 64
+    assert capi.workspace_bytes(a) == same
 
 
 def test_missing_workspace_is_refused_before_launch():

@@ -163,6 +163,23 @@ def test_varlen_matches_per_sequence_torch(causal):
     assert np.abs(out - brute).max() < 1e-12 and np.abs(lse - blse).max() < 1e-12
 
 
+@pytest.mark.parametrize("dv", [4, 16])
+def test_varlen_value_dim_differs(dv):
+    """v [Tk, Hk, Dv] with Dv != D (the reference's packed op takes it,
+    aten_varlen.cpp:160-208): the oracle against torch float64 SDPA per sequence (which
+    takes a value dim of its own) and the brute-force form; lse does not depend on v."""
+    cu_q, cu_k = [0, 5, 21, 30], [0, 9, 27, 40]
+    q, k = _t64(30, 4, 8, seed=27), _t64(40, 2, 8, seed=28)
+    v = _t64(40, 2, dv, seed=29)
+    out, lse = A.sdpa_varlen(q.numpy(), k.numpy(), v.numpy(), cu_q, cu_k, is_causal=True)
+    assert out.shape == (30, 4, dv)
+    assert np.abs(out - _torch_varlen(q, k, v, cu_q, cu_k, True)).max() < 1e-12
+    brute, blse = A.sdpa_varlen_bruteforce(q.numpy(), k.numpy(), v.numpy(), cu_q, cu_k, is_causal=True)
+    assert np.abs(out - brute).max() < 1e-12 and np.abs(lse - blse).max() < 1e-12
+    _, lse8 = A.sdpa_varlen(q.numpy(), k.numpy(), _t64(40, 2, 8, seed=30).numpy(), cu_q, cu_k, is_causal=True)
+    assert np.abs(lse - lse8).max() < 1e-12
+
+
 def test_varlen_key_mask_and_packed_mask():
     cu = [0, 10, 25]
     q, k, v = _t64(25, 4, 8, seed=23), _t64(25, 4, 8, seed=24), _t64(25, 4, 8, seed=25)
