@@ -151,6 +151,11 @@ Plan make_plan(const kmi_attn_args* a) {
         int64_t wgs = std::min<int64_t>({ceil_div(256, units), int64_t{32}, most});
         if (a->num_splits > 1) wgs = std::min<int64_t>(a->num_splits, most);
         if (splits_override() > 0) wgs = std::min<int64_t>(splits_override(), most);
+        // The partials (fp32, [splits][rows][Hq][D]) stay under 2^31 bytes: the kernels
+        // address them with 32-bit buffer offsets.
+        const int64_t rows = a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q;
+        const int64_t per_split = rows * a->heads_q * (dp + 2) * static_cast<int64_t>(sizeof(float));
+        wgs = std::max<int64_t>(1, std::min<int64_t>(wgs, ((int64_t{1} << 31) - 1) / std::max<int64_t>(per_split, 1)));
         pl.splits = static_cast<int>(wgs);
         pl.tiles_per_split = static_cast<int>(ceil_div(nk, wgs));
         pl.nqb = 1;

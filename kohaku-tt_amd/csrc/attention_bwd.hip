@@ -28,6 +28,7 @@
 // along the other index comes out of the same tile through gfx950's transposed LDS reads
 // (tr_frag).  lse is the forward's natural-log row LSE.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.hpp"
@@ -258,9 +259,12 @@ __device__ __forceinline__ u32x4 frag(const T* base, int64_t rs, int row, int nr
 // query head of the group.  Two barriers per item.
 constexpr int KW = 64;
 
-template <typename T, int DP, int MK>
+template <typename T, int DP, int MK, bool DV>
 __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) {
     typedef typename BwdMfma<T>::v8 v8;
+    // v / dO / out width: a separate value dim only in the DV instances (one width keeps
+    // the equal-dim kernels' registers).
+    const int dval = DV ? p.dval : p.d;
     constexpr int RP = DP + 8;
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T qs[BT * RP];
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
             kf[c] = __builtin_bit_cast(v8, frag(kp, p.ks[2], kw0 + l16, g.lk, 32 * c + 8 * g4, p.d));
-            vf[c] = __builtin_bit_cast(v8, frag(vp, p.vs[2], kw0 + l16, g.lk, 32 * c + 8 * g4, p.dval));
+            vf[c] = __builtin_bit_cast(v8, frag(vp, p.vs[2], kw0 + l16, g.lk, 32 * c + 8 * g4, dval));
         }
     }
     f32x4 dk[DB], dv[DB];
@@ -334,7 +338,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
         int h, r0;
         item_at(split, h, r0);
         load_regs<T, DP>(q_of(h), p.qs[2], r0, g.lq, p.d, qr);
-        load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, p.dval, dor);
+        load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, dval, dor);
         load_stats(h, r0);
     }
     for (int it = split; it < items; it += p.splits) {
@@ -357,7 +361,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
             int h2, r2;
             item_at(it + p.splits, h2, r2);
             load_regs<T, DP>(q_of(h2), p.qs[2], r2, g.lq, p.d, qr);
-            load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, p.dval, dor);
+            load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, dval, dor);
             load_stats(h2, r2);
         }
 #pragma unroll
@@ -430,7 +434,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
                 const int key = kw0 + 4 * g4 + j;
                 if (key < kwrite) {
                     if (d < p.d) p.pdk[(base + key) * DP + d] = dk[db][j] * p.scale;
-                    if (d < p.dval) p.pdv[(base + key) * DP + d] = dv[db][j];
+                    if (d < dval) p.pdv[(base + key) * DP + d] = dv[db][j];
                 }
             }
         }
@@ -446,7 +450,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
             const int key = kw0 + 4 * g4 + j;
             if (key < kwrite) {
                 if (d < p.d) dkp[static_cast<int64_t>(key) * p.dks[2] + d] = from_f32<T>(dk[db][j] * p.scale);
-                if (d < p.dval) dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[db][j]);
+                if (d < dval) dvp[static_cast<int64_t>(key) * p.dvs[2] + d] = from_f32<T>(dv[db][j]);
             }
         }
     }
@@ -511,9 +515,12 @@ __device__ __forceinline__ void kv_sum_item(const BwdParams& p, const int64_t it
 // forms dS of its rows, passes it through its own LDS rows and accumulates dQ += dS K.
 constexpr int QW = 64;
 
-template <typename T, int DP, int MK>
+template <typename T, int DP, int MK, bool DV>
 __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     typedef typename BwdMfma<T>::v8 v8;
+    // v / dO / out width: a separate value dim only in the DV instances (one width keeps
+    // the equal-dim kernels' registers).
+    const int dval = DV ? p.dval : p.d;
     constexpr int RP = DP + 8;
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T ks[BT * RP];
@@ -548,8 +555,8 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
         for (int c = 0; c < DC; ++c) {
             const int col = 32 * c + 8 * g4;
             qf[c] = __builtin_bit_cast(v8, frag(qp, p.qs[2], rw0 + l16, g.lq, col, p.d));
-            of[c] = __builtin_bit_cast(v8, frag(dp, p.dos[2], rw0 + l16, g.lq, col, p.dval));
-            const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], rw0 + l16, g.lq, col, p.dval));
+            of[c] = __builtin_bit_cast(v8, frag(dp, p.dos[2], rw0 + l16, g.lq, col, dval));
+            const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], rw0 + l16, g.lq, col, dval));
 #pragma unroll
             for (int e = 0; e < 8; ++e) rdot += to_f32(of[c][e]) * to_f32(yv[e]);
         }
@@ -582,7 +589,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int kstep = p.ksplit * BT;
     if (ksp * BT < kend) {
         load_regs<T, DP>(kbase, p.ks[2], ksp * BT, g.lk, p.d, kr);
-        load_regs<T, DP>(vbase, p.vs[2], ksp * BT, g.lk, p.dval, vr);
+        load_regs<T, DP>(vbase, p.vs[2], ksp * BT, g.lk, dval, vr);
     }
     for (int k0 = ksp * BT; k0 < kend; k0 += kstep) {
         __syncthreads();
@@ -591,7 +598,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
         __syncthreads();
         if (k0 + kstep < kend) {  // the next tile's loads overlap this tile's products
             load_regs<T, DP>(kbase, p.ks[2], k0 + kstep, g.lk, p.d, kr);
-            load_regs<T, DP>(vbase, p.vs[2], k0 + kstep, g.lk, p.dval, vr);
+            load_regs<T, DP>(vbase, p.vs[2], k0 + kstep, g.lk, dval, vr);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -755,26 +762,49 @@ const char* check_bwd(const kmi_attn_bwd_args* a) {
 int64_t rows_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q; }
 int64_t keys_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_k : a->batch * a->seq_k; }
 
-// Workgroups the split rules aim for (eight per CU: each backward workgroup runs its items
+// Workgroups the split rules aim for (six per CU: each backward workgroup runs its items
 // with one wavefront per SIMD and two barriers per item, so it is latency-bound; C1
-// backward 143 us at 512, 114 at 1024, 108 at 2048, 116 at 4096), and the split caps.
-constexpr int64_t kBwdTargetWgs = 2048;
+// backward 219 us at 256, 143 at 512, 113 at 1024, 107 at 1536, 113 at 2048, 118 at 4096;
+// every split adds a K/V-sized fp32 partial, so the fewest that keep the time), and the
+// split caps.
+constexpr int64_t kBwdTargetWgs = 1536;
 constexpr int64_t kBwdMaxSplits = 32;
 constexpr int64_t kBwdMaxKsplit = 8;
+
+// KMI_BWD_TARGET_WGS=n (read once; tuning): the workgroup count the split rules aim for.
+int64_t bwd_target_wgs() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("KMI_BWD_TARGET_WGS");
+        const long long n = e ? std::atoll(e) : 0;
+        return n > 0 ? static_cast<int64_t>(n) : kBwdTargetWgs;
+    }();
+    return v;
+}
 
 // dK / dV splits: about kBwdTargetWgs workgroups (at most kBwdMaxSplits splits, at most
 // one per (query head, query block) item).
 int bwd_splits(const kmi_attn_bwd_args* a) {
     const int64_t wgs = a->batch * a->heads_kv * ceil_div(a->seq_k, KW);
     const int64_t items = (a->heads_q / a->heads_kv) * ceil_div(a->seq_q, BT);
-    const int64_t s = std::min<int64_t>(kBwdMaxSplits, std::max<int64_t>(1, ceil_div(kBwdTargetWgs, wgs)));
+    const int64_t s = std::min<int64_t>(kBwdMaxSplits, std::max<int64_t>(1, ceil_div(bwd_target_wgs(), wgs)));
     return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(s, items)));
+}
+
+// KMI_BWD_KSPLIT=n (read once; tuning): pins the dQ key splits.
+int bwd_ksplit_override() {
+    static const int v = [] {
+        const char* e = std::getenv("KMI_BWD_KSPLIT");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
 }
 
 // dQ key splits, by the same rule over (query head, 64-row block) workgroups.
 int bwd_ksplit(const kmi_attn_bwd_args* a) {
+    if (bwd_ksplit_override() > 0)
+        return static_cast<int>(std::min<int64_t>({bwd_ksplit_override(), kBwdMaxKsplit, ceil_div(a->seq_k, BT)}));
     const int64_t wgs = a->batch * a->heads_q * ceil_div(a->seq_q, QW);
-    const int64_t ks = std::min<int64_t>(kBwdMaxKsplit, std::max<int64_t>(1, ceil_div(kBwdTargetWgs, wgs)));
+    const int64_t ks = std::min<int64_t>(kBwdMaxKsplit, std::max<int64_t>(1, ceil_div(bwd_target_wgs(), wgs)));
     return static_cast<int>(std::min<int64_t>(ks, ceil_div(a->seq_k, BT)));
 }
 
@@ -805,12 +835,15 @@ template <typename T, int DP, int MK>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
     const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, QW);
     // dQ first: it writes the row dots that dK / dV read.
-    hipLaunchKernelGGL((attn_bwd_dq<T, DP, MK>),
-                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit)),
-                       dim3(BWD_THREADS), 0, s, p);
-    hipLaunchKernelGGL((attn_bwd_dkdv<T, DP, MK>),
-                       dim3(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hkv * ntk * p.splits)),
-                       dim3(BWD_THREADS), 0, s, p);
+    const dim3 gdq(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit));
+    const dim3 gkv(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hkv * ntk * p.splits));
+    if (p.dval != p.d) {
+        hipLaunchKernelGGL((attn_bwd_dq<T, DP, MK, true>), gdq, dim3(BWD_THREADS), 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_dkdv<T, DP, MK, true>), gkv, dim3(BWD_THREADS), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((attn_bwd_dq<T, DP, MK, false>), gdq, dim3(BWD_THREADS), 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_dkdv<T, DP, MK, false>), gkv, dim3(BWD_THREADS), 0, s, p);
+    }
     const int64_t dq_blocks = p.pdq ? ceil_div(static_cast<int64_t>(p.hq) * p.rows_total * (p.d / 4), 256) : 0;
     const int64_t kv_blocks =
         p.pdk ? ceil_div(static_cast<int64_t>(p.hkv) * p.keys_total * (std::max(p.d, p.dval) / 4), 256) : 0;

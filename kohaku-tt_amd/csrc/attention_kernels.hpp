@@ -1291,6 +1291,23 @@ __device__ __forceinline__ f32x2 load_dev(const float* p) {
                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
+// The 16-byte forms for the partial outputs, through a buffer resource over the whole
+// partial array (the plan keeps it under 2^31 bytes) with the cache policy of those
+// device-scope accesses (sc1).  An 8-byte store costs a whole write transaction of its own
+// (the C3 partials wrote 4.2 MB for 1 MB of data).
+constexpr int kDevScope = 16;  // raw buffer cache-policy bits: sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const AttnParams& p) {
+    return buffer_rsrc(p.part_o, 0x7fffffffu);
+}
+__device__ __forceinline__ void store_dev4(__amdgpu_buffer_rsrc_t r, int64_t elem, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, static_cast<uint32_t>(elem * 4), 0,
+                                           kDevScope);
+}
+__device__ __forceinline__ f32x4 load_dev4(__amdgpu_buffer_rsrc_t r, int64_t elem) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<uint32_t>(elem * 4), 0,
+                                                                          kDevScope));
+}
+
 // Merge of a decode unit's split partials, in split order (deterministic).  Two running
 // merges per row: the splits that met a kept key (masked mode) and the raw-score ones;
 // a row that met a kept key in some split takes the first, a fully masked row the second
@@ -1309,6 +1326,7 @@ __device__ __forceinline__ void decode_merge_unit(const AttnParams& p, const int
     // Splits that are not live load the first live split's record (no per-split branch;
     // their weight is zero).
     const int s_any = live ? __builtin_ctz(live) : 0;
+    const auto pr = part_rsrc(p);
     for (int item = threadIdx.x; item < items; item += NTHREADS) {
         const int rr = item / C4;
         const int c = 4 * (item - rr * C4);
@@ -1326,8 +1344,7 @@ __device__ __forceinline__ void decode_merge_unit(const AttnParams& p, const int
                 const bool use = s < p.splits && ((live >> s) & 1u);
                 const int64_t prow = static_cast<int64_t>(use ? s : s_any) * split_rows + row0;
                 e[j] = load_dev(p.part_lse + 2 * prow);
-                const f32x2 lo = load_dev(p.part_o + prow * D + c), hi = load_dev(p.part_o + prow * D + c + 2);
-                v[j] = f32x4{lo[0], lo[1], hi[0], hi[1]};
+                v[j] = load_dev4(pr, prow * D + c);
                 if (!use) e[j] = f32x2{-INFINITY, 0.f};
             }
             float ck = mk, cr = mr;
@@ -1798,10 +1815,16 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     }
     if (valid) {
         const int64_t prow = (static_cast<int64_t>(split) * p.rows_total + row_base + pos) * p.hq + head;
-        float* dst = p.part_o + prow * D + c0;
+        const auto pr = part_rsrc(p);
 #pragma unroll
-        for (int j = 0; j < PER; j += 2)
-            if (c0 + j < p.dv) store_dev(dst + j, f32x2{acc[j] * inv, acc[j + 1] * inv});
+        for (int j = 0; j < PER; j += (PER % 4 == 0 ? 4 : 2)) {
+            if (c0 + j >= p.dv) continue;  // dv is a multiple of 8: a chunk is in or out
+            if constexpr (PER % 4 == 0) {
+                store_dev4(pr, prow * D + c0 + j, f32x4{acc[j] * inv, acc[j + 1] * inv, acc[j + 2] * inv, acc[j + 3] * inv});
+            } else {
+                store_dev(p.part_o + prow * D + c0 + j, f32x2{acc[j] * inv, acc[j + 1] * inv});
+            }
+        }
         if (wave == 0 && g4 == 0)
             store_dev(p.part_lse + 2 * prow,
                       f32x2{L > 0.f ? M + log2f(L) : -INFINITY, (MASKED && !sel_masked) ? 1.f : 0.f});
