@@ -79,9 +79,19 @@ void* stream_of(const Tensor& t) {
 
 bool mask_given(const optional<Tensor>& m) { return m.has_value() && m->defined(); }
 
-// Head dims the kernels take: multiples of 8 (16-byte rows) up to 256; the kernels pad
-// the head dim to a whole number of 32-wide MFMA blocks with zeros.
-bool head_dim_ok(int64_t d) { return d >= 8 && d <= 256 && d % 8 == 0; }
+// Head dims the ops take: up to 256.  The kernels read 16-byte rows (multiples of 8) and
+// pad to whole 32-wide MFMA blocks with zeros in registers; other head dims are padded
+// with zero columns to a multiple of 8 here (pad_head) and the outputs narrowed back, as
+// the reference's flash pads any head dim to whole tiles (aten_attention.cpp:57-60).
+bool head_dim_ok(int64_t d) { return d >= 1 && d <= 256; }
+
+// `t` with its last dim padded by zero columns to a multiple of 8 (`t` itself when it is
+// one already).  Zero columns of q and k add nothing to the scores and those of v only
+// fill output columns that are dropped.
+Tensor pad_head(const Tensor& t) {
+    const int64_t d = t.size(-1);
+    return d % 8 == 0 ? t : at::constant_pad_nd(t, {0, 8 - d % 8}, 0);
+}
 
 // Tensors whose data the kernels can read: not meta, not fake / functional wrappers
 // (torch.compile and export trace with those; they must take the composite route).
@@ -96,8 +106,8 @@ bool real_data(const Tensor& t) {
 // q/k/v of one float type, fp32 only without gradients (cast to bf16 at entry), no
 // dropout, one head dim, K/V heads dividing Q heads, causal without a mask, a mask that
 // broadcasts to [B, H, Sq, Sk]; plus what these kernels cover: GPU tensors (meta tensors
-// answer by their sizes and dtypes), head dims that are multiples of 8 up to 256,
-// bool / bf16 / f16 / f32 / f64 masks.
+// answer by their sizes and dtypes), head dims up to 256, bool / bf16 / f16 / f32 / f64
+// masks.
 std::string sdpa_refusal_impl(const Tensor& q, const Tensor& k, const Tensor& v, const optional<Tensor>& mask,
                               double dropout_p, bool is_causal) {
     if (!g_attention.load()) return "kohakutt_amd attention is switched off";
@@ -112,7 +122,7 @@ std::string sdpa_refusal_impl(const Tensor& q, const Tensor& k, const Tensor& v,
     if (dropout_p != 0.0) return "dropout";
     const int64_t d = q.size(3);
     if (k.size(3) != d || v.size(3) != d) return "q, k and v need one head dim";
-    if (!head_dim_ok(d)) return "head dim must be a multiple of 8 up to 256";
+    if (!head_dim_ok(d)) return "head dim must be at most 256";
     if (k.size(0) != q.size(0) || v.size(0) != q.size(0) || v.size(1) != k.size(1) || q.size(1) % k.size(1) != 0 ||
         v.size(2) != k.size(2))
         return "q, k and v shapes do not match (K / V heads must divide Q heads)";
@@ -173,7 +183,8 @@ bool head_view(const Tensor& t) {
 // dense [B, S, H D] tensor, so that transposing it back to the projection layout is free.
 Tensor attention_output(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, bool masked, const Tensor& q) {
     const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3);
-    const bool pitched = g_pitched_out && !masked && q_in.scalar_type() == at::kBFloat16 && !q_in.requires_grad() &&
+    const bool pitched = g_pitched_out && !masked && q_in.size(3) == D && q_in.scalar_type() == at::kBFloat16 &&
+                         !q_in.requires_grad() &&
                          !k_in.requires_grad() && !v_in.requires_grad() && head_view(q_in) && head_view(k_in) &&
                          head_view(v_in);
     if (!pitched) return at::empty({B, H, Sq, D}, q.options());
@@ -192,9 +203,10 @@ AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in
         k = k.to(at::kBFloat16);
         v = v.to(at::kBFloat16);
     }
-    q = kernel_operand(q, 2);
-    k = kernel_operand(k, 2);
-    v = kernel_operand(v, 2);
+    const int64_t D0 = q.size(3);  // the caller's head dim (the default scale's)
+    q = kernel_operand(pad_head(q), 2);
+    k = kernel_operand(pad_head(k), 2);
+    v = kernel_operand(pad_head(v), 2);
     const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), D = q.size(3);
     const int64_t Hk = k.size(1), Sk = k.size(2);
     Tensor out = attention_output(q_in, k_in, v_in, mask_given(mask), q);
@@ -220,7 +232,7 @@ AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in
         a.o_stride[i] = out.stride(i);
         a.lse_stride[i] = lse.stride(i);
     }
-    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D));
+    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(D0));
     Tensor m;
     if (mask_given(mask)) {
         m = mask_operand(*mask, q, Sk);
@@ -236,6 +248,7 @@ AttnOut run_attention(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in
     if (ws) work = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
     check(kmi_attn_fwd(&a, ws ? work.data_ptr() : nullptr, ws, stream_of(q)), "kmi_attn_fwd");
     g_attn_calls.fetch_add(1);
+    if (D0 != D) out = out.narrow(3, 0, D0);
     if (fp32) out = out.to(at::kFloat);
     return {out, lse};
 }
@@ -315,9 +328,12 @@ struct BwdCall {
 std::tuple<Tensor, Tensor, Tensor> run_backward(const BwdCall& c) {
     const bool varlen = c.cu_q.defined();
     const int64_t row_dim = varlen ? 0 : 2;
-    const Tensor q = kernel_operand(c.q, row_dim), k = kernel_operand(c.k, row_dim), v = kernel_operand(c.v, row_dim);
-    const Tensor go = kernel_operand(c.grad, row_dim);
-    const Tensor o = kernel_operand(c.out, row_dim);
+    // Head dims that are not multiples of 8 run zero-padded (pad_head); the gradients are
+    // narrowed back below.
+    const Tensor q = kernel_operand(pad_head(c.q), row_dim), k = kernel_operand(pad_head(c.k), row_dim),
+                 v = kernel_operand(pad_head(c.v), row_dim);
+    const Tensor go = kernel_operand(pad_head(c.grad), row_dim);
+    const Tensor o = kernel_operand(pad_head(c.out), row_dim);
     Tensor dq = at::empty(q.sizes(), q.options());
     Tensor dk = at::empty(k.sizes(), k.options());
     Tensor dv = at::empty(v.sizes(), v.options());
@@ -399,7 +415,7 @@ std::tuple<Tensor, Tensor, Tensor> run_backward(const BwdCall& c) {
     Tensor work = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
     check(kmi_attn_bwd(&a, work.data_ptr(), ws, stream_of(q)), "kmi_attn_bwd");
     g_attn_bwd_calls.fetch_add(1);
-    return {dq, dk, dv};
+    return {dq.narrow(-1, 0, c.q.size(-1)), dk.narrow(-1, 0, c.k.size(-1)), dv.narrow(-1, 0, c.v.size(-1))};
 }
 
 std::tuple<Tensor, Tensor, Tensor> flash_backward(const Tensor& grad_out, const Tensor& q, const Tensor& k,
@@ -670,11 +686,16 @@ struct VarlenCall {
 
 // Forward of a packed call: (out [Tq, H, Dv] in the input dtype, lse [H, Tq] fp32).
 std::tuple<Tensor, Tensor> run_varlen(const VarlenCall& c, bool fp32) {
-    const Tensor q = kernel_operand(c.q, 0), k = kernel_operand(c.k, 0), v = kernel_operand(c.v, 0);
+    const Tensor q = kernel_operand(pad_head(c.q), 0), k = kernel_operand(pad_head(c.k), 0),
+                 v = kernel_operand(pad_head(c.v), 0);
     const int64_t Tq = q.size(0), H = q.size(1), D = q.size(2), Dv = v.size(2), Tk = k.size(0);
+    const int64_t Dv0 = c.v.size(2);  // the caller's value dim (v may run zero-padded)
     Tensor out = at::empty({Tq, H, Dv}, q.options());
     Tensor lse = at::empty({H, Tq}, q.options().dtype(at::kFloat));
-    if (Tq == 0) return {fp32 ? out.to(at::kFloat) : out, lse};
+    if (Tq == 0) {
+        if (Dv0 != Dv) out = out.narrow(2, 0, Dv0);
+        return {fp32 ? out.to(at::kFloat) : out, lse};
+    }
     TORCH_CHECK(Tk > 0, "kohakutt_amd: sdpa_varlen: a sequence with queries needs keys");
     kmi_attn_args a{};
     a.q = q.data_ptr();
@@ -726,6 +747,7 @@ std::tuple<Tensor, Tensor> run_varlen(const VarlenCall& c, bool fp32) {
     if (ws) work = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
     check(kmi_attn_fwd(&a, ws ? work.data_ptr() : nullptr, ws, stream_of(q)), "kmi_attn_fwd (varlen)");
     g_attn_calls.fetch_add(1);
+    if (Dv0 != Dv) out = out.narrow(2, 0, Dv0);
     return {fp32 ? out.to(at::kFloat) : out, lse};
 }
 
@@ -744,8 +766,7 @@ void packed_operands(const char* op, const Tensor& q_in, const Tensor& k_in, con
                                     k_in.size(1) > 0 && q_in.size(1) % k_in.size(1) == 0,
                                 "kohakutt_amd: ", op, " q / k / v shapes do not match (K / V heads must divide Q heads)");
     TORCH_CHECK_NOT_IMPLEMENTED(q_in.size(2) == k_in.size(2) && head_dim_ok(q_in.size(2)) && head_dim_ok(v_in.size(2)),
-                                "kohakutt_amd: ", op, " needs q and k of one head dim and head dims that are multiples of 8 "
-                                "up to 256");
+                                "kohakutt_amd: ", op, " needs q and k of one head dim and head dims up to 256");
     fp32 = q_in.scalar_type() == at::kFloat;
     c.q = fp32 ? q_in.to(at::kBFloat16) : q_in;
     c.k = fp32 ? k_in.to(at::kBFloat16) : k_in;

@@ -48,12 +48,12 @@ def test_refusal_answers_on_meta_tensors_with_the_callers_arguments():
     assert torch.ops.ktt.sdpa_refusal(q, k, k, mask, 0.0, False, 0.125) == ""
     assert torch.ops.ktt.sdpa_refusal(q, k, k, mask, 0.0, True, None) == "causal takes no mask"
     assert torch.ops.ktt.sdpa_refusal(q, k, k, None, 0.1, False, None) == "dropout"
-    assert "head dim" in torch.ops.ktt.sdpa_refusal(_meta(1, 2, 8, 60), _meta(1, 2, 8, 60), _meta(1, 2, 8, 60),
-                                                    None, 0.0, False, None)
+    assert "head dim" in torch.ops.ktt.sdpa_refusal(_meta(1, 2, 8, 264), _meta(1, 2, 8, 264),
+                                                    _meta(1, 2, 8, 264), None, 0.0, False, None)
     assert "divide" in torch.ops.ktt.sdpa_refusal(_meta(1, 3, 8, 64), _meta(1, 2, 8, 64), _meta(1, 2, 8, 64),
                                                   None, 0.0, False, None)
-    # head dims: multiples of 8 up to 256
-    for d in (8, 32, 40, 80, 96, 128, 160, 256):
+    # head dims up to 256 (the op layer zero-pads those that are not multiples of 8)
+    for d in (1, 4, 8, 20, 32, 40, 60, 80, 96, 100, 128, 160, 250, 256):
         t = _meta(1, 2, 8, d)
         assert torch.ops.ktt.sdpa_refusal(t, t, t, None, 0.0, False, None) == "", d
     # CPU tensors are refused (the kernels are GPU only)
