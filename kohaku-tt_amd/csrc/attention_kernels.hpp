@@ -1198,13 +1198,16 @@ void attn_fwd_kernel(const AttnParams p) {
         // whose K/V then stay in its L2 instead of every XCD streaming every unit.
         const int x = lin & 7, s = lin >> 3;
         int bh, xi;
-        if (p.xcd_map == 1) {
-            // Unit u on XCD u % 8; within an XCD the query tile rows go heaviest first.
+        if (p.xcd_map == 1 || p.xcd_map == 3) {
+            // Unit u on XCD u % 8; within an XCD the query tile rows go heaviest first
+            // (mode 3: the units of a row rotated by the row, as the plain varlen order).
             const int nxu = (units - x + 7) >> 3;
             if (nxu <= 0) return;
             const int rank = s / nxu;
             if (rank >= p.nx) return;
-            bh = x + 8 * (s - rank * nxu);
+            int slot = s - rank * nxu;
+            if (p.xcd_map == 3) slot = (slot + rank) % nxu;
+            bh = x + 8 * slot;
             xi = p.causal ? p.nx - 1 - rank : rank;
         } else {
             // The unit-major query tiles, one contiguous chunk per XCD.
@@ -1965,8 +1968,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
             wsum > 0.f ? (m + log2f(wsum)) * kLn2 + (any_masked ? 0.f : kMaskedLogit) : -INFINITY;
 }
 
-// KMI_ATTN_XCD_MAP (read once): 0 keeps the plain workgroup order everywhere, 1 also
-// orders causal / varlen grids by XCD; unset: non-causal dense grids only.
+// KMI_ATTN_XCD_MAP (read once): 0 keeps the plain workgroup order everywhere; 1 and 3 also
+// order dense causal grids by XCD (1 without the per-row unit rotation); unset: by XCD for
+// non-causal dense grids (mode 2) and varlen grids (mode 3).
 inline int xcd_map_mode() {
     static const int v = [] {
         const char* e = std::getenv("KMI_ATTN_XCD_MAP");
@@ -2007,12 +2011,13 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
         p.npair = static_cast<int>(std::min<int64_t>(ceil_div(extra, units), p.nx / 2));
         grid -= static_cast<int64_t>(p.npair) * units;
     }
-    // XCD-aware order for non-causal dense grids whose units' K/V exceed an XCD's 4 MB L2:
-    // each XCD takes a contiguous chunk of the unit-major query tiles (C5 self: 149 -> 47
-    // MB of L2 misses for 42 MB of data, 140 -> 136 us).  Causal and varlen grids keep the
-    // plain order: unit u on XCD u % 8 cut C4's misses 352 -> 54 MB but ran 63 -> 73 us
-    // (its misses were served by the MALL, not what bounded it); KMI_ATTN_XCD_MAP=1 asks
-    // for it.
+    // XCD-aware order for grids whose units' K/V exceed an XCD's 4 MB L2.  Non-causal dense
+    // grids: each XCD takes a contiguous chunk of the unit-major query tiles (C5 self: 149
+    // -> 47 MB of L2 misses for 42 MB of data, 140 -> 136 us).  Varlen grids: unit u on XCD
+    // u % 8, query tile rows heaviest first with each row's units rotated by the row (C4:
+    // 61 -> 54 us, masked 127 -> 114 us; without the rotation 71 and 153 us, the in-order
+    // dispatch then meets the same few units' work row after row).  Dense causal grids keep
+    // the plain (snake) order unless KMI_ATTN_XCD_MAP asks.
     p.xcd_map = 0;
     p.snake = 0;
     if (p.causal && !p.cu_q && p.splits == 1 && p.npair == 0 && slots > 0 && grid <= slots) p.snake = cu_count();
@@ -2020,8 +2025,9 @@ hipError_t launch_fwd(const AttnParams& p_in, int64_t grid, hipStream_t stream) 
     const int64_t kv_bytes = units * static_cast<int64_t>(p.seq_k) * (p.d + p.dv) * static_cast<int64_t>(sizeof(T));
     if (!RS && p.splits == 1 && p.npair == 0 && kv_bytes > (int64_t{4} << 20) && xcd_map_mode() != 0) {
         if (p.cu_q || p.causal) {
-            if (units >= 8 && xcd_map_mode() == 1) {
-                p.xcd_map = 1;
+            const int mode = xcd_map_mode() == 2 ? (p.cu_q ? 3 : 0) : xcd_map_mode();
+            if (units >= 8 && (mode == 1 || mode == 3)) {
+                p.xcd_map = mode;
                 p.snake = 0;
                 grid = 8 * ceil_div(units, 8) * static_cast<int64_t>(p.nx);
             }

@@ -73,8 +73,9 @@ struct AttnParams {
     int nx;  // query tiles per (sequence, K/V head)
     int npair;  // causal: the 2 npair shortest query tiles of a unit run two per workgroup
     // Workgroup order across the XCDs (block b runs on XCD b % 8): 0 the plain order; 1
-    // unit u on XCD u % 8, query tiles heaviest first; 2 the unit-major query tiles in one
-    // contiguous chunk per XCD.  Either keeps a unit's K/V in the L2 of one or two XCDs.
+    // unit u on XCD u % 8, query tiles heaviest first; 3 the same with each tile row's units
+    // rotated by the row; 2 the unit-major query tiles in one contiguous chunk per XCD.
+    // Each keeps a unit's K/V in the L2 of one or two XCDs.
     int xcd_map;
     // Causal grids resident in one round: the CU count n (0: off).  Blocks b, b + n, b + 2n
     // ... run on one CU, so the heaviest-first rank order runs forward in even rounds of n
