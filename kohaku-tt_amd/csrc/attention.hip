@@ -121,6 +121,12 @@ Plan make_plan(const kmi_attn_args* a) {
     if (a->mask_mode != KMI_MASK_NONE) nqb = std::min(nqb, dp == 64 ? 2 : 1);
     const int forced = nqb_override();
     if (nqb_allowed(dp, forced, a->mask_mode != KMI_MASK_NONE)) nqb = forced;
+    // K or V rows that overlap in memory (a row stride below the head dim, from an
+    // as_strided view) take the 16-row variants, whose tile loads read each row in full
+    // (the LDS DMA variants' ranges assume whole strides per row).
+    const bool overlap = (a->k_stride[2] > 0 && a->k_stride[2] < a->head_dim) ||
+                         (a->v_stride[2] > 0 && a->v_stride[2] < value_dim(a));
+    if (overlap) nqb = 1;
     pl.nqb = nqb;
     const int64_t bm = 16 * pl.nqb;
     pl.nx = static_cast<int>(ceil_div(vrows, bm));
@@ -167,6 +173,7 @@ Plan make_plan(const kmi_attn_args* a) {
     if (!pl.decode && pl.splits == 1 && !a->causal && a->mask_mode == KMI_MASK_NONE && nk <= 8 && dp <= 128) {
         int q = dp == 64 ? (ceil_div(vrows, 256) * units >= 512 ? 4 : 2) : 1;
         if (nqb_allowed(dp, forced, false)) q = forced;
+        if (overlap) q = 1;
         const int64_t nx_rs = ceil_div(vrows, NWAVES * 16 * q);
         if (nx_rs * units >= 256) {
             pl.rs = true;

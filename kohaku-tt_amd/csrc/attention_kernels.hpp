@@ -389,7 +389,10 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
                                                       static_cast<int64_t>(k0) * p.vs[2]);
     const uint32_t k_lane = KD ? static_cast<uint32_t>(l16 * kstride + 16 * g4) : static_cast<uint32_t>(krow * kstride + 16 * dgc);
     const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dgcv);
-    // Bytes per key of a resource's range (a zero row stride repeats one row).
+    // Bytes per key of the DMA variants' ranges (rows x span; the host keeps rows that
+    // overlap off them; a zero row stride repeats one row).  The other tile loads' ranges
+    // end with the last row's data (rows_extent), so rows that overlap, as in an
+    // as_strided view with a row stride below the head dim, are read in full.
     const uint32_t kspan = static_cast<uint32_t>(kstride > 0 ? kstride : p.d * static_cast<int64_t>(sizeof(T)));
     const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : p.dv * static_cast<int64_t>(sizeof(T)));
     T* kl = reinterpret_cast<T*>(smem) + wave * S::TILE;
@@ -445,6 +448,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
             const int key0 = tt * TW;
             const int rows_here = min(lk - key0, TW);
             const int64_t stride = V ? vstride : kstride;
+            // Rows of `stride` bytes (the host keeps rows that overlap off these variants).
             const auto rs = buffer_rsrc((V ? vunit : kunit) + key0 * stride,
                                         static_cast<uint32_t>(rows_here) * (V ? vspan : kspan));
             T* const dst = V ? vd2 : kd2;
@@ -493,7 +497,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // per-lane offsets from being precomputed into registers held across the loop.
     auto load_k = [&](int t, KRegs& kr) {
         const int key0 = t * TW;
-        const auto rs = buffer_rsrc(kunit + key0 * kstride, static_cast<uint32_t>(min(lk - key0, TW)) * kspan);
+        const auto rs = buffer_rsrc(kunit + key0 * kstride, rows_extent(min(lk - key0, TW), static_cast<uint32_t>(kstride), static_cast<uint32_t>(p.d * sizeof(T))));
         uint32_t step = static_cast<uint32_t>(kstride);
         __asm__ volatile("" : "+s"(step));
         if constexpr (KD) {
@@ -523,7 +527,7 @@ __device__ __forceinline__ void attn_block(const AttnParams& p, const int split,
     // V rows and mask values of tile t.
     auto load_v = [&](int t) {
         const int key0 = t * TW;
-        const auto rs = buffer_rsrc(vunit + key0 * vstride, static_cast<uint32_t>(min(lk - key0, TW)) * vspan);
+        const auto rs = buffer_rsrc(vunit + key0 * vstride, rows_extent(min(lk - key0, TW), static_cast<uint32_t>(vstride), static_cast<uint32_t>(p.dv * sizeof(T))));
         uint32_t step = static_cast<uint32_t>(vstride);
         __asm__ volatile("" : "+s"(step));
 #pragma unroll
@@ -1528,8 +1532,8 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     const bool kpad = p.d < D;
     const uint32_t k_lane = static_cast<uint32_t>(l16 * kstride + 16 * g4);
     const uint32_t v_lane = static_cast<uint32_t>(krow * vstride + 16 * dgc);
-    const uint32_t kspan = static_cast<uint32_t>(kstride > 0 ? kstride : p.d * static_cast<int64_t>(sizeof(T)));
-    const uint32_t vspan = static_cast<uint32_t>(vstride > 0 ? vstride : p.dv * static_cast<int64_t>(sizeof(T)));
+    // Resources end with the last row's data (overlapping rows read in full).
+    const uint32_t krow_b = static_cast<uint32_t>(p.d * sizeof(T)), vrow_b = static_cast<uint32_t>(p.dv * sizeof(T));
     T* vl = reinterpret_cast<T*>(smem) + wave * WN * VP;
 
     // One tile's registers: K fragments, the V rows this lane stages, the mask values.
@@ -1538,9 +1542,9 @@ __global__ __launch_bounds__(NTHREADS) void attn_decode_kernel(const AttnParams 
     MRaw mpre[MASKED ? KB : 1][4];
     auto load_tile = [&](int i) {
         const int key0 = (slot + i * nslots) * WN;
-        const uint32_t rows = static_cast<uint32_t>(min(lk - key0, WN));
-        const auto rk = buffer_rsrc(kunit + key0 * kstride, rows * kspan);
-        const auto rv = buffer_rsrc(vunit + key0 * vstride, rows * vspan);
+        const int rows = min(lk - key0, WN);
+        const auto rk = buffer_rsrc(kunit + key0 * kstride, rows_extent(rows, static_cast<uint32_t>(kstride), krow_b));
+        const auto rv = buffer_rsrc(vunit + key0 * vstride, rows_extent(rows, static_cast<uint32_t>(vstride), vrow_b));
         uint32_t kst = static_cast<uint32_t>(kstride), vst = static_cast<uint32_t>(vstride);
         __asm__ volatile("" : "+s"(kst), "+s"(vst));
 #pragma unroll

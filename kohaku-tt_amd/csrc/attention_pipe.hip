@@ -45,6 +45,14 @@ constexpr int PWAVE_BYTES = std::max<int>(2 * PKT * 2, PB * PCP * 4);
 template <int NW>
 constexpr size_t pipe_lds_bytes() { return static_cast<size_t>(NW) * (PWAVE_BYTES + PB * 8); }
 
+// Maximum of a lane's eight scores of one row block, shaped for three v_max3_f32 and one
+// v_max_f32 (the kernels never see NaN scores).
+__device__ __forceinline__ float lane_max8(const f32x4& a, const f32x4& b) {
+    const float t0 = fmaxf(fmaxf(a[0], a[1]), a[2]);
+    const float t1 = fmaxf(fmaxf(a[3], b[0]), b[1]);
+    return fmaxf(fmaxf(fmaxf(t0, t1), b[2]), b[3]);
+}
+
 // Key tiles of query tile xt of a unit: (ntiles, nfull); [0, nfull) are visible to every
 // row (no mask), [nfull, ntiles) need the per-element causal / key-tail test.
 template <bool CAUSAL>
@@ -133,11 +141,12 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
     const uint32_t vstride = static_cast<uint32_t>(p.vs[2] * static_cast<int64_t>(sizeof(T)));
     const char* kunit = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + seq * p.ks[0] + kvh * p.ks[1]);
     const char* vunit = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + seq * p.vs[0] + kvh * p.vs[1]);
-    // Bytes per key of a resource's range (a zero row stride repeats one row).
-    const uint32_t kspan = kstride > 0 ? kstride : PD * static_cast<uint32_t>(sizeof(T));
-    const uint32_t vspan = vstride > 0 ? vstride : PD * static_cast<uint32_t>(sizeof(T));
-    const auto krs = buffer_rsrc(kunit, static_cast<uint32_t>(lk) * kspan);
-    const auto vrs = buffer_rsrc(vunit, static_cast<uint32_t>(lk) * vspan);
+    // A resource's range ends with the unit's last key row, so the rows of a partial last
+    // tile past it read as zeros (their keys are masked on edge tiles and their P is 0);
+    // a zero row stride repeats one row.
+    const uint32_t row_bytes = PD * static_cast<uint32_t>(sizeof(T));
+    const auto krs = buffer_rsrc(kunit, rows_extent(lk, kstride, row_bytes));
+    const auto vrs = buffer_rsrc(vunit, rows_extent(lk, vstride, row_bytes));
     // Lane offsets of DMA instruction i depend on the parity of i only (the swizzles of rows
     // 8 i + a do); the row term 8 i * stride is added to the scalar offset.
     uint32_t dko[2], dvo[2];
@@ -160,32 +169,17 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
 #pragma unroll
         for (int d = 0; d < 4; ++d) vtro[d] = r * PD + 8 * (((2 * d) ^ vswz(r)) | ((l16 >> 1) & 1)) + 4 * (l16 & 1);
     }
-    // One operand of tile tt into its LDS tile.  A partial last tile repeats its last key
-    // row (finite values; those keys are masked), so every lane reads in range and every
-    // slot is written.
+    // One operand of tile tt into its LDS tile (a partial last tile's rows past the last
+    // key arrive as zeros: out of the resource's range).
     auto dma = [&](int tt, bool V) {
-        const int key0 = tt * PT;
         const uint32_t stride = V ? vstride : kstride;
         const auto rs = V ? vrs : krs;
         T* const dst = V ? vl : kl;
-        if (key0 + PT <= lk) {
-            const int soff = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(key0) * stride));
+        const int soff = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(tt * PT) * stride));
 #pragma unroll
-            for (int i = 0; i < PT / 8; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 512), 16,
-                                                         V ? dvo[i & 1] : dko[i & 1],
-                                                         soff + static_cast<int>(8 * i * stride), 0, 0);
-        } else {
-            const int last = lk - 1;
-#pragma unroll
-            for (int i = 0; i < PT / 8; ++i) {
-                const int r = 8 * i + (lane >> 3);
-                const uint32_t rr = static_cast<uint32_t>(min(key0 + r, last));
-                const uint32_t off = rr * stride + 16u * static_cast<uint32_t>((lane & 7) ^ (V ? vswz(r) : kswz(r)));
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 512), 16,
-                                                         off, 0, 0, 0);
-            }
-        }
+        for (int i = 0; i < PT / 8; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 512), 16,
+                                                     V ? dvo[i & 1] : dko[i & 1], soff + static_cast<int>(8 * i * stride), 0, 0);
     };
 
     // Running state: O^T accumulators, row sums as MFMA columns (P times a column of
@@ -206,15 +200,18 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
         }
     }
     float c2 = p.scale_log2;
-    if (c2 < 0.f) {
-        // A negative scale flips Q's sign (exact), so the multiplier is positive and a
-        // larger score is a larger logit.
-        c2 = -c2;
+    // A negative scale flips Q's sign (exact), so the multiplier is positive and a larger
+    // score is a larger logit.  Applied once the first tile's loads are out: the test waits
+    // for the scale's scalar load, which then overlaps their flight.
+    auto fix_sign = [&] {
+        if (c2 < 0.f) {
+            c2 = -c2;
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int c = 0; c < 2; ++c) qf[b][c] = __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, qf[b][c]) ^ 0x80008000u);
-    }
+                for (int c = 0; c < 2; ++c) qf[b][c] = __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, qf[b][c]) ^ 0x80008000u);
+        }
+    };
 
     auto read_k = [&](v8 (&kf)[2][2]) {
 #pragma unroll
@@ -256,11 +253,8 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
     auto rescale = [&](const f32x4 (&s)[2][2]) -> bool {
         float lmax[2];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            lmax[b] = fmaxf(fmaxf(s[0][b][0], s[0][b][1]), fmaxf(s[0][b][2], s[0][b][3]));
-            lmax[b] = fmaxf(lmax[b], fmaxf(fmaxf(s[1][b][0], s[1][b][1]), fmaxf(s[1][b][2], s[1][b][3])));
-        }
-        if (__builtin_amdgcn_ballot_w64(fmaxf(lmax[0] - m_thr[0], lmax[1] - m_thr[1]) > 0.f)) {
+        for (int b = 0; b < 2; ++b) lmax[b] = lane_max8(s[0][b], s[1][b]);
+        if (__builtin_amdgcn_ballot_w64((lmax[0] > m_thr[0]) | (lmax[1] > m_thr[1]))) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 const float rmax = row_max4(lmax[b]);
@@ -304,6 +298,9 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
         if (nt_w > 0) {
             dma(tile_of(0), false);
             dma(tile_of(0), true);
+        }
+        fix_sign();
+        if (nt_w > 0) {
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
             v8 kf[2][2];
             read_k(kf);
@@ -374,6 +371,7 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
             dma(tile_of(0), false);
             dma(tile_of(0), true);
         }
+        fix_sign();
         auto load_step = [&](const int j, f32x4 (&s)[2][2], v8 (&vf)[4]) {
             const int t = tile_of(j);
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -399,9 +397,7 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
             load_step(0, s, vf);
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                float lmax = fmaxf(fmaxf(s[0][b][0], s[0][b][1]), fmaxf(s[0][b][2], s[0][b][3]));
-                lmax = fmaxf(lmax, fmaxf(fmaxf(s[1][b][0], s[1][b][1]), fmaxf(s[1][b][2], s[1][b][3])));
-                const float rmax = row_max4(lmax);
+                const float rmax = row_max4(lane_max8(s[0][b], s[1][b]));
                 const bool seen = rmax > -INFINITY;
                 m_run[b] = seen ? rmax * c2 : -INFINITY;
                 m_thr[b] = seen ? rmax + kLazy / c2 : -INFINITY;
@@ -517,6 +513,11 @@ __device__ __forceinline__ void pipe_combine(const AttnParams& p, const int bh, 
 template <typename T, bool CAUSAL, int NW, bool PIPE>
 __global__ __launch_bounds__(NW * kWave, PIPE ? 3 : 4) void attn_pipe_kernel(const AttnParams p) {
     extern __shared__ __align__(16) unsigned char smem[];
+    // Read one word of each 64-byte argument line the kernel uses, all in one batch: the
+    // compiler splits the argument loads into batches by use (the workgroup mapping, then
+    // the tile's pointers and strides, then the scale), each a round trip before the first
+    // K / V loads go out; with the lines in the scalar cache the later batches hit it.
+    __asm__ volatile("" ::"s"(p.q), "s"(p.ks[0]), "s"(p.os[0]), "s"(p.batch), "s"(p.fd_units.m));
     const int units = p.batch * p.hkv;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     int lin = blockIdx.x;

@@ -31,6 +31,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
+// Bytes from the first of `rows` rows at `stride` bytes to the end of the last one's
+// `row_bytes` of data (0 for no rows).  Ranges built from it read every row in full, also
+// rows that overlap (a stride below the row's data), and read zeros past the last row.
+__device__ __forceinline__ uint32_t rows_extent(int rows, uint32_t stride, uint32_t row_bytes) {
+    return rows > 0 ? static_cast<uint32_t>(rows - 1) * stride + row_bytes : 0u;
+}
+
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
 }

@@ -456,6 +456,42 @@ def test_broadcast_key_rows_and_partial_tiles(native, dev, sk, d, causal):
     assert err.max() < 1e-2, err.max()
 
 
+@pytest.mark.parametrize("sk,causal", [(100, True), (77, False)])
+def test_overlapping_key_rows(native, dev, sk, causal):
+    """K and V rows that overlap in memory (a row stride of 32 elements at head dim 64, as
+    an as_strided view makes): every key row is read in full, including the last, whose
+    end lies 32 elements past the start of the row after it; the result equals the
+    oracle on the materialised K/V."""
+    from kohakutt_amd import capi
+
+    b, hq, hk, sq, d, rs = 1, 4, 2, 96, 64, 32
+    g = C.gen(800 + sk)
+    q = C.randn(g, b, hq, sq, d)
+    kb, vb = C.randn(g, b * hk * (sk * rs + d)), C.randn(g, b * hk * (sk * rs + d))
+    shape, stride = (b, hk, sk, d), (hk * (sk * rs + d), sk * rs + d, rs, 1)
+    k, v = kb.as_strided(shape, stride), vb.as_strided(shape, stride)
+    qd = q.to(dev)
+    kbd, vbd = kb.to(dev), vb.to(dev)
+    kd, vd = kbd.as_strided(shape, stride), vbd.as_strided(shape, stride)
+    out = torch.empty_like(qd)
+    a = capi.AttnArgs(
+        q=qd.data_ptr(), k=kd.data_ptr(), v=vd.data_ptr(), out=out.data_ptr(), lse=0,
+        dtype=capi.KMI_BF16, causal=int(causal), batch=b, heads_q=hq, heads_kv=hk, seq_q=sq, seq_k=sk,
+        head_dim=d, scale=d**-0.5,
+    )
+    a.q_stride[:] = qd.stride()[:3]
+    a.k_stride[:] = kd.stride()[:3]
+    a.v_stride[:] = vd.stride()[:3]
+    a.o_stride[:] = out.stride()[:3]
+    n = capi.workspace_bytes(a)
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=dev)
+    capi.attn_fwd(a, ws.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    kc, vc = k.contiguous(), v.contiguous()
+    ref, _ = oatt.sdpa(C.f64(q), C.f64(kc), C.f64(vc), is_causal=causal)
+    _check(out.cpu(), C.torch_cpu_sdpa(q, kc, vc, None, causal, d**-0.5), ref, f"overlapping rows sk={sk}")
+
+
 @pytest.mark.parametrize("b,s,h,hk,d,causal", [(2, 197, 12, 12, 64, False), (1, 300, 8, 2, 128, True)])
 def test_head_view_inputs_give_a_projection_layout_output(native, dev, b, s, h, hk, d, causal):
     """q, k, v as head views of [B, S, C] projections (a fused qkv for MHA, separate q and
