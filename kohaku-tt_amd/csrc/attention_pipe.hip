@@ -116,16 +116,20 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
         const int rr = r < r_end ? r : r_begin;
         return CAUSAL ? min(lk, fdiv(rr, p.fd_group) + 1) : lk;
     };
+    // Issued after the first tile's K / V loads (which need only scalar set-up and two
+    // lane offsets), so that those go out first.
+    auto load_q = [&] {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const int r = r_begin + 16 * b + l16;
-        const int rr = r < r_end ? r : r_begin;
-        const int pos = fdiv(rr, p.fd_group);
-        const int head = kvh * G + (rr - pos * G);
-        const T* src = qp + seq * p.qs[0] + head * p.qs[1] + static_cast<int64_t>(pos) * p.qs[2];
+        for (int b = 0; b < 2; ++b) {
+            const int r = r_begin + 16 * b + l16;
+            const int rr = r < r_end ? r : r_begin;
+            const int pos = fdiv(rr, p.fd_group);
+            const int head = kvh * G + (rr - pos * G);
+            const T* src = qp + seq * p.qs[0] + head * p.qs[1] + static_cast<int64_t>(pos) * p.qs[2];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) qf[b][c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
-    }
+            for (int c = 0; c < 2; ++c) qf[b][c] = *reinterpret_cast<const v8*>(src + 32 * c + 8 * g4);
+        }
+    };
 
     // K / V tiles by LDS DMA (buffer loads with the lds modifier), 16-byte chunks
     // XOR-swizzled per row so that K's fragment reads and V's transposed reads hit
@@ -169,17 +173,28 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
 #pragma unroll
         for (int d = 0; d < 4; ++d) vtro[d] = r * PD + 8 * (((2 * d) ^ vswz(r)) | ((l16 >> 1) & 1)) + 4 * (l16 & 1);
     }
-    // One operand of tile tt into its LDS tile (a partial last tile's rows past the last
-    // key arrive as zeros: out of the resource's range).
+    // One operand of tile tt into its LDS tile.  Full tiles carry their row offsets in the
+    // scalar offset.  The last, partial tile carries them in the lane offset, to which the
+    // hardware's range check applies: its rows past the last key read as zeros (those keys
+    // are masked and their P is 0).
     auto dma = [&](int tt, bool V) {
         const uint32_t stride = V ? vstride : kstride;
         const auto rs = V ? vrs : krs;
         T* const dst = V ? vl : kl;
         const int soff = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(tt * PT) * stride));
+        if ((tt + 1) * PT <= lk) {
 #pragma unroll
-        for (int i = 0; i < PT / 8; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 512), 16,
-                                                     V ? dvo[i & 1] : dko[i & 1], soff + static_cast<int>(8 * i * stride), 0, 0);
+            for (int i = 0; i < PT / 8; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 512), 16,
+                                                         V ? dvo[i & 1] : dko[i & 1], soff + static_cast<int>(8 * i * stride),
+                                                         0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < PT / 8; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs, (__attribute__((address_space(3))) void*)(dst + i * 512), 16,
+                    (V ? dvo[i & 1] : dko[i & 1]) + static_cast<uint32_t>(soff) + 8u * i * stride, 0, 0, 0);
+        }
     };
 
     // Running state: O^T accumulators, row sums as MFMA columns (P times a column of
@@ -203,6 +218,9 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
     // A negative scale flips Q's sign (exact), so the multiplier is positive and a larger
     // score is a larger logit.  Applied once the first tile's loads are out: the test waits
     // for the scale's scalar load, which then overlaps their flight.
+    // The lazy-rescale margin in raw-score units (a hardware reciprocal: any margin near
+    // kLazy / c2 keeps the exponents bounded).
+    float lazy_raw = 0.f;
     auto fix_sign = [&] {
         if (c2 < 0.f) {
             c2 = -c2;
@@ -211,6 +229,7 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
 #pragma unroll
                 for (int c = 0; c < 2; ++c) qf[b][c] = __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, qf[b][c]) ^ 0x80008000u);
         }
+        lazy_raw = kLazy * __builtin_amdgcn_rcpf(c2);
     };
 
     auto read_k = [&](v8 (&kf)[2][2]) {
@@ -263,7 +282,7 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
                 const float alpha = move ? __builtin_amdgcn_exp2f(m_run[b] - mt) : 1.f;  // 0 while m was -inf
                 if (move) {
                     m_run[b] = mt;
-                    m_thr[b] = rmax + kLazy / c2;
+                    m_thr[b] = rmax + lazy_raw;
                     neg_m[b] = -mt;
                 }
                 lacc[b] *= alpha;
@@ -283,10 +302,13 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
             pf[4 + i] = static_cast<T>(e1);
         }
     };
-    auto pv = [&](const v8 (&vf)[4], int b, const v8& pf) {
-        v8 ones;  // rebuilt per use from scalar constants: no registers held across the loop
+    // The row-sum MFMA's column of ones, held in four VGPRs across the loop (the empty asm
+    // keeps the compiler from rebuilding it from scalar constants at every use).
+    v8 ones;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ones[j] = static_cast<T>(1.f);
+    for (int j = 0; j < 8; ++j) ones[j] = static_cast<T>(1.f);
+    __asm__ volatile("" : "+v"(ones));
+    auto pv = [&](const v8 (&vf)[4], int b, const v8& pf) {
         lacc[b] = Mfma<T>::run(ones, pf, lacc[b]);
 #pragma unroll
         for (int d = 0; d < 4; ++d) o[d][b] = Mfma<T>::run(vf[d], pf, o[d][b]);
@@ -299,6 +321,7 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
             dma(tile_of(0), false);
             dma(tile_of(0), true);
         }
+        load_q();
         fix_sign();
         if (nt_w > 0) {
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -371,6 +394,7 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
             dma(tile_of(0), false);
             dma(tile_of(0), true);
         }
+        load_q();
         fix_sign();
         auto load_step = [&](const int j, f32x4 (&s)[2][2], v8 (&vf)[4]) {
             const int t = tile_of(j);
@@ -400,7 +424,7 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
                 const float rmax = row_max4(lane_max8(s[0][b], s[1][b]));
                 const bool seen = rmax > -INFINITY;
                 m_run[b] = seen ? rmax * c2 : -INFINITY;
-                m_thr[b] = seen ? rmax + kLazy / c2 : -INFINITY;
+                m_thr[b] = seen ? rmax + lazy_raw : -INFINITY;
                 neg_m[b] = seen ? -m_run[b] : 0.f;
             }
             v8 pf[2];
@@ -408,9 +432,6 @@ __device__ __forceinline__ void pipe_tile(const AttnParams& p, const int bh, con
             probs(s, 1, pf[1]);
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                v8 ones;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ones[e] = static_cast<T>(1.f);
                 lacc[b] = Mfma<T>::run(ones, pf[b], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                 for (int d = 0; d < 4; ++d) o[d][b] = Mfma<T>::run(vf[d], pf[b], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -484,7 +505,10 @@ __device__ __forceinline__ void pipe_combine(const AttnParams& p, const int bh, 
         hi += *reinterpret_cast<const f32x4*>(ow + 4 * ((2 * cg + 1) ^ (row & 15))) * wt;
     }
     if (r >= vrows) return;
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    // lt >= 1 when a row saw a key (the wavefront whose reference point is the row's
+    // maximum contributes exp2(0) = 1 at weight 1): the hardware reciprocal and log2 are
+    // used without range reduction (the output is rounded to 16 bits).
+    const float inv = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;
     const int pos = fdiv(r, p.fd_group);
     const int head = kvh * G + (r - pos * G);
     typedef T v8o __attribute__((ext_vector_type(8)));
@@ -499,7 +523,7 @@ __device__ __forceinline__ void pipe_combine(const AttnParams& p, const int bh, 
     *reinterpret_cast<v8o*>(dst) = w8;
     if (p.lse && cg == 0)
         p.lse[seq * p.ls[0] + head * p.ls[1] + static_cast<int64_t>(pos) * p.ls[2]] =
-            lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+            lt > 0.f ? (m + __builtin_amdgcn_logf(lt)) * kLn2 : -INFINITY;
 }
 
 // Workgroup -> group of query tiles.  Four wavefronts: one query tile per workgroup, in
