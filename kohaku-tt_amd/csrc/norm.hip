@@ -593,18 +593,22 @@ __global__ __launch_bounds__(kNormBwdWaves * kWave) void norm_bwd_rows(const T* 
             if constexpr (HB) ab[i][j] = 0.f;
         }
     const float inv_w = 1.f / static_cast<float>(width);
-    // This wavefront's rows r0 + wave, r0 + wave + kNormBwdWaves, ...: the next row's dy and x are
-    // requested before the current row is worked on.
+    // This wavefront's rows r0 + wave, r0 + wave + kNormBwdWaves, ...: the next row's dy, x and
+    // statistics are requested before the current row is worked on (the statistics read in
+    // the row's own iteration cost every row a round trip).
     int voff[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) voff[i] = min(lane + kWave * i, nvec - 1) * E;
     u32x4 nx_x[VPL], nx_g[VPL];
+    float nx_m = 0.f, nx_r = 0.f;
     if (r0 + wave < r1) {
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
             nx_x[i] = *reinterpret_cast<const u32x4*>(x + (r0 + wave) * width + voff[i]);
             nx_g[i] = *reinterpret_cast<const u32x4*>(dy + (r0 + wave) * width + voff[i]);
         }
+        if constexpr (LAYER) nx_m = mean[r0 + wave];
+        nx_r = rstd[r0 + wave];
     }
     for (int64_t row = r0 + wave; row < r1; row += kNormBwdWaves) {
         u32x4 rx[VPL], rg[VPL];
@@ -612,17 +616,19 @@ __global__ __launch_bounds__(kNormBwdWaves * kWave) void norm_bwd_rows(const T* 
             rx[i] = nx_x[i];
             rg[i] = nx_g[i];
         }
+        const float m = nx_m, r = nx_r;
         if (row + kNormBwdWaves < r1) {
 #pragma unroll
             for (int i = 0; i < VPL; ++i) {
                 nx_x[i] = *reinterpret_cast<const u32x4*>(x + (row + kNormBwdWaves) * width + voff[i]);
                 nx_g[i] = *reinterpret_cast<const u32x4*>(dy + (row + kNormBwdWaves) * width + voff[i]);
             }
+            if constexpr (LAYER) nx_m = mean[row + kNormBwdWaves];
+            nx_r = rstd[row + kNormBwdWaves];
         }
 #pragma unroll
         for (int i = 0; i < VPL; ++i)
             if (lane + kWave * i >= nvec) rx[i] = rg[i] = u32x4{0u, 0u, 0u, 0u};
-        const float m = LAYER ? mean[row] : 0.f, r = rstd[row];
         float sg = 0.f, sgx = 0.f;
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
