@@ -19,6 +19,11 @@
 #include <type_traits>
 
 namespace kmi {
+namespace fwd {
+// Split counters shared with the decode merge (attention.hip): zero-initialised device
+// words, one slab per stream, left zero by every use (null: none free).
+unsigned long long* decode_counters(hipStream_t stream, int64_t units);
+}  // namespace fwd
 namespace {
 
 // Row-block grids.  HIP bounds each grid dimension at 2^32 - 1 work-items, which one
@@ -564,7 +569,7 @@ int64_t rms_bwd_chunks(int64_t rows) {
 // VPL 16-byte vectors per lane, reduces mean(g) and mean(g xh) across its lanes, writes dx
 // and adds dy xh (and dy) into per-lane column sums.  The wavefronts' column sums
 // meet in LDS in wavefront order and the block writes one partial row pair;
-// norm_bwd_colsum adds the blocks' partials in block order (deterministic, no atomics).
+// norm_bwd_colsum_parts adds the blocks' partials in a fixed order (deterministic).
 // Wavefronts per block of the one-pass backward (eight measured slower: C5 LayerNorm's
 // row pass 14.9 -> 23 us).
 constexpr int kNormBwdWaves = 4;
@@ -696,27 +701,38 @@ __global__ __launch_bounds__(kNormBwdWaves * kWave) void norm_bwd_rows(const T* 
     }
 }
 
-// dw (and db) from the blocks' partial rows: 64 columns per block, 16 lanes over the
-// partial rows (lane l takes rows l, l + 16, ... -- at most 32 of them, all loaded in one
-// round: a loop of dependent rounds made this pass as long as the row pass), their sums
-// added in lane order.
+// dw (and db) from the blocks' partial rows, in two levels in one launch: workgroup
+// (chunk of 64 columns, part p) adds the blocks of its part (blocks p * per .. + per - 1):
+// 16 lanes per column over them (lane l takes blocks l, l + 16, ..., all loaded in one
+// round: a loop of dependent rounds made one-level sums as long as the row pass), their
+// sums added in lane order, and stores the part's sums with device-scope stores; the last
+// of a chunk's kColsumParts workgroups to count itself in (a split counter, zero between
+// calls) adds the parts in part order and clears the word.  Eight parts: with one workgroup per
+// chunk reading every block's partial, C5 LayerNorm's backward took 19.0 us, not 17.9.
 constexpr int kColsumRowsPerLane = 32;  // norm_bwd_blocks() <= 16 * this
-__global__ __launch_bounds__(1024) void norm_bwd_colsum(const float* part, void* dw, void* db, int w_dtype,
-                                                        int b_dtype, int nblocks, int width) {
+constexpr int kColsumParts = 8;
+__global__ __launch_bounds__(1024) void norm_bwd_colsum_parts(const float* part, float* lvl, unsigned long long* ctr,
+                                                              void* dw, void* db, int w_dtype, int b_dtype,
+                                                              int nblocks, int width) {
     __shared__ float red[2][16][64];
-    const int c = blockIdx.x * 64 + (threadIdx.x & 63), l = threadIdx.x >> 6;
+    __shared__ int last;
+    const int cx = blockIdx.x, pi = blockIdx.y;
+    const int c = cx * 64 + (threadIdx.x & 63), l = threadIdx.x >> 6;
+    const int per = (nblocks + kColsumParts - 1) / kColsumParts;
+    const int b0 = pi * per, b1 = min(nblocks, b0 + per);
     float sw = 0.f, sb = 0.f;
     if (c < width) {
-        float vw[kColsumRowsPerLane], vb[kColsumRowsPerLane];
+        constexpr int KMAX = kColsumRowsPerLane / kColsumParts + 1;  // per <= 16 * KMAX
+        float vw[KMAX], vb[KMAX];
 #pragma unroll
-        for (int i = 0; i < kColsumRowsPerLane; ++i) {
-            const int b = min(l + 16 * i, nblocks - 1);
+        for (int i = 0; i < KMAX; ++i) {
+            const int b = min(b0 + l + 16 * i, nblocks - 1);
             vw[i] = part[static_cast<int64_t>(b) * 2 * width + c];
             vb[i] = db ? part[static_cast<int64_t>(b) * 2 * width + width + c] : 0.f;
         }
 #pragma unroll
-        for (int i = 0; i < kColsumRowsPerLane; ++i) {
-            if (l + 16 * i < nblocks) {
+        for (int i = 0; i < KMAX; ++i) {
+            if (b0 + l + 16 * i < b1) {
                 sw += vw[i];
                 sb += vb[i];
             }
@@ -732,9 +748,47 @@ __global__ __launch_bounds__(1024) void norm_bwd_colsum(const float* part, void*
             tw += red[0][i][threadIdx.x];
             tb += red[1][i][threadIdx.x];
         }
-        if (dw) store_any(dw, w_dtype, c, tw);
-        if (db) store_any(db, b_dtype, c, tb);
+        uint32_t* lp = reinterpret_cast<uint32_t*>(lvl + static_cast<int64_t>(pi) * 2 * width);
+        __hip_atomic_store(lp + c, __builtin_bit_cast(uint32_t, tw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(lp + width + c, __builtin_bit_cast(uint32_t, tb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (!ctr) return;  // the parts are added by norm_bwd_colsum_finish
+    // The part's sums are complete device-wide before it counts itself in.
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long n = __hip_atomic_fetch_add(ctr + cx, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+        const bool is_last = n == static_cast<unsigned long long>(kColsumParts);
+        if (is_last) __hip_atomic_store(ctr + cx, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = is_last ? 1 : 0;
+    }
+    __syncthreads();
+    if (!last || l != 0 || c >= width) return;
+    float tw = 0.f, tb = 0.f;
+#pragma unroll
+    for (int q = 0; q < kColsumParts; ++q) {
+        const uint32_t* lp = reinterpret_cast<const uint32_t*>(lvl + static_cast<int64_t>(q) * 2 * width);
+        tw += __builtin_bit_cast(float, __hip_atomic_load(lp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        tb += __builtin_bit_cast(float, __hip_atomic_load(lp + width + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    if (dw) store_any(dw, w_dtype, c, tw);
+    if (db) store_any(db, b_dtype, c, tb);
+}
+
+// Second launch of the two-level column sums when no split counters are free: the same
+// additions in the same order as norm_bwd_colsum_parts' last workgroup.
+__global__ __launch_bounds__(256) void norm_bwd_colsum_finish(const float* lvl, void* dw, void* db, int w_dtype,
+                                                              int b_dtype, int width) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= width) return;
+    float tw = 0.f, tb = 0.f;
+#pragma unroll
+    for (int q = 0; q < kColsumParts; ++q) {
+        tw += lvl[static_cast<int64_t>(q) * 2 * width + c];
+        tb += lvl[static_cast<int64_t>(q) * 2 * width + width + c];
+    }
+    if (dw) store_any(dw, w_dtype, c, tw);
+    if (db) store_any(db, b_dtype, c, tb);
 }
 
 // Blocks of the one-pass backward: about two per CU, whole wavefront rows each.
@@ -743,6 +797,11 @@ int64_t norm_bwd_blocks(int64_t rows) {
 }
 int64_t norm_bwd_rows_per_block(int64_t rows) {
     return ceil_div(ceil_div(rows, norm_bwd_blocks(rows)), kNormBwdWaves) * kNormBwdWaves;
+}
+// Workspace floats of the one-pass backward: the blocks' partial rows, then the column
+// sums' per-part rows.
+int64_t norm_bwd_part_floats(int64_t rows, int64_t width) {
+    return (2 * norm_bwd_blocks(rows) + 2 * kColsumParts) * width;
 }
 
 // The vector lanes the one-pass backward needs for a row (0 when it does not apply: the
@@ -796,8 +855,14 @@ hipError_t launch_norm_bwd(const void* dy, const void* x, const float* mean, con
 #undef KMI_BWD_LAUNCH
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || (!dw && !db)) return err;
-    hipLaunchKernelGGL(norm_bwd_colsum, dim3(static_cast<unsigned>(ceil_div(width, 64))), dim3(1024), 0, s, part, dw,
-                       db, w_dtype, b_dtype, static_cast<int>(nb), width);
+    const int64_t chunks = ceil_div(width, 64);
+    float* lvl = part + 2 * nb * width;
+    unsigned long long* ctr = fwd::decode_counters(s, chunks);
+    hipLaunchKernelGGL(norm_bwd_colsum_parts, dim3(static_cast<unsigned>(chunks), kColsumParts), dim3(1024), 0, s, part,
+                       lvl, ctr, dw, db, w_dtype, b_dtype, static_cast<int>(nb), width);
+    if (!ctr)
+        hipLaunchKernelGGL(norm_bwd_colsum_finish, dim3(static_cast<unsigned>(ceil_div(width, 256))), dim3(256), 0, s,
+                           lvl, dw, db, w_dtype, b_dtype, width);
     return hipGetLastError();
 }
 
@@ -908,7 +973,7 @@ extern "C" int kmi_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t width, siz
     if (rows < 0 || width < 0) return fail(KMI_EINVAL, "kmi_rms_norm_bwd_workspace_bytes: negative size");
     // Enough for either path: the one-pass kernel's per-block partial rows or the
     // row-chunk column sums of the element path.
-    const int64_t n = std::max(rms_bwd_chunks(rows), 2 * norm_bwd_blocks(rows)) * width;
+    const int64_t n = std::max(rms_bwd_chunks(rows) * width, norm_bwd_part_floats(rows, width));
     *bytes = rows == 0 ? 0 : static_cast<size_t>(n) * sizeof(float);
     return KMI_OK;
 }
@@ -917,7 +982,7 @@ extern "C" int kmi_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t width, s
     using namespace kmi;
     if (!bytes) return fail(KMI_EINVAL, "kmi_layer_norm_bwd_workspace_bytes: null bytes");
     if (rows < 0 || width < 0) return fail(KMI_EINVAL, "kmi_layer_norm_bwd_workspace_bytes: negative size");
-    *bytes = rows == 0 ? 0 : static_cast<size_t>(2 * norm_bwd_blocks(rows) * width) * sizeof(float);
+    *bytes = rows == 0 ? 0 : static_cast<size_t>(norm_bwd_part_floats(rows, width)) * sizeof(float);
     return KMI_OK;
 }
 
@@ -943,7 +1008,7 @@ extern "C" int kmi_layer_norm_bwd(const void* dy, const void* x, const float* me
     if (vpl == 0)
         return fail(KMI_EUNSUPPORTED, std::string(name) + ": rows must be whole 16-byte vectors (16-byte aligned, "
                                                           "at most 256 vectors) with weight in x's dtype or fp32");
-    const size_t need = static_cast<size_t>(2 * norm_bwd_blocks(rows) * width) * sizeof(float);
+    const size_t need = static_cast<size_t>(norm_bwd_part_floats(rows, width)) * sizeof(float);
     if ((dweight || dbias) && (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 4))
         return fail(KMI_EWORKSPACE, std::string(name) + ": workspace missing or smaller than "
                                                         "kmi_layer_norm_bwd_workspace_bytes");
@@ -970,7 +1035,7 @@ extern "C" int kmi_rms_norm_bwd(const void* dy, const void* x, const void* weigh
     if (rows > (int64_t{1} << 31) || width > (int64_t{1} << 30))
         return fail(KMI_EUNSUPPORTED, std::string(name) + ": too many rows or too wide");
     const int64_t chunks = rms_bwd_chunks(rows);
-    const size_t need = static_cast<size_t>(std::max(chunks, 2 * norm_bwd_blocks(rows)) * width) * sizeof(float);
+    const size_t need = static_cast<size_t>(std::max(chunks * width, norm_bwd_part_floats(rows, width))) * sizeof(float);
     if (dweight && (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 4))
         return fail(KMI_EWORKSPACE, std::string(name) + ": workspace missing or smaller than "
                                                         "kmi_rms_norm_bwd_workspace_bytes");

@@ -163,9 +163,10 @@ def test_rms_norm_backward_rejects_malformed_calls_before_launch():
     lib = capi.lib()
     n = ctypes.c_size_t()
     assert lib.kmi_rms_norm_bwd_workspace_bytes(2048, 896, ctypes.byref(n)) == capi.KMI_OK
-    # the larger of the one-pass kernel's partial rows (2 x 512 blocks of four rows) and
-    # the element path's 16-row chunks (128) of fp32 column sums
-    assert n.value == max(2 * 512, 128) * 896 * 4
+    # the larger of the one-pass kernel's partial rows (2 x 512 blocks of four rows, then
+    # 2 x 8 rows of per-part column sums) and the element path's 16-row chunks (128) of
+    # fp32 column sums
+    assert n.value == max(2 * 512 + 2 * 8, 128) * 896 * 4
     assert lib.kmi_rms_norm_bwd_workspace_bytes(-1, 896, ctypes.byref(n)) == capi.KMI_EINVAL
     p = 0x1000
     # Unknown dtype, null operands, dweight without weight, missing workspace.
@@ -182,9 +183,10 @@ def test_layer_norm_backward_rejects_malformed_calls_before_launch():
     lib = capi.lib()
     n = ctypes.c_size_t()
     assert lib.kmi_layer_norm_bwd_workspace_bytes(8192, 640, ctypes.byref(n)) == capi.KMI_OK
-    assert n.value == 2 * 512 * 640 * 4  # dweight and dbias partial rows of 512 blocks
+    # dweight and dbias partial rows of 512 blocks, then of the column sums' 8 parts
+    assert n.value == (2 * 512 + 2 * 8) * 640 * 4
     assert lib.kmi_layer_norm_bwd_workspace_bytes(3, 640, ctypes.byref(n)) == capi.KMI_OK
-    assert n.value == 2 * 1 * 640 * 4
+    assert n.value == (2 * 1 + 2 * 8) * 640 * 4
     p = 0x1000
     bf = capi.KMI_BF16
     call = lib.kmi_layer_norm_bwd

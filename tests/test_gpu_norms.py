@@ -228,6 +228,36 @@ def test_layer_norm_backward_kernel(native, dev, shape, x_dtype, w_dtype, has_bi
     assert all(torch.equal(a, b2) for a, b2 in zip(got, again))
 
 
+def test_norm_backward_column_sums_are_the_same_on_every_stream(native, dev):
+    """dweight / dbias add their blocks' partials in two levels: in one launch (the last
+    part of a column chunk to finish adds the parts, found by a per-stream counter that it
+    clears) on up to 16 streams, and in a second launch with the same additions beyond
+    them: twenty streams in turn, each called twice, give bit-identical gradients."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(4096, 640, generator=g) * 2 + 0.3).bfloat16().to(dev)
+    gy = torch.randn(4096, 640, generator=g).bfloat16().to(dev)
+    w = (1 + 0.1 * torch.randn(640, generator=g)).bfloat16().to(dev)
+    b = (0.1 * torch.randn(640, generator=g)).bfloat16().to(dev)
+
+    def run():
+        xx, ww, bb = (t.detach().clone().requires_grad_() for t in (x, w, b))
+        F.layer_norm(xx, (640,), ww, bb, 1e-5).backward(gy)
+        rr, rw = xx.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
+        F.rms_norm(rr, (640,), rw, 1e-6).backward(gy)
+        return [xx.grad, ww.grad, bb.grad, rr.grad, rw.grad]
+
+    first = run()
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(20)]
+    for i, s in enumerate(streams):
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for rep in range(2):
+                got = run()
+                s.synchronize()
+                assert all(torch.equal(a, f) for a, f in zip(got, first)), (i, rep)
+
+
 @pytest.mark.parametrize("case", ["x_offset_1", "weight_slice_bf16", "weight_slice_f32"])
 def test_layer_norm_backward_misaligned_operands(native, dev, case):
     """A contiguous x at storage offset 1 and a weight sliced at offset 4 from a flat
