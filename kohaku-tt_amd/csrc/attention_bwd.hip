@@ -8,17 +8,18 @@
 // mask (the forward's modes), GQA, any head dim that is a multiple of 8 up to 256 (padded
 // to DP with zeros in registers), bf16 / fp16:
 //
-//   attn_bwd_dq      one workgroup per (sequence, query head, 64-row block): the row dots
-//                    Dr = sum_d dO O (fp32, kept for the next kernel), then over the key
+//   attn_bwd_rowdot  the row dots Dr = sum_d dO O (fp32) of every query row and head
+//   attn_bwd_grads   one launch of both gradient passes, their workgroups interleaved:
+//     dQ             per (sequence, query head, 64-row block, key split): over the key
 //                    tiles it sees P = exp2(c S + mask - lse2), dP = dO V^T,
 //                    dS = P (dP - Dr), dQ += dS K
-//   attn_bwd_dkdv    one workgroup per (sequence, K/V head, 64-key tile, split): over the
-//                    (query head of the group, 32-row query block) items that see the
-//                    tile -- split s takes items s, s + splits, ... -- the same P / dS;
-//                    dV += P^T dO, dK += dS^T Q in fp32 registers.  One split: it
-//                    writes dK / dV; several: fp32 partials per split that
+//     dK / dV        per (sequence, K/V head, 64-key tile, split): over the (query head
+//                    of the group, 32-row query block) items that see the tile -- split
+//                    s takes items s, s + splits, ... -- the same P / dS; dV += P^T dO,
+//                    dK += dS^T Q in fp32 registers.  One split: it writes dK / dV;
+//                    several: fp32 partials per split that
 //   attn_bwd_sums    adds in split order (no atomics: repeat calls are bit-identical),
-//                    together with attn_bwd_dq's key-split dQ partials
+//                    together with the key-split dQ partials
 //
 // Probabilities follow the forward exactly: keys past the causal limit or masked
 // (logit <= -5e5) get P = 0; a row whose lse carries the -5e5 offset of a fully-masked
@@ -260,7 +261,7 @@ __device__ __forceinline__ u32x4 frag(const T* base, int64_t rs, int row, int nr
 constexpr int KW = 64;
 
 template <typename T, int DP, int MK, bool DV>
-__global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) {
+__device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid) {
     typedef typename BwdMfma<T>::v8 v8;
     // v / dO / out width: a separate value dim only in the DV instances (one width keeps
     // the equal-dim kernels' registers).
@@ -278,9 +279,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4, l16 = lane & 15;
     const int ntk = (p.seq_k + KW - 1) / KW;
-    const int split = blockIdx.x % p.splits;
-    const int tile = (blockIdx.x / p.splits) % ntk;
-    const int bkv = blockIdx.x / (p.splits * ntk);  // (sequence, K/V head)
+    const int split = bid % p.splits;
+    const int tile = (bid / p.splits) % ntk;
+    const int bkv = bid / (p.splits * ntk);  // (sequence, K/V head)
     const int seq = bkv / p.hkv, kvh = bkv - seq * p.hkv;
     const Geo g = geo_of(p, seq);
     const int kt0 = tile * KW;
@@ -459,6 +460,45 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dkdv(const BwdParams p) 
 // Partials a sum kernel loads before it adds them.
 constexpr int kSumBatch = 8;
 
+// dQ: a workgroup takes QW query rows (16 per wavefront).
+constexpr int QW = 64;
+
+// The row dots D = sum(dO * O) (fp32) of every query row and head, for both gradient
+// kernels, which run concurrently: one workgroup per (sequence, query head, QW-row block),
+// lane (g4, l16) of wavefront w taking row 16 w + l16, dims 32 c + 8 g4 .. + 7 (the dQ
+// kernel's fragment layout), the four lanes of a row added by two butterflies.
+template <typename T, int DP, bool DV>
+__global__ __launch_bounds__(BWD_THREADS) void attn_bwd_rowdot(const BwdParams p) {
+    typedef typename BwdMfma<T>::v8 v8;
+    const int dval = DV ? p.dval : p.d;
+    constexpr int DC = DP / 32;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g4 = lane >> 4, l16 = lane & 15;
+    const int nqb = (p.seq_q + QW - 1) / QW;
+    const int qb = blockIdx.x % nqb;
+    const int bh = blockIdx.x / nqb;
+    const int seq = bh / p.hq, h = bh - seq * p.hq;
+    const Geo g = geo_of(p, seq);
+    const int row = qb * QW + 16 * wave + l16;
+    if (qb * QW >= g.lq) return;
+    const T* dp = static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
+    const T* op = static_cast<const T*>(p.o) + g.ob + h * p.os[1] + static_cast<int64_t>(g.q0) * p.os[2];
+    float rdot = 0.f;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+        const int col = 32 * c + 8 * g4;
+        const v8 dv = __builtin_bit_cast(v8, frag(dp, p.dos[2], row, g.lq, col, dval));
+        const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], row, g.lq, col, dval));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rdot += to_f32(dv[e]) * to_f32(yv[e]);
+    }
+    rdot += __shfl_xor(rdot, 16, kWave);
+    rdot += __shfl_xor(rdot, 32, kWave);
+    if (g4 == 0 && row < g.lq) p.dr[h * p.rows_total + g.row_base + row] = rdot;
+}
+
+
 // dK / dV rows from the splits' fp32 partials, added in split order.  One item per
 // (K/V head, key row, 4 head-dim columns).
 template <typename T, int DP>
@@ -513,10 +553,9 @@ __device__ __forceinline__ void kv_sum_item(const BwdParams& p, const int64_t it
 // and dO fragments in registers (the A operands of S = Q K^T and dP = dO V^T).  Per
 // 32-key tile the workgroup stages K and V (row-major) once; each wavefront
 // forms dS of its rows, passes it through its own LDS rows and accumulates dQ += dS K.
-constexpr int QW = 64;
 
 template <typename T, int DP, int MK, bool DV>
-__global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
+__device__ __forceinline__ void attn_bwd_dq(const BwdParams& p, const int bid) {
     typedef typename BwdMfma<T>::v8 v8;
     // v / dO / out width: a separate value dim only in the DV instances (one width keeps
     // the equal-dim kernels' registers).
@@ -531,9 +570,9 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4, l16 = lane & 15;
     const int nqb = (p.seq_q + QW - 1) / QW;
-    const int ksp = blockIdx.x % p.ksplit;
-    const int qb = (blockIdx.x / p.ksplit) % nqb;
-    const int bh = blockIdx.x / (p.ksplit * nqb);
+    const int ksp = bid % p.ksplit;
+    const int qb = (bid / p.ksplit) % nqb;
+    const int bh = bid / (p.ksplit * nqb);
     const int seq = bh / p.hq, h = bh - seq * p.hq;
     const int kvh = h / p.group;
     const Geo g = geo_of(p, seq);
@@ -542,29 +581,19 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     const int rw0 = r0 + 16 * wave;  // this wavefront's first row
 
     // Q / dO fragments: lane (g4, l16) holds row rw0 + l16, dims 32 c + 8 g4 .. + 7; the
-    // row statistics of rows rw0 + 4 g4 + j (the rows of its accumulator lanes).  The row
-    // dot D = sum(dO * O) is formed here from the same dO fragments and written for the
-    // dK / dV kernel, which runs after this one.
+    // row statistics and row dots (attn_bwd_rowdot's) of rows rw0 + 4 g4 + j (the rows of
+    // its accumulator lanes).
     v8 qf[DC], of[DC];
-    float rdot = 0.f;
     {
         const T* qp = static_cast<const T*>(p.q) + g.qb + h * p.qs[1] + static_cast<int64_t>(g.q0) * p.qs[2];
         const T* dp = static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
-        const T* op = static_cast<const T*>(p.o) + g.ob + h * p.os[1] + static_cast<int64_t>(g.q0) * p.os[2];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
             const int col = 32 * c + 8 * g4;
             qf[c] = __builtin_bit_cast(v8, frag(qp, p.qs[2], rw0 + l16, g.lq, col, p.d));
             of[c] = __builtin_bit_cast(v8, frag(dp, p.dos[2], rw0 + l16, g.lq, col, dval));
-            const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], rw0 + l16, g.lq, col, dval));
-#pragma unroll
-            for (int e = 0; e < 8; ++e) rdot += to_f32(of[c][e]) * to_f32(yv[e]);
         }
     }
-    // The four lanes of a row (g4 = 0..3) each hold a quarter of its dims.
-    rdot += __shfl_xor(rdot, 16, kWave);
-    rdot += __shfl_xor(rdot, 32, kWave);
-    if (ksp == 0 && g4 == 0 && rw0 + l16 < g.lq) p.dr[h * p.rows_total + g.row_base + rw0 + l16] = rdot;
     float l2[4], drv[4];
     bool raw[4];
 #pragma unroll
@@ -572,7 +601,7 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
         const int row = rw0 + 4 * g4 + j;
         const int rc = min(row, g.lq - 1);
         const float lv = p.lse[g.lb + h * p.ls[1] + static_cast<int64_t>(g.q0 + rc) * p.ls[2]];
-        const float dv = __shfl(rdot, 4 * g4 + j, kWave);  // lane 4 g4 + j holds that row's dot
+        const float dv = p.dr[h * p.rows_total + g.row_base + rc];
         row_stats(lv, row < g.lq, l2[j], raw[j]);
         drv[j] = row < g.lq ? dv : 0.f;
     }
@@ -669,6 +698,28 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_dq(const BwdParams p) {
     }
 }
 
+// Both gradient passes in one launch (they read the same inputs and the row dots, and
+// neither reads the other's output), their workgroups interleaved in proportion (block b
+// is dQ workgroup floor(b n_dq / n) when that count steps at b, else a dK / dV workgroup),
+// so that the two kinds share every CU from the start.
+// Workgroups per CU the fused kernel keeps resident (the register budget it compiles to,
+// without spills): those of the dK / dV kernel alone at head dims 64 and 128 for the
+// unmasked equal-dim variants, one fewer for masked or value-dim ones.
+constexpr int bwd_min_blocks(int dp, bool plain) {
+    return dp <= 64 ? (plain ? 4 : 3) : (dp <= 128 ? (plain ? 3 : 2) : 1);
+}
+
+template <typename T, int DP, int MK, bool DV>
+__global__ __launch_bounds__(BWD_THREADS, bwd_min_blocks(DP, MK == MK_NONE && !DV)) void attn_bwd_grads(
+    const BwdParams p, const int kv_blocks, const int dq_blocks) {
+    const int64_t b = blockIdx.x, n = static_cast<int64_t>(kv_blocks) + dq_blocks;
+    const int q0 = static_cast<int>(b * dq_blocks / n), q1 = static_cast<int>((b + 1) * dq_blocks / n);
+    if (q1 > q0)
+        attn_bwd_dq<T, DP, MK, DV>(p, q0);
+    else
+        attn_bwd_dkdv<T, DP, MK, DV>(p, static_cast<int>(b) - q0);
+}
+
 // dQ rows from the key splits' fp32 partials, in split order.  One item per (query head,
 // query row, 4 head-dim columns).
 template <typename T, int DP>
@@ -762,32 +813,36 @@ const char* check_bwd(const kmi_attn_bwd_args* a) {
 int64_t rows_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_q : a->batch * a->seq_q; }
 int64_t keys_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->total_k : a->batch * a->seq_k; }
 
-// Workgroups the split rules aim for (six per CU: each backward workgroup runs its items
-// with one wavefront per SIMD and two barriers per item, so it is latency-bound; C1
-// backward 219 us at 256, 143 at 512, 113 at 1024, 107 at 1536, 113 at 2048, 118 at 4096;
-// every split adds a K/V-sized fp32 partial, so the fewest that keep the time), and the
-// split caps.
-constexpr int64_t kBwdTargetWgs = 1536;
+// Split rules.  dK / dV and dQ workgroups run interleaved in one launch, so each kind
+// needs enough work per workgroup to amortise its set-up and few enough splits to keep
+// the fp32 partials small, rather than a grid that fills the chip alone.  A dK / dV
+// workgroup takes at most kBwdItemsPerWg (query head, 32-row block) items when splitting
+// allows it, a dQ workgroup at most kBwdTilesPerWg 32-key tiles; below
+// kBwdMinWgs workgroups of a kind, splits go down to kBwdMinItems items (or tiles) each.
+// Measured on C1 / C4 varlen (us, split target of the former per-kind rule): 108 / 254 at
+// 512 workgroups, 95 / 255 at 768, 96 / 255 at 1024, 102 / 214 at 1536, 107 / 216 at
+// 2048, 111 / 229 at 3072; C1 is best at 12-16 dK / dV splits with 2-3 dQ key splits, C4
+// at 2 dK / dV splits (64 items per workgroup unsplit) and none for dQ.
+constexpr int64_t kBwdItemsPerWg = 32;
+constexpr int64_t kBwdTilesPerWg = 32;
+constexpr int64_t kBwdMinWgs = 512;
+constexpr int64_t kBwdMinItems = 8;
 constexpr int64_t kBwdMaxSplits = 32;
 constexpr int64_t kBwdMaxKsplit = 8;
 
-// KMI_BWD_TARGET_WGS=n (read once; tuning): the workgroup count the split rules aim for.
-int64_t bwd_target_wgs() {
-    static const int64_t v = [] {
-        const char* e = std::getenv("KMI_BWD_TARGET_WGS");
-        const long long n = e ? std::atoll(e) : 0;
-        return n > 0 ? static_cast<int64_t>(n) : kBwdTargetWgs;
-    }();
-    return v;
+// Splits of `units` workgroups of `work` items (or tiles) each under the rules above,
+// `per_wg` the kind's bound.
+int64_t bwd_split_count(int64_t units, int64_t work, int64_t per_wg, int64_t cap) {
+    const int64_t by_work = ceil_div(work, per_wg);
+    const int64_t by_fill = std::min(ceil_div(kBwdMinWgs, std::max<int64_t>(1, units)), ceil_div(work, kBwdMinItems));
+    return std::max<int64_t>(1, std::min<int64_t>({cap, std::max(by_work, by_fill), std::max<int64_t>(1, work)}));
 }
 
-// dK / dV splits: about kBwdTargetWgs workgroups (at most kBwdMaxSplits splits, at most
-// one per (query head, query block) item).
+// dK / dV splits over the (query head of the group, 32-row block) items of a key tile.
 int bwd_splits(const kmi_attn_bwd_args* a) {
     const int64_t wgs = a->batch * a->heads_kv * ceil_div(a->seq_k, KW);
     const int64_t items = (a->heads_q / a->heads_kv) * ceil_div(a->seq_q, BT);
-    const int64_t s = std::min<int64_t>(kBwdMaxSplits, std::max<int64_t>(1, ceil_div(bwd_target_wgs(), wgs)));
-    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(s, items)));
+    return static_cast<int>(bwd_split_count(wgs, items, kBwdItemsPerWg, kBwdMaxSplits));
 }
 
 // KMI_BWD_KSPLIT=n (read once; tuning): pins the dQ key splits.
@@ -799,13 +854,13 @@ int bwd_ksplit_override() {
     return v;
 }
 
-// dQ key splits, by the same rule over (query head, 64-row block) workgroups.
+// dQ key splits over the 32-key tiles of a (query head, 64-row block).
 int bwd_ksplit(const kmi_attn_bwd_args* a) {
+    const int64_t tiles = ceil_div(a->seq_k, BT);
     if (bwd_ksplit_override() > 0)
-        return static_cast<int>(std::min<int64_t>({bwd_ksplit_override(), kBwdMaxKsplit, ceil_div(a->seq_k, BT)}));
+        return static_cast<int>(std::min<int64_t>({bwd_ksplit_override(), kBwdMaxKsplit, tiles}));
     const int64_t wgs = a->batch * a->heads_q * ceil_div(a->seq_q, QW);
-    const int64_t ks = std::min<int64_t>(kBwdMaxKsplit, std::max<int64_t>(1, ceil_div(bwd_target_wgs(), wgs)));
-    return static_cast<int>(std::min<int64_t>(ks, ceil_div(a->seq_k, BT)));
+    return static_cast<int>(bwd_split_count(wgs, tiles, kBwdTilesPerWg, kBwdMaxKsplit));
 }
 
 // Workspace floats: row dot products (padded to 16 bytes); with GQA or splits the dK / dV
@@ -834,15 +889,19 @@ size_t bwd_ws_bytes(const kmi_attn_bwd_args* a) {
 template <typename T, int DP, int MK>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t s) {
     const int64_t ntk = ceil_div(p.seq_k, KW), nqb = ceil_div(p.seq_q, QW);
-    // dQ first: it writes the row dots that dK / dV read.
-    const dim3 gdq(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit));
-    const dim3 gkv(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hkv * ntk * p.splits));
+    // The row dots first (both gradient passes read them), then dK / dV and dQ in one grid.
+    const dim3 grd(static_cast<unsigned>(static_cast<int64_t>(p.batch) * p.hq * nqb));
+    const int64_t ndq = static_cast<int64_t>(p.batch) * p.hq * nqb * p.ksplit;
+    const int64_t nkv = static_cast<int64_t>(p.batch) * p.hkv * ntk * p.splits;
+    const dim3 grid(static_cast<unsigned>(nkv + ndq));
     if (p.dval != p.d) {
-        hipLaunchKernelGGL((attn_bwd_dq<T, DP, MK, true>), gdq, dim3(BWD_THREADS), 0, s, p);
-        hipLaunchKernelGGL((attn_bwd_dkdv<T, DP, MK, true>), gkv, dim3(BWD_THREADS), 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_rowdot<T, DP, true>), grd, dim3(BWD_THREADS), 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_grads<T, DP, MK, true>), grid, dim3(BWD_THREADS), 0, s, p, static_cast<int>(nkv),
+                           static_cast<int>(ndq));
     } else {
-        hipLaunchKernelGGL((attn_bwd_dq<T, DP, MK, false>), gdq, dim3(BWD_THREADS), 0, s, p);
-        hipLaunchKernelGGL((attn_bwd_dkdv<T, DP, MK, false>), gkv, dim3(BWD_THREADS), 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_rowdot<T, DP, false>), grd, dim3(BWD_THREADS), 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_grads<T, DP, MK, false>), grid, dim3(BWD_THREADS), 0, s, p, static_cast<int>(nkv),
+                           static_cast<int>(ndq));
     }
     const int64_t dq_blocks = p.pdq ? ceil_div(static_cast<int64_t>(p.hq) * p.rows_total * (p.d / 4), 256) : 0;
     const int64_t kv_blocks =

@@ -154,8 +154,16 @@ def test_backward_rejects_malformed_calls_before_launch():
     a.heads_kv = 2
     n = ctypes.c_size_t()
     assert capi.lib().kmi_attn_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == capi.KMI_OK
-    # fp32 row dot products, then (GQA) the dK / dV partials of every query head.
-    assert n.value == (4 * 8 + 2 * 4 * 8 * 64) * 4
+    # fp32 row dot products only: each key tile sees two (query head, row block) items,
+    # below the eight a split needs, so dK / dV are written directly (no partials).
+    assert n.value == 4 * 8 * 4
+    # Longer rows split: 2048 query rows give 7 x 64 items per key tile of C1's GQA,
+    # fourteen splits of 32 each (fp32 dK and dV partials per K/V head and split), and
+    # 64 key tiles per dQ workgroup two key splits (fp32 dQ partials per head and split).
+    a.heads_q, a.heads_kv, a.seq_q, a.seq_k = 14, 2, 2048, 2048
+    assert capi.lib().kmi_attn_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == capi.KMI_OK
+    assert n.value == (14 * 2048 + 2 * (2 * 14 * 2048 * 64) + 14 * 2 * 2048 * 64) * 4
+    a.heads_q, a.heads_kv, a.seq_q, a.seq_k = 4, 2, 8, 8
     assert capi.lib().kmi_attn_bwd(ctypes.byref(a), None, 0, None) == capi.KMI_EWORKSPACE
 
 
