@@ -38,7 +38,6 @@ namespace kmi {
 namespace {
 
 constexpr int BT = 32;          // keys per K/V tile and rows per query block
-constexpr int TP = BT + 8;      // pitch of transposed / [32][32] tiles (elements)
 constexpr int PP = 24;          // pitch of a wavefront's [32][16] P / dS tiles (elements)
 constexpr int BWD_THREADS = 256;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -463,41 +462,51 @@ constexpr int kSumBatch = 8;
 // dQ: a workgroup takes QW query rows (16 per wavefront).
 constexpr int QW = 64;
 
-// The row dots D = sum(dO * O) (fp32) of every query row and head, for both gradient
-// kernels, which run concurrently: one workgroup per (sequence, query head, QW-row block),
-// lane (g4, l16) of wavefront w taking row 16 w + l16, dims 32 c + 8 g4 .. + 7 (the dQ
-// kernel's fragment layout), the four lanes of a row added by two butterflies.
+// The row dots D = sum(dO * O) (fp32) of every query row and head, read by both gradient
+// passes, which run concurrently: one workgroup per (sequence, query head, QW-row block),
+// 16 rows per wavefront.  A row's CH = dval / 8 16-byte chunks go to CP (CH rounded up to
+// a power of two) adjacent lanes, so that each load instruction reads whole rows
+// contiguously; the lanes' partial dots meet in a butterfly over those CP lanes.
 template <typename T, int DP, bool DV>
 __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_rowdot(const BwdParams p) {
-    typedef typename BwdMfma<T>::v8 v8;
     const int dval = DV ? p.dval : p.d;
-    constexpr int DC = DP / 32;
+    constexpr int CP = DP / 8 > 16 ? 32 : (DP / 8 > 8 ? 16 : (DP / 8 > 4 ? 8 : 4));  // lanes per row (>= DP / 8)
+    constexpr int RPI = kWave / CP;  // rows per load instruction
+    constexpr int NI = 16 / RPI;     // instructions for the wavefront's 16 rows
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int g4 = lane >> 4, l16 = lane & 15;
     const int nqb = (p.seq_q + QW - 1) / QW;
     const int qb = blockIdx.x % nqb;
     const int bh = blockIdx.x / nqb;
     const int seq = bh / p.hq, h = bh - seq * p.hq;
     const Geo g = geo_of(p, seq);
-    const int row = qb * QW + 16 * wave + l16;
     if (qb * QW >= g.lq) return;
     const T* dp = static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
     const T* op = static_cast<const T*>(p.o) + g.ob + h * p.os[1] + static_cast<int64_t>(g.q0) * p.os[2];
-    float rdot = 0.f;
+    const int c = lane % CP;
+    const int row0 = qb * QW + 16 * wave + lane / CP;
+    u32x4 dv[NI], ov[NI];
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
-        const int col = 32 * c + 8 * g4;
-        const v8 dv = __builtin_bit_cast(v8, frag(dp, p.dos[2], row, g.lq, col, dval));
-        const v8 yv = __builtin_bit_cast(v8, frag(op, p.os[2], row, g.lq, col, dval));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) rdot += to_f32(dv[e]) * to_f32(yv[e]);
+    for (int i = 0; i < NI; ++i) {
+        const int row = min(row0 + RPI * i, g.lq - 1);
+        const int col = min(8 * c, dval - 8);
+        dv[i] = *reinterpret_cast<const u32x4*>(dp + static_cast<int64_t>(row) * p.dos[2] + col);
+        ov[i] = *reinterpret_cast<const u32x4*>(op + static_cast<int64_t>(row) * p.os[2] + col);
     }
-    rdot += __shfl_xor(rdot, 16, kWave);
-    rdot += __shfl_xor(rdot, 32, kWave);
-    if (g4 == 0 && row < g.lq) p.dr[h * p.rows_total + g.row_base + row] = rdot;
+    typedef typename BwdMfma<T>::v8 v8;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const v8 a = __builtin_bit_cast(v8, dv[i]), b = __builtin_bit_cast(v8, ov[i]);
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dot += to_f32(a[e]) * to_f32(b[e]);
+        if (8 * c >= dval) dot = 0.f;
+#pragma unroll
+        for (int o = CP / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, kWave);
+        const int row = row0 + RPI * i;
+        if (c == 0 && row < g.lq) p.dr[h * p.rows_total + g.row_base + row] = dot;
+    }
 }
-
 
 // dK / dV rows from the splits' fp32 partials, added in split order.  One item per
 // (K/V head, key row, 4 head-dim columns).
