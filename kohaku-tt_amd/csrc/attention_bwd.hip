@@ -475,10 +475,12 @@ __global__ __launch_bounds__(BWD_THREADS) void attn_bwd_rowdot(const BwdParams p
     constexpr int NI = 16 / RPI;     // instructions for the wavefront's 16 rows
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    // Heads fastest: workgroups that run together read the same query rows of every head
+    // (one contiguous span per token in packed [T, H, D] layouts).
     const int nqb = (p.seq_q + QW - 1) / QW;
-    const int qb = blockIdx.x % nqb;
-    const int bh = blockIdx.x / nqb;
-    const int seq = bh / p.hq, h = bh - seq * p.hq;
+    const int h = blockIdx.x % p.hq;
+    const int sq = blockIdx.x / p.hq;
+    const int seq = sq / nqb, qb = sq - seq * nqb;
     const Geo g = geo_of(p, seq);
     if (qb * QW >= g.lq) return;
     const T* dp = static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
