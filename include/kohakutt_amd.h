@@ -166,8 +166,9 @@ int kmi_attn_fwd_noalloc(const kmi_attn_args* args, void* stream);
  * stride[1] the head and stride[2] the token stride, lse [Hq, Tq]); head-dim stride 1;
  * q, k, v, out, grad_out 16-byte aligned with strides multiples of 8.  Masks take the
  * forward's modes and strides and get no gradient.  Workspace:
- * kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row dot products; with GQA or split
- * query / key ranges also fp32 dK / dV and dQ partials, added in a fixed order).
+ * kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row dot products; when the query
+ * rows of a key tile or the key tiles of a query block are split over workgroups, also
+ * fp32 dK / dV and dQ partials, added in a fixed order).
  * Does the work of the reference's flash backward behind tt_sdpa_overrideable_backward's stats
  * route (aten_attention.cpp:716-812; bridge in device_attention.cpp:1208-1281;
  * docs/reference/kernels/flash.md:151-206) and its packed backward behind
