@@ -364,6 +364,9 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
             load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, dval, dor);
             load_stats(h2, r2);
         }
+        // Unmasked items whose 32 rows see all of this wavefront's 16 keys (uniform): no
+        // per-element causal or key-tail test.
+        const bool full = MK == MK_NONE && kw0 + 15 < g.lk && (!p.causal || kw0 + 15 <= r0 + g.coff);
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
             // S^T and dP^T of this wavefront's 16 keys x rows rb 16 .. + 15: lane (g4, l16)
@@ -387,20 +390,29 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
             const bool raw = raws[rl] != 0;
             typedef T t4 __attribute__((ext_vector_type(4)));
             t4 pv, sv;
+            // Rows past the end carry lse2 = +inf: their P is exactly 0.
+            if (full) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int key = kw0 + 4 * g4 + j;
-                bool keep = key < g.lk && (!p.causal || key <= row + g.coff);
-                float add = 0.f;
-                if constexpr (MK != MK_NONE) {
-                    const float ml = (keep && row < g.lq) ? mask_at<MK>(p, g, h, row, key) : 0.f;
-                    keep = keep && (raw || ml > kMaskedLogit);
-                    add = raw ? 0.f : ml * kLog2e;
+                for (int j = 0; j < 4; ++j) {
+                    const float e = __builtin_amdgcn_exp2f(st[j] * p.c2 - l2);
+                    pv[j] = from_f32<T>(e);
+                    sv[j] = from_f32<T>(e * (dpt[j] - dr));
                 }
-                // Rows past the end carry lse2 = +inf: their P is exactly 0.
-                const float e = keep ? __builtin_amdgcn_exp2f(st[j] * p.c2 + add - l2) : 0.f;
-                pv[j] = from_f32<T>(e);
-                sv[j] = from_f32<T>(e * (dpt[j] - dr));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int key = kw0 + 4 * g4 + j;
+                    bool keep = key < g.lk && (!p.causal || key <= row + g.coff);
+                    float add = 0.f;
+                    if constexpr (MK != MK_NONE) {
+                        const float ml = (keep && row < g.lq) ? mask_at<MK>(p, g, h, row, key) : 0.f;
+                        keep = keep && (raw || ml > kMaskedLogit);
+                        add = raw ? 0.f : ml * kLog2e;
+                    }
+                    const float e = keep ? __builtin_amdgcn_exp2f(st[j] * p.c2 + add - l2) : 0.f;
+                    pv[j] = from_f32<T>(e);
+                    sv[j] = from_f32<T>(e * (dpt[j] - dr));
+                }
             }
             // Row rl, keys 4 g4 .. + 3: one 8-byte store each.
             *reinterpret_cast<t4*>(ptw + rl * PP + 4 * g4) = pv;
@@ -657,18 +669,29 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdParams& p, const int bid) {
             const int key = k0 + kb * 16 + l16;
             typedef T t4 __attribute__((ext_vector_type(4)));
             t4 dsv;
+            // Unmasked key blocks that all of this wavefront's 16 rows see (uniform): no
+            // per-element causal or key-tail test.
+            const int kb0 = k0 + kb * 16;
+            if (MK == MK_NONE && kb0 + 15 < g.lk && (!p.causal || kb0 + 15 <= rw0 + g.coff)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int row = rw0 + 4 * g4 + j;
-                bool keep = key < g.lk && (!p.causal || key <= row + g.coff);
-                float add = 0.f;
-                if constexpr (MK != MK_NONE) {
-                    const float ml = (keep && row < g.lq) ? mask_at<MK>(p, g, h, row, key) : 0.f;
-                    keep = keep && (raw[j] || ml > kMaskedLogit);
-                    add = raw[j] ? 0.f : ml * kLog2e;
+                for (int j = 0; j < 4; ++j) {
+                    const float e = __builtin_amdgcn_exp2f(sv[j] * p.c2 - l2[j]);
+                    dsv[j] = from_f32<T>(e * (dpv[j] - drv[j]));
                 }
-                const float e = keep ? __builtin_amdgcn_exp2f(sv[j] * p.c2 + add - l2[j]) : 0.f;
-                dsv[j] = from_f32<T>(e * (dpv[j] - drv[j]));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int row = rw0 + 4 * g4 + j;
+                    bool keep = key < g.lk && (!p.causal || key <= row + g.coff);
+                    float add = 0.f;
+                    if constexpr (MK != MK_NONE) {
+                        const float ml = (keep && row < g.lq) ? mask_at<MK>(p, g, h, row, key) : 0.f;
+                        keep = keep && (raw[j] || ml > kMaskedLogit);
+                        add = raw[j] ? 0.f : ml * kLog2e;
+                    }
+                    const float e = keep ? __builtin_amdgcn_exp2f(sv[j] * p.c2 + add - l2[j]) : 0.f;
+                    dsv[j] = from_f32<T>(e * (dpv[j] - drv[j]));
+                }
             }
             // Key kb 16 + l16, rows 4 g4 .. + 3: one 8-byte store.
             *reinterpret_cast<t4*>(dsw + (kb * 16 + l16) * PP + 4 * g4) = dsv;
