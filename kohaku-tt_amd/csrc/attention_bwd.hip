@@ -312,10 +312,21 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
     const int rfirst = p.causal ? max(0, kt0 - g.coff) / BT : 0;
     const int nblk = (kt0 < g.lk && g.lq > rfirst * BT) ? (g.lq + BT - 1) / BT - rfirst : 0;
     const int items = nblk * p.group;
-    auto item_at = [&](int it, int& h, int& r0) {
-        const int gi = it / nblk;
+    // Item it = gi nblk + bi is query head kvh G + gi, rows (rfirst + bi) 32 ..; the walk
+    // it, it + splits, ... steps (gi, bi) by (splits / nblk, splits % nblk) with one carry
+    // (no division per item).
+    const int sp_g = nblk > 0 ? p.splits / nblk : 0, sp_b = p.splits - sp_g * nblk;
+    auto step = [&](int& gi, int& bi) {
+        gi += sp_g;
+        bi += sp_b;
+        if (bi >= nblk) {
+            bi -= nblk;
+            ++gi;
+        }
+    };
+    auto item_at = [&](int gi, int bi, int& h, int& r0) {
         h = kvh * p.group + gi;
-        r0 = (rfirst + (it - gi * nblk)) * BT;
+        r0 = (rfirst + bi) * BT;
     };
     auto q_of = [&](int h) {
         return static_cast<const T*>(p.q) + g.qb + h * p.qs[1] + static_cast<int64_t>(g.q0) * p.qs[2];
@@ -334,16 +345,18 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
             dr_n = p.dr[h * p.rows_total + g.row_base + ic];
         }
     };
+    int gi = nblk > 0 ? split / nblk : 0, bi = split - gi * nblk;
     if (split < items) {
         int h, r0;
-        item_at(split, h, r0);
+        item_at(gi, bi, h, r0);
         load_regs<T, DP>(q_of(h), p.qs[2], r0, g.lq, p.d, qr);
         load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, dval, dor);
         load_stats(h, r0);
     }
     for (int it = split; it < items; it += p.splits) {
         int h, r0;
-        item_at(it, h, r0);
+        item_at(gi, bi, h, r0);
+        step(gi, bi);  // (gi, bi) is now the next item's
         __syncthreads();  // the previous item's LDS reads are done
         store_regs<T, DP>(qr, qs);
         store_regs<T, DP>(dor, dos);
@@ -359,7 +372,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
         __syncthreads();
         if (it + p.splits < items) {  // the next item's loads overlap this item's products
             int h2, r2;
-            item_at(it + p.splits, h2, r2);
+            item_at(gi, bi, h2, r2);
             load_regs<T, DP>(q_of(h2), p.qs[2], r2, g.lq, p.d, qr);
             load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, dval, dor);
             load_stats(h2, r2);
