@@ -335,12 +335,13 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
         return static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
     };
     TileRegs<DP> qr, dor;
-    // Row statistics of an item's rows (threads < BT hold one row each), loaded with its
-    // Q and dO a whole item ahead.
+    // Row statistics of an item's rows, loaded with its Q and dO a whole item ahead by
+    // wavefront 0 (a uniform branch), lane l holding row l % BT (both halves the same).
+    const int srow = lane & (BT - 1);
     float lv_n = 0.f, dr_n = 0.f;
     auto load_stats = [&](int h, int r0) {
-        if (threadIdx.x < BT) {
-            const int ic = min(r0 + static_cast<int>(threadIdx.x), g.lq - 1);
+        if (wave == 0) {
+            const int ic = min(r0 + srow, g.lq - 1);
             lv_n = p.lse[g.lb + h * p.ls[1] + static_cast<int64_t>(g.q0 + ic) * p.ls[2]];
             dr_n = p.dr[h * p.rows_total + g.row_base + ic];
         }
@@ -360,14 +361,14 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
         __syncthreads();  // the previous item's LDS reads are done
         store_regs<T, DP>(qr, qs);
         store_regs<T, DP>(dor, dos);
-        if (threadIdx.x < BT) {
-            const bool ok = r0 + static_cast<int>(threadIdx.x) < g.lq;
+        if (wave == 0) {  // lanes l and l + 32 write the same values
+            const bool ok = r0 + srow < g.lq;
             float l2;
             bool raw;
             row_stats(lv_n, ok, l2, raw);
-            lse2[threadIdx.x] = l2;
-            raws[threadIdx.x] = raw ? 1 : 0;
-            drs[threadIdx.x] = ok ? dr_n : 0.f;
+            lse2[srow] = l2;
+            raws[srow] = raw ? 1 : 0;
+            drs[srow] = ok ? dr_n : 0.f;
         }
         __syncthreads();
         if (it + p.splits < items) {  // the next item's loads overlap this item's products
