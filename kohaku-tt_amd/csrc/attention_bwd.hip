@@ -38,7 +38,7 @@ namespace kmi {
 namespace {
 
 constexpr int BT = 32;          // keys per K/V tile and rows per query block
-constexpr int PP = 24;          // pitch of a wavefront's [32][16] P / dS tiles (elements)
+constexpr int PP = 20;          // pitch of a wavefront's [32][16] P / dS tiles (elements; 16, 24, 28, 40, 48 measured slower)
 constexpr int BWD_THREADS = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 // A forward lse below this carries the -5e5 offset of a row with no kept key.
