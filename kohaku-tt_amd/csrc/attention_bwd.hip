@@ -207,7 +207,7 @@ __device__ __forceinline__ void row_stats(float lse_nat, bool valid, float& lse2
 
 // Staging of rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) in two steps:
 // loads into registers (16-byte chunks, zeros past the last row and the head dim), issued
-// a tile ahead, and their LDS stores, row-major at pitch DP + 8.
+// a tile ahead, and their LDS stores, row-major at pitch DP + 16 (8 or 24 measured slower).
 template <int DP>
 struct TileRegs {
     static constexpr int NV = BT * DP / 8;  // 16-byte chunks of a tile
@@ -236,7 +236,7 @@ __device__ __forceinline__ void store_regs(const TileRegs<DP>& t, T* dst) {
         const int c = threadIdx.x + BWD_THREADS * j;
         if (c >= TileRegs<DP>::NV) break;
         const int r = c % BT, ch = c / BT;
-        *reinterpret_cast<u32x4*>(dst + r * (DP + 8) + 8 * ch) = t.v[j];
+        *reinterpret_cast<u32x4*>(dst + r * (DP + 16) + 8 * ch) = t.v[j];
     }
 }
 
@@ -265,7 +265,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
     // v / dO / out width: a separate value dim only in the DV instances (one width keeps
     // the equal-dim kernels' registers).
     const int dval = DV ? p.dval : p.d;
-    constexpr int RP = DP + 8;
+    constexpr int RP = DP + 16;
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T qs[BT * RP];
     __shared__ __align__(16) T dos[BT * RP];
@@ -597,7 +597,7 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdParams& p, const int bid) {
     // v / dO / out width: a separate value dim only in the DV instances (one width keeps
     // the equal-dim kernels' registers).
     const int dval = DV ? p.dval : p.d;
-    constexpr int RP = DP + 8;
+    constexpr int RP = DP + 16;
     constexpr int DC = DP / 32, DB = DP / 16;
     __shared__ __align__(16) T ks[BT * RP];
     __shared__ __align__(16) T vs[BT * RP];
