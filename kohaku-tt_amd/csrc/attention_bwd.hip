@@ -864,14 +864,16 @@ int64_t keys_total_of(const kmi_attn_bwd_args* a) { return a->cu_seqlens_q ? a->
 // Split rules.  dK / dV and dQ workgroups run interleaved in one launch, so each kind
 // needs enough work per workgroup to amortise its set-up and few enough splits to keep
 // the fp32 partials small, rather than a grid that fills the chip alone.  A dK / dV
-// workgroup takes at most kBwdItemsPerWg (query head, 32-row block) items when splitting
-// allows it, a dQ workgroup at most kBwdTilesPerWg 32-key tiles; below
-// kBwdMinWgs workgroups of a kind, splits go down to kBwdMinItems items (or tiles) each.
-// Measured on C1 / C4 varlen (us, split target of the former per-kind rule): 108 / 254 at
-// 512 workgroups, 95 / 255 at 768, 96 / 255 at 1024, 102 / 214 at 1536, 107 / 216 at
-// 2048, 111 / 229 at 3072; C1 is best at 12-16 dK / dV splits with 2-3 dQ key splits, C4
-// at 2 dK / dV splits (64 items per workgroup unsplit) and none for dQ.
-constexpr int64_t kBwdItemsPerWg = 32;
+// workgroup takes at most kBwdItemsPerWg64 (query head, 32-row block) items up to head
+// dim 64 and kBwdItemsPerWg128 at 128 (in proportion fewer past it) when splitting allows
+// it, a dQ workgroup at most kBwdTilesPerWg 32-key tiles; below kBwdMinWgs workgroups of a
+// kind, splits go down to kBwdMinItems items (or tiles) each.  Measured on C1 / C4 varlen
+// (us): items per workgroup 20 / 24 / 32 / 40 / 48 at every head dim gave 101 / 96 / 92 /
+// 88 / 95 on C1 (19 / 19 / 14 / 12 / 10 splits) and 225 / 180 / 205 / 204 / 204 on C4 (4 /
+// 3 / 2 / 2 / 2 splits); 43 scaled by 64 / head dim gave 90.3 (11 splits) / 179.0 (3).
+// dQ tiles per workgroup 16 / 24 / 32 / 48: C1 94 / 93 / 91 / 92, C4 249 / 248 / 205 / 205.
+constexpr int64_t kBwdItemsPerWg64 = 40;
+constexpr int64_t kBwdItemsPerWg128 = 22;
 constexpr int64_t kBwdTilesPerWg = 32;
 constexpr int64_t kBwdMinWgs = 512;
 constexpr int64_t kBwdMinItems = 8;
@@ -890,7 +892,9 @@ int64_t bwd_split_count(int64_t units, int64_t work, int64_t per_wg, int64_t cap
 int bwd_splits(const kmi_attn_bwd_args* a) {
     const int64_t wgs = a->batch * a->heads_kv * ceil_div(a->seq_k, KW);
     const int64_t items = (a->heads_q / a->heads_kv) * ceil_div(a->seq_q, BT);
-    return static_cast<int>(bwd_split_count(wgs, items, kBwdItemsPerWg, kBwdMaxSplits));
+    const int64_t dp = padded_head_dim(std::max(a->head_dim, bwd_value_dim(a)));
+    const int64_t per_wg = dp <= 64 ? kBwdItemsPerWg64 : ceil_div(kBwdItemsPerWg128 * 128, dp);
+    return static_cast<int>(bwd_split_count(wgs, items, per_wg, kBwdMaxSplits));
 }
 
 // KMI_BWD_KSPLIT=n (read once; tuning): pins the dQ key splits.

@@ -158,11 +158,17 @@ def test_backward_rejects_malformed_calls_before_launch():
     # below the eight a split needs, so dK / dV are written directly (no partials).
     assert n.value == 4 * 8 * 4
     # Longer rows split: 2048 query rows give 7 x 64 items per key tile of C1's GQA,
-    # fourteen splits of 32 each (fp32 dK and dV partials per K/V head and split), and
+    # twelve splits of at most 40 (fp32 dK and dV partials per K/V head and split), and
     # 64 key tiles per dQ workgroup two key splits (fp32 dQ partials per head and split).
     a.heads_q, a.heads_kv, a.seq_q, a.seq_k = 14, 2, 2048, 2048
     assert capi.lib().kmi_attn_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == capi.KMI_OK
-    assert n.value == (14 * 2048 + 2 * (2 * 14 * 2048 * 64) + 14 * 2 * 2048 * 64) * 4
+    assert n.value == (14 * 2048 + 2 * (2 * 12 * 2048 * 64) + 14 * 2 * 2048 * 64) * 4
+    # Head dim 128: at most 22 items a workgroup: 64 items, three splits,
+    # with 8 x 8 x 16 key-tile workgroups (no fill splits) and no dQ key splits.
+    a.batch, a.heads_q, a.heads_kv, a.seq_q, a.seq_k, a.head_dim = 8, 16, 8, 1024, 1024, 128
+    assert capi.lib().kmi_attn_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == capi.KMI_OK
+    assert n.value == (16 * 8 * 1024 + 2 * (8 * 3 * 8 * 1024 * 128)) * 4
+    a.batch, a.head_dim = 1, 64
     a.heads_q, a.heads_kv, a.seq_q, a.seq_k = 4, 2, 8, 8
     assert capi.lib().kmi_attn_bwd(ctypes.byref(a), None, 0, None) == capi.KMI_EWORKSPACE
 
