@@ -802,8 +802,8 @@ __device__ __forceinline__ void dq_sum_item(const BwdParams& p, const int64_t it
     for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(acc[e]);
 }
 
-// Both sums in one launch (after dK / dV: neither reads the other's output): blocks
-// [0, dq_blocks) take dQ items (attn_bwd_dq's key-split partials), the rest dK / dV items.
+// Both sums in one launch (after the gradient launch; neither reads the other's output): blocks
+// [0, dq_blocks) take dQ items (the key-split dQ partials), the rest dK / dV items.
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void attn_bwd_sums(const BwdParams p, const int64_t dq_blocks) {
     const int64_t b = blockIdx.x;
