@@ -98,6 +98,28 @@ __device__ __forceinline__ void unpack(const u32x4& raw, float* out) {
     }
 }
 
+// Sum over a wavefront's 64 lanes without LDS round trips: a butterfly within each row of
+// 16 lanes through DPP (xor 1 and xor 2 by quad permutes, then the half-row and row
+// mirrors), the four row sums read from lanes 0, 16, 32, 48 and added in that order; every
+// lane gets the result.  (The lane-shuffle butterfly takes six dependent LDS-crossbar
+// round trips.)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f32<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_f32<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    const int iv = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 // LayerNorm statistics of a set of values: count, mean and centred sum of squares.  A
 // wavefront forms them exactly over its values (a sum for the mean, then the centred
 // squares, both plain cross-lane sums); sets held by different wavefronts merge by Chan,
@@ -650,9 +672,9 @@ __global__ __launch_bounds__(kNormBwdWaves * kWave) void norm_bwd_rows(const T* 
                 if constexpr (HB) ab[i][j] += gv[j];
             }
         }
-        sgx = wave_sum(sgx);
+        sgx = wave_sum_dpp(sgx);
         const float b = sgx * inv_w;
-        const float a = LAYER ? wave_sum(sg) * inv_w : 0.f;
+        const float a = LAYER ? wave_sum_dpp(sg) * inv_w : 0.f;
         T* dr = dx + row * width;
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
