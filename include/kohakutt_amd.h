@@ -164,7 +164,8 @@ int kmi_attn_fwd_noalloc(const kmi_attn_args* args, void* stream);
  * stored.  GQA: dk / dv of a K/V head sum its query heads.  Layouts as kmi_attn_fwd's
  * (dense: element strides of the batch, head and sequence dims; varlen: [T, H, D] with
  * stride[1] the head and stride[2] the token stride, lse [Hq, Tq]); head-dim stride 1;
- * q, k, v, out, grad_out 16-byte aligned with strides multiples of 8.  Masks take the
+ * q, k, v, out, grad_out 16-byte aligned with strides multiples of 8 (row strides below
+ * 2^25 elements).  Masks take the
  * forward's modes and strides and get no gradient.  Workspace:
  * kmi_attn_bwd_workspace_bytes, 16-byte aligned (fp32 row dot products; when the query
  * rows of a key tile or the key tiles of a query block are split over workgroups, also

@@ -206,8 +206,13 @@ __device__ __forceinline__ void row_stats(float lse_nat, bool valid, float& lse2
 }
 
 // Staging of rows [r0, r0 + 32) of a [S, D] operand (row stride rs elements) in two steps:
-// loads into registers (16-byte chunks, zeros past the last row and the head dim), issued
-// a tile ahead, and their LDS stores, row-major at pitch DP + 16 (8 or 24 measured slower).
+// loads into registers (16-byte chunks), issued a tile ahead, and their LDS stores,
+// row-major at pitch DP + 16 (8 or 24 measured slower).  The loads go through a buffer
+// resource over the tile's rows, built in scalar registers per tile, at byte offsets each
+// thread fixes once per call (TileOffs): a tile costs no per-lane address arithmetic.
+// Chunks past the head dim carry an offset past every range and rows past the last one
+// lie past the range's end, so both read zeros (overlapping rows, a stride below the head
+// dim, read their real, finite data there, which gets zero weight).
 template <int DP>
 struct TileRegs {
     static constexpr int NV = BT * DP / 8;  // 16-byte chunks of a tile
@@ -215,18 +220,33 @@ struct TileRegs {
     u32x4 v[PER];
 };
 
+template <int DP>
+struct TileOffs {
+    uint32_t o[TileRegs<DP>::PER];
+};
+
+constexpr uint32_t kNoChunk = 0x80000000u;  // past every tile's range (the host keeps ranges below 2^31 bytes)
+
 template <typename T, int DP>
-__device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int nrows, int d, TileRegs<DP>& t) {
+__device__ __forceinline__ TileOffs<DP> tile_offs(int64_t rs, int d) {
+    TileOffs<DP> t;
 #pragma unroll
     for (int j = 0; j < TileRegs<DP>::PER; ++j) {
         const int c = threadIdx.x + BWD_THREADS * j;
         const int r = c % BT, ch = c / BT;
-        const bool ok = c < TileRegs<DP>::NV && r0 + r < nrows && 8 * ch < d;
-        const int row = min(r0 + r, nrows - 1);  // in range; dropped below when past the end
-        const int col = min(8 * ch, d - 8);
-        const u32x4 val = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(row) * rs + col);
-        t.v[j] = ok ? val : u32x4{0u, 0u, 0u, 0u};
+        t.o[j] = (c < TileRegs<DP>::NV && 8 * ch < d) ? static_cast<uint32_t>(r * rs * sizeof(T)) + 16u * ch : kNoChunk;
     }
+    return t;
+}
+
+template <typename T, int DP>
+__device__ __forceinline__ void load_regs(const T* src, int64_t rs, int r0, int nrows, int d, const TileOffs<DP>& off,
+                                          TileRegs<DP>& t) {
+    const int n = min(BT, nrows - r0);
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(
+        src + r0 * rs, rows_extent(n, static_cast<uint32_t>(rs * sizeof(T)), static_cast<uint32_t>(d * sizeof(T))));
+#pragma unroll
+    for (int j = 0; j < TileRegs<DP>::PER; ++j) t.v[j] = buffer_load16(r, off.o[j]);
 }
 
 template <typename T, int DP>
@@ -335,6 +355,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
         return static_cast<const T*>(p.dout) + g.dob + h * p.dos[1] + static_cast<int64_t>(g.q0) * p.dos[2];
     };
     TileRegs<DP> qr, dor;
+    const TileOffs<DP> oq = tile_offs<T, DP>(p.qs[2], p.d), odo = tile_offs<T, DP>(p.dos[2], dval);
     // Row statistics of an item's rows, loaded with its Q and dO a whole item ahead by
     // wavefront 0 (a uniform branch), lane l holding row l % BT (both halves the same).
     const int srow = lane & (BT - 1);
@@ -350,8 +371,8 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
     if (split < items) {
         int h, r0;
         item_at(gi, bi, h, r0);
-        load_regs<T, DP>(q_of(h), p.qs[2], r0, g.lq, p.d, qr);
-        load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, dval, dor);
+        load_regs<T, DP>(q_of(h), p.qs[2], r0, g.lq, p.d, oq, qr);
+        load_regs<T, DP>(do_of(h), p.dos[2], r0, g.lq, dval, odo, dor);
         load_stats(h, r0);
     }
     for (int it = split; it < items; it += p.splits) {
@@ -374,8 +395,8 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdParams& p, const int bid)
         if (it + p.splits < items) {  // the next item's loads overlap this item's products
             int h2, r2;
             item_at(gi, bi, h2, r2);
-            load_regs<T, DP>(q_of(h2), p.qs[2], r2, g.lq, p.d, qr);
-            load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, dval, dor);
+            load_regs<T, DP>(q_of(h2), p.qs[2], r2, g.lq, p.d, oq, qr);
+            load_regs<T, DP>(do_of(h2), p.dos[2], r2, g.lq, dval, odo, dor);
             load_stats(h2, r2);
         }
         // Unmasked items whose 32 rows see all of this wavefront's 16 keys (uniform): no
@@ -652,10 +673,11 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdParams& p, const int bid) {
     const T* kbase = static_cast<const T*>(p.k) + g.kb + kvh * p.ks[1] + static_cast<int64_t>(g.k0) * p.ks[2];
     const T* vbase = static_cast<const T*>(p.v) + g.vb + kvh * p.vs[1] + static_cast<int64_t>(g.k0) * p.vs[2];
     TileRegs<DP> kr, vr;
+    const TileOffs<DP> okk = tile_offs<T, DP>(p.ks[2], p.d), ovv = tile_offs<T, DP>(p.vs[2], dval);
     const int kstep = p.ksplit * BT;
     if (ksp * BT < kend) {
-        load_regs<T, DP>(kbase, p.ks[2], ksp * BT, g.lk, p.d, kr);
-        load_regs<T, DP>(vbase, p.vs[2], ksp * BT, g.lk, dval, vr);
+        load_regs<T, DP>(kbase, p.ks[2], ksp * BT, g.lk, p.d, okk, kr);
+        load_regs<T, DP>(vbase, p.vs[2], ksp * BT, g.lk, dval, ovv, vr);
     }
     for (int k0 = ksp * BT; k0 < kend; k0 += kstep) {
         __syncthreads();
@@ -663,8 +685,8 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdParams& p, const int bid) {
         store_regs<T, DP>(vr, vs);
         __syncthreads();
         if (k0 + kstep < kend) {  // the next tile's loads overlap this tile's products
-            load_regs<T, DP>(kbase, p.ks[2], k0 + kstep, g.lk, p.d, kr);
-            load_regs<T, DP>(vbase, p.vs[2], k0 + kstep, g.lk, dval, vr);
+            load_regs<T, DP>(kbase, p.ks[2], k0 + kstep, g.lk, p.d, okk, kr);
+            load_regs<T, DP>(vbase, p.vs[2], k0 + kstep, g.lk, dval, ovv, vr);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -844,6 +866,9 @@ const char* check_bwd(const kmi_attn_bwd_args* a) {
     for (const int64_t* s : strides)
         for (int i = 0; i < 3; ++i)
             if (s[i] < 0 || s[i] % 8) return "q, k, v, out and grad_out strides must be non-negative multiples of 8";
+    // The staging loads address a 32-row tile with 32-bit byte offsets.
+    for (const int64_t* s : strides)
+        if (s[2] >= (int64_t{1} << 25)) return "q, k, v, out and grad_out row strides must be below 2^25 elements";
     const int64_t* ostrides[] = {a->dq_stride, a->dk_stride, a->dv_stride};
     for (const int64_t* s : ostrides)
         for (int i = 0; i < 3; ++i)
