@@ -171,6 +171,13 @@ def test_backward_rejects_malformed_calls_before_launch():
     a.batch, a.head_dim = 1, 64
     a.heads_q, a.heads_kv, a.seq_q, a.seq_k = 4, 2, 8, 8
     assert capi.lib().kmi_attn_bwd(ctypes.byref(a), None, 0, None) == capi.KMI_EWORKSPACE
+    # The staging loads address a 32-row tile with 32-bit byte offsets: row strides stop
+    # below 2^25 elements.
+    a.k_stride[2] = 1 << 25
+    assert capi.lib().kmi_attn_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == capi.KMI_EINVAL
+    assert "row strides must be below 2^25" in capi.lib().kmi_last_error().decode()
+    a.k_stride[2] = (1 << 25) - 8
+    assert capi.lib().kmi_attn_bwd_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == capi.KMI_OK
 
 
 def test_rms_norm_backward_rejects_malformed_calls_before_launch():
